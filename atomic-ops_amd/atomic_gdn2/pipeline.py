@@ -1,0 +1,131 @@
+"""The operator: ``make_blr_trainable(cfg, scale)(q, k, v, w, b, g, h0=None) -> (o, h_final)``.
+
+Drop-in for the reference's ``atomic_gdn2/pipeline.py:17-66``:
+
+* head-major ``(B,H,L,D)`` inputs of any float dtype, ``L % cfg.bt == 0`` (else ValueError);
+* ``o`` (B,H,L,D) and ``h_final`` (B,H,D,D) are float32 whatever the input dtype;
+* sequences longer than ``cfg.max_chunks_per_call`` chunks are split into segments with the
+  state carried through ``h0``/``h_final`` (pipeline.py:57-64);
+* each segment is one custom autograd node (the analogue of the reference's
+  ``jax.custom_vjp``): the forward runs the HIP forward (``gdn2_fwd``) and keeps its residual
+  buffer, the backward runs ``gdn2_bwd`` and returns gradients through ``_fin``
+  (pipeline.py:11-14): sanitized at 1e4 and cast back to each input's dtype.
+
+Every call goes to the HIP kernels in ``libgdn2_hip.so``; there is no other backend.  Tensors
+must live on a ROCm device.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from .precision import sanitize
+
+_FINAL_CLIP = 1e4
+
+
+def _fin(x, dt, cfg):
+    """pipeline.py:11-14: pass through if already in dtype and clipped at <= 1e4."""
+    if x.dtype == dt and cfg.clip <= _FINAL_CLIP:
+        return x
+    return sanitize(x, _FINAL_CLIP).to(dt)
+
+
+def _f32(t):
+    return t.to(torch.float32).contiguous()
+
+
+def _check_inputs(ts, names):
+    q = ts[0]
+    if q.dim() != 4:
+        raise ValueError(f"expected (B,H,L,D) inputs, got q.shape={tuple(q.shape)}")
+    for t, n in zip(ts, names):
+        if t.shape != q.shape:
+            raise ValueError(f"{n}.shape={tuple(t.shape)} differs from q.shape={tuple(q.shape)}")
+        if not t.is_floating_point():
+            raise TypeError(f"{n} must be a floating-point tensor")
+        if t.device != q.device:
+            raise ValueError(f"{n} is on {t.device}, q on {q.device}")
+
+
+def _check_device(q):
+    if q.device.type != "cuda":
+        raise RuntimeError("atomic_gdn2 runs on the HIP kernels only: move the inputs to a ROCm "
+                           f"device (got {q.device})")
+
+
+def make_blr_trainable(cfg, scale):
+    scale = float(scale)
+
+    class _Segment(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, q, k, v, w, b, g, h0):
+            dts = tuple(t.dtype for t in (q, k, v, w, b, g, h0))
+            xs = [_f32(t) for t in (q, k, v, w, b, g)]
+            h0c = _f32(h0)
+            B, H, L, D = xs[0].shape
+            desc = _lib.make_desc(cfg, B, H, L, D, scale)
+            dev = xs[0].device
+            need_res = any(ctx.needs_input_grad)
+            o = torch.empty((B, H, L, D), dtype=torch.float32, device=dev)
+            hf = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
+            L_ = _lib.lib()
+            with torch.cuda.device(dev):
+                _, tot = _lib.residual_layout(desc)      # validates the descriptor
+                res = torch.empty(tot, dtype=torch.uint8, device=dev) if need_res else None
+                wsb = L_.gdn2_fwd_workspace_bytes(ctypes.byref(desc), int(need_res))
+                ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+                _lib.check(L_.gdn2_fwd(ctypes.byref(desc), *map(_lib.ptr, xs), _lib.ptr(h0c),
+                                       _lib.ptr(o), _lib.ptr(hf), _lib.ptr(res), _lib.ptr(ws),
+                                       _lib.stream_handle(dev)), "gdn2_fwd")
+            if need_res:
+                ctx.save_for_backward(*xs, res)
+                ctx.desc = desc
+                ctx.dts = dts
+            return o, hf
+
+        @staticmethod
+        def backward(ctx, do, dhf):
+            *xs, res = ctx.saved_tensors
+            q = xs[0]
+            B, H, L, D = q.shape
+            dev = q.device
+            do = torch.zeros_like(q) if do is None else _f32(do)
+            dhf = q.new_zeros((B, H, D, D)) if dhf is None else _f32(dhf)
+            grads = [torch.empty_like(q) for _ in range(6)]
+            dh0 = q.new_empty((B, H, D, D))
+            L_ = _lib.lib()
+            with torch.cuda.device(dev):
+                ws = torch.empty(L_.gdn2_bwd_workspace_bytes(ctypes.byref(ctx.desc)), dtype=torch.uint8,
+                                 device=dev)
+                dq, dk, dv, dw, db, dg = grads
+                _lib.check(L_.gdn2_bwd(ctypes.byref(ctx.desc), *map(_lib.ptr, xs), _lib.ptr(res),
+                                       _lib.ptr(do), _lib.ptr(dhf), _lib.ptr(dq), _lib.ptr(dk),
+                                       _lib.ptr(dv), _lib.ptr(dw), _lib.ptr(db), _lib.ptr(dg),
+                                       _lib.ptr(dh0), _lib.ptr(ws), _lib.stream_handle(dev)), "gdn2_bwd")
+            outs = (dq, dk, dv, dw, db, dg, dh0)
+            return tuple(_fin(x, dt, cfg) for x, dt in zip(outs, ctx.dts))
+
+    def call(q, k, v, w, b, g, h0=None):
+        """q..g: (B,H,L,D), L % bt == 0. Returns (o (B,H,L,D) f32, h_final (B,H,D,D) f32)."""
+        _check_inputs((q, k, v, w, b, g), "qkvwbg")
+        bsz, H, L, D = q.shape
+        if L % cfg.bt:
+            raise ValueError(f"L={L} must be divisible by bt={cfg.bt}")
+        nc = L // cfg.bt
+        h = q.new_zeros((bsz, H, D, D), dtype=torch.float32) if h0 is None else h0
+        if h.shape != (bsz, H, D, D):
+            raise ValueError(f"h0.shape={tuple(h.shape)} must be {(bsz, H, D, D)}")
+        _check_device(q)
+        outs = []
+        for s in range(0, nc, cfg.max_chunks_per_call):
+            e = min(nc, s + cfg.max_chunks_per_call)
+            a, c = s * cfg.bt, e * cfg.bt
+            seg = (q, k, v, w, b, g) if (a == 0 and c == L) else tuple(t[:, :, a:c] for t in (q, k, v, w, b, g))
+            o_seg, h = _Segment.apply(*seg, h)
+            outs.append(o_seg)
+        return (outs[0] if len(outs) == 1 else torch.cat(outs, dim=2)), h
+
+    return call

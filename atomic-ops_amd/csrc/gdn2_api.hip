@@ -1,0 +1,339 @@
+// C ABI of the GDN-2 library: descriptor validation, residual / workspace layout, kernel
+// sequencing per segment, and optional per-kernel HIP-event timing.
+#include <string>
+#include <vector>
+
+#include "../../include/gdn2.h"
+#include "gdn2_kernels.hpp"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
+
+// Validation mirrors BLRConfig.__post_init__ (atomic_gdn2/config.py:62-75) plus this
+// build's supported geometry.
+int validate(const gdn2_desc* d) {
+  if (!d) return fail(GDN2_ERR_INVALID, "null descriptor");
+  if (d->B <= 0 || d->H <= 0 || d->L <= 0 || d->D <= 0) return fail(GDN2_ERR_INVALID, "non-positive shape");
+  if (d->bt <= 0 || d->L % d->bt) return fail(GDN2_ERR_INVALID, "L must be divisible by bt");
+  if (d->score_bs <= 0 || d->bs2 <= 0 || d->bt % d->score_bs || d->score_bs % d->bs2)
+    return fail(GDN2_ERR_INVALID, "need bt % score_bs == 0 and score_bs % bs2 == 0");
+  if (!pow2(d->mb) || d->bt % d->mb || !pow2(d->bt / d->mb))
+    return fail(GDN2_ERR_INVALID, "mb and bt/mb must be powers of two dividing bt");
+  if (!(d->wy_eps >= 0.0 && d->wy_eps < 1.0)) return fail(GDN2_ERR_INVALID, "wy_eps in [0,1)");
+  for (int m : {d->dot_mode, d->solve_dot_mode, d->b3_dot_mode})
+    if (m < GDN2_DOT_HIGHEST || m > GDN2_DOT_DEFAULT) return fail(GDN2_ERR_INVALID, "unknown dot mode");
+  if (d->diag != GDN2_DIAG_BTL && d->diag != GDN2_DIAG_LEAN) return fail(GDN2_ERR_INVALID, "unknown diag");
+  if (!(d->clip > 0.0)) return fail(GDN2_ERR_INVALID, "clip must be positive");
+  if (d->bt != gdn2::T) return fail(GDN2_ERR_UNSUPPORTED, "this build supports bt == 64 only");
+  if (d->D != 64 && d->D != 128) return fail(GDN2_ERR_UNSUPPORTED, "this build supports D in {64, 128}");
+  if (d->bs2 < 16) return fail(GDN2_ERR_UNSUPPORTED, "this build supports bs2 >= 16");
+  return GDN2_OK;
+}
+
+// Pieces of the two-level block-local rescaling (fwd/scores.py:42-75): for each row block
+// [q0, q0+bs2) of outer block p0: its diagonal block, the level-2 part [p0, q0) with anchor
+// q0 and the level-1 part [0, p0) with anchor p0, cut into squares of side min(bs2, 32).
+void make_pieces(int T, int sbs, int bs2, gdn2::PieceList* out) {
+  const int P = bs2 < 32 ? bs2 : 32;
+  int n = 0;
+  auto add = [&](int r, int c, int kind, int anchor, int s0, int s1) {
+    gdn2::Piece& p = out->p[n++];
+    p.row0 = (int8_t)r; p.col0 = (int8_t)c; p.P = (int8_t)P; p.kind = (int8_t)kind;
+    p.anchor = (int8_t)anchor; p.s0 = (int8_t)s0; p.s1 = (int8_t)s1; p.pad = 0;
+  };
+  for (int q0 = 0; q0 < T; q0 += bs2) {
+    const int q1 = q0 + bs2, p0 = (q0 / sbs) * sbs;
+    for (int r = q0; r < q1; r += P)
+      for (int c = q0; c <= r; c += P) add(r, c, 1, q0, q0, q1);
+    for (int c = p0; c < q0; c += P)
+      for (int r = q0; r < q1; r += P) add(r, c, 0, q0, 0, 0);
+    for (int c = 0; c < p0; c += P)
+      for (int r = q0; r < q1; r += P) add(r, c, 0, p0, 0, 0);
+  }
+  out->n = n;
+}
+
+gdn2::Cfg make_cfg(const gdn2_desc* d) {
+  gdn2::Cfg c{};
+  c.scale = (float)d->scale;
+  c.wy_eps = (float)d->wy_eps;
+  c.ome = (float)(1.0 - d->wy_eps);
+  c.clip = (float)d->clip;
+  c.diff_clip = (float)d->diff_clip;
+  c.diag = d->diag;
+  c.dot_mode = d->dot_mode;
+  c.solve_mode = d->solve_dot_mode;
+  c.b3_mode = d->b3_dot_mode;
+  c.mb = d->mb;
+  make_pieces(d->bt, d->score_bs, d->bs2, &c.pieces);
+  return c;
+}
+
+struct Dims {
+  size_t n_chunks, n_bh, nc, tD, tT, DD, D;
+};
+Dims dims(const gdn2_desc* d) {
+  Dims x;
+  x.nc = (size_t)(d->L / d->bt);
+  x.n_bh = (size_t)d->B * d->H;
+  x.n_chunks = x.n_bh * x.nc;
+  x.D = (size_t)d->D;
+  x.tD = (size_t)d->bt * d->D;
+  x.tT = (size_t)d->bt * d->bt;
+  x.DD = (size_t)d->D * d->D;
+  return x;
+}
+
+void residual_sizes(const gdn2_desc* d, size_t sz[GDN2_RES_COUNT]) {
+  const Dims x = dims(d);
+  sz[GDN2_RES_AQK] = x.n_chunks * x.tT * 4;
+  sz[GDN2_RES_A] = x.n_chunks * x.tT * 4;
+  sz[GDN2_RES_HPRE] = x.n_chunks * x.DD * 4;
+  sz[GDN2_RES_VNEW] = x.n_chunks * x.tD * 4;
+  sz[GDN2_RES_WP] = x.n_chunks * x.tD * 4;
+  sz[GDN2_RES_KG] = x.n_chunks * x.tD * 4;
+  sz[GDN2_RES_QG] = x.n_chunks * x.tD * 4;
+  sz[GDN2_RES_GL] = x.n_chunks * x.D * 4;
+}
+
+void residual_offsets(const gdn2_desc* d, size_t off[GDN2_RES_COUNT], size_t* total) {
+  size_t sz[GDN2_RES_COUNT];
+  residual_sizes(d, sz);
+  size_t o = 0;
+  for (int i = 0; i < GDN2_RES_COUNT; ++i) {
+    off[i] = o;
+    o = align_up(o + sz[i]);
+  }
+  *total = o;
+}
+
+// ---- profiling ------------------------------------------------------------------------
+struct ProfRec {
+  int kid;
+  hipEvent_t a, b;
+};
+struct Prof {
+  bool on = false;
+  int cap = 0;
+  std::vector<ProfRec> pool;
+  int used = 0;
+} g_prof;
+
+template <class F>
+hipError_t timed(int kid, hipStream_t s, F&& launch) {
+  ProfRec* rec = nullptr;
+  if (g_prof.on && g_prof.used < g_prof.cap) rec = &g_prof.pool[g_prof.used++];
+  if (rec) {
+    rec->kid = kid;
+    hipEventRecord(rec->a, s);
+  }
+  hipError_t e = launch();
+  if (rec) hipEventRecord(rec->b, s);
+  return e;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(GDN2_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+template <class T>
+T* at(void* base, size_t off) {
+  return reinterpret_cast<T*>(reinterpret_cast<char*>(base) + off);
+}
+
+}  // namespace
+
+extern "C" {
+
+int gdn2_abi_version(void) { return GDN2_ABI_VERSION; }
+
+const char* gdn2_last_error(void) { return g_err.c_str(); }
+
+int gdn2_residual_layout(const gdn2_desc* d, size_t offsets[GDN2_RES_COUNT], size_t* total_bytes) {
+  const int st = validate(d);
+  if (st) return st;
+  if (!offsets || !total_bytes) return fail(GDN2_ERR_INVALID, "null output pointer");
+  residual_offsets(d, offsets, total_bytes);
+  return GDN2_OK;
+}
+
+// forward workspace: [u] or, without a residual buffer, [u | aqk | wp | kg | qg | gl]
+size_t gdn2_fwd_workspace_bytes(const gdn2_desc* d, int with_residual) {
+  if (validate(d)) return 0;
+  const Dims x = dims(d);
+  size_t n = align_up(x.n_chunks * x.tD * 4);
+  if (!with_residual) {
+    n += align_up(x.n_chunks * x.tT * 4);
+    n += 3 * align_up(x.n_chunks * x.tD * 4);
+    n += align_up(x.n_chunks * x.D * 4);
+  }
+  return n;
+}
+
+// backward workspace: [dv_new | dh_next | dqg | dwp | dkg | dlast]
+size_t gdn2_bwd_workspace_bytes(const gdn2_desc* d) {
+  if (validate(d)) return 0;
+  const Dims x = dims(d);
+  return 4 * align_up(x.n_chunks * x.tD * 4) + align_up(x.n_chunks * x.DD * 4) +
+         align_up(x.n_chunks * x.D * 4);
+}
+
+int gdn2_fwd(const gdn2_desc* d, const float* q, const float* k, const float* v, const float* w,
+             const float* b, const float* g, const float* h0, float* o, float* h_final, void* residual,
+             void* workspace, void* stream) {
+  int st = validate(d);
+  if (st) return st;
+  if (!q || !k || !v || !w || !b || !g || !o || !h_final || !workspace)
+    return fail(GDN2_ERR_INVALID, "null tensor pointer");
+  const Dims x = dims(d);
+  const gdn2::Cfg cfg = make_cfg(d);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+
+  float *aqk, *A = nullptr, *hpre = nullptr, *vnew = nullptr, *wp, *kg, *qg, *gl;
+  float* u = at<float>(workspace, 0);
+  if (residual) {
+    size_t off[GDN2_RES_COUNT], tot;
+    residual_offsets(d, off, &tot);
+    aqk = at<float>(residual, off[GDN2_RES_AQK]);
+    A = at<float>(residual, off[GDN2_RES_A]);
+    hpre = at<float>(residual, off[GDN2_RES_HPRE]);
+    vnew = at<float>(residual, off[GDN2_RES_VNEW]);
+    wp = at<float>(residual, off[GDN2_RES_WP]);
+    kg = at<float>(residual, off[GDN2_RES_KG]);
+    qg = at<float>(residual, off[GDN2_RES_QG]);
+    gl = at<float>(residual, off[GDN2_RES_GL]);
+  } else {
+    size_t o2 = align_up(x.n_chunks * x.tD * 4);
+    aqk = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tT * 4);
+    wp = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
+    kg = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
+    qg = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
+    gl = at<float>(workspace, o2);
+  }
+
+  gdn2::WyFwdArgs wa{q, k, v, w, b, g, aqk, A, wp, u, kg, qg, gl, nullptr, (int)x.n_chunks, cfg};
+  hipError_t e = timed(0, s, [&] { return gdn2::launch_wy_fwd(d->D, wa, s); });
+  if (e != hipSuccess) return hip_fail(e, "wy_fwd launch");
+
+  gdn2::ScanFwdArgs sa{wp, u, kg, qg, gl, aqk, h0, o, h_final, hpre, vnew, (int)x.nc, (int)x.n_bh, cfg};
+  e = timed(1, s, [&] { return gdn2::launch_scan_fwd(d->D, sa, s); });
+  if (e != hipSuccess) return hip_fail(e, "scan_fwd launch");
+  return GDN2_OK;
+}
+
+int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v, const float* w,
+             const float* b, const float* g, const void* residual, const float* d_o, const float* d_hf,
+             float* dq, float* dk, float* dv, float* dw, float* db, float* dg, float* dh0, void* workspace,
+             void* stream) {
+  int st = validate(d);
+  if (st) return st;
+  if (!q || !k || !v || !w || !b || !g || !residual || !d_o || !d_hf || !dq || !dk || !dv || !dw || !db ||
+      !dg || !dh0 || !workspace)
+    return fail(GDN2_ERR_INVALID, "null tensor pointer");
+  const Dims x = dims(d);
+  const gdn2::Cfg cfg = make_cfg(d);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  size_t off[GDN2_RES_COUNT], tot;
+  residual_offsets(d, off, &tot);
+  void* res = const_cast<void*>(residual);
+  const float* aqk = at<float>(res, off[GDN2_RES_AQK]);
+  const float* A = at<float>(res, off[GDN2_RES_A]);
+  const float* hpre = at<float>(res, off[GDN2_RES_HPRE]);
+  const float* vnew = at<float>(res, off[GDN2_RES_VNEW]);
+  const float* wp = at<float>(res, off[GDN2_RES_WP]);
+  const float* kg = at<float>(res, off[GDN2_RES_KG]);
+  const float* qg = at<float>(res, off[GDN2_RES_QG]);
+  const float* gl = at<float>(res, off[GDN2_RES_GL]);
+
+  size_t o2 = 0;
+  float* dvn = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
+  float* dhn = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.DD * 4);
+  float* dqg = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
+  float* dwp = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
+  float* dkg = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
+  float* dlast = at<float>(workspace, o2);
+
+  gdn2::ScanBwdArgs sa{wp, kg, qg, gl, aqk, d_o, d_hf, dvn, dhn, dh0, (int)x.nc, (int)x.n_bh, cfg};
+  hipError_t e = timed(2, s, [&] { return gdn2::launch_scan_bwd(d->D, sa, s); });
+  if (e != hipSuccess) return hip_fail(e, "scan_bwd launch");
+
+  gdn2::BwdStateArgs ba{d_o, dvn, vnew, hpre, dhn, dqg, dwp, dkg, dlast, (int)x.n_chunks, cfg};
+  e = timed(3, s, [&] { return gdn2::launch_bwd_state(d->D, ba, s); });
+  if (e != hipSuccess) return hip_fail(e, "bwd_state launch");
+
+  gdn2::BwdWyArgs wa{q, k, v, w, b, g, A, aqk, d_o, vnew, dvn, dqg, dwp, dkg, dlast,
+                     dq, dk, dv, dw, db, dg, (int)x.n_chunks, cfg};
+  e = timed(4, s, [&] { return gdn2::launch_bwd_wy(d->D, wa, s); });
+  if (e != hipSuccess) return hip_fail(e, "bwd_wy launch");
+  return GDN2_OK;
+}
+
+int gdn2_wy_stage(const gdn2_desc* d, const float* q, const float* k, const float* v, const float* w,
+                  const float* b, const float* g, float* aqk, float* akk, float* A, float* wp, float* u,
+                  float* kg, float* qg, float* gl, void* stream) {
+  int st = validate(d);
+  if (st) return st;
+  if (!q || !k || !v || !w || !b || !g || !aqk || !wp || !u || !kg || !qg || !gl)
+    return fail(GDN2_ERR_INVALID, "null tensor pointer");
+  const Dims x = dims(d);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  gdn2::WyFwdArgs wa{q, k, v, w, b, g, aqk, A, wp, u, kg, qg, gl, akk, (int)x.n_chunks, make_cfg(d)};
+  hipError_t e = timed(0, s, [&] { return gdn2::launch_wy_fwd(d->D, wa, s); });
+  if (e != hipSuccess) return hip_fail(e, "wy_fwd launch");
+  return GDN2_OK;
+}
+
+int gdn2_debug_gemm(int mode, const float* A, const float* B, float* C, int M, int N, int K, void* stream) {
+  if (mode < 0 || mode > 2) return fail(GDN2_ERR_INVALID, "unknown dot mode");
+  if (M <= 0 || N <= 0 || K <= 0 || M > 64 || N > 64 || K > 128 || M % 16 || N % 16 || K % 16)
+    return fail(GDN2_ERR_INVALID, "gemm probe shape");
+  if (!A || !B || !C) return fail(GDN2_ERR_INVALID, "null tensor pointer");
+  hipError_t e = gdn2::launch_gemm_probe(mode, A, B, C, M, N, K, reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "gemm probe launch");
+  return GDN2_OK;
+}
+
+int gdn2_prof_begin(int max_launches) {
+  if (max_launches <= 0) return fail(GDN2_ERR_INVALID, "max_launches must be positive");
+  while ((int)g_prof.pool.size() < max_launches) {
+    ProfRec r{};
+    if (hipEventCreate(&r.a) != hipSuccess || hipEventCreate(&r.b) != hipSuccess)
+      return fail(GDN2_ERR_HIP, "hipEventCreate failed");
+    g_prof.pool.push_back(r);
+  }
+  g_prof.cap = max_launches;
+  g_prof.used = 0;
+  g_prof.on = true;
+  return GDN2_OK;
+}
+
+int gdn2_prof_end(double ms_sum[GDN2_NUM_KERNELS], int counts[GDN2_NUM_KERNELS]) {
+  for (int i = 0; i < GDN2_NUM_KERNELS; ++i) {
+    ms_sum[i] = 0.0;
+    counts[i] = 0;
+  }
+  g_prof.on = false;
+  for (int i = 0; i < g_prof.used; ++i) {
+    ProfRec& r = g_prof.pool[i];
+    if (hipEventSynchronize(r.b) != hipSuccess) return fail(GDN2_ERR_HIP, "hipEventSynchronize failed");
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess) return fail(GDN2_ERR_HIP, "hipEventElapsedTime failed");
+    ms_sum[r.kid] += ms;
+    counts[r.kid] += 1;
+  }
+  g_prof.used = 0;
+  return GDN2_OK;
+}
+
+}  // extern "C"

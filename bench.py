@@ -1,0 +1,174 @@
+"""Benchmark of the GDN-2 operator's gradient evaluation on one MI355X.
+
+Workload: (B,H,L,D) = (4,6,2048,128) fp32, chunk 64, wy_eps = 0,
+zero h0, synthetic seeded inputs (atomic_gdn2.synthetic); one step = forward + backward of
+sum(o^2) + sum(h_final^2) w.r.t. q, k, v, w, b, g, all dot modes 'highest' (fp32 MFMA).
+
+Prints ONE JSON line.  ``value`` is the canonical-FLOP throughput of the whole step in
+TFLOP/s (F_grad = B*H*L*(32*T*D + 18*D^2 + 4*T^2)); ``ms_per_step`` is the latency.
+``roofline`` describes the dominant kernel, timed live with HIP events recorded on the launch
+stream by the library (gdn2_prof_begin / gdn2_prof_end).  ``cpu_baseline`` times the torch
+float32 CPU restatement of the reference algorithm (oracle/gdn2_oracle.py) on a bounded
+sample of the same workload on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path[:0] = [str(ROOT), str(ROOT / "atomic-ops_amd")]
+
+PEAK_FP32_MFMA = 157.3      # TFLOP/s, MI355X dense fp32 matrix
+PEAK_HBM = 8000.0           # GB/s
+B_, H_, L_, D_, T_ = 4, 6, 2048, 128, 64
+
+# Algorithmic FLOPs per (batch, head, token) of the work each kernel does, in the dense
+# convention of the canonical count (every T x T operand dense).  Their sum is the canonical
+# F_grad minus the W recompute (2*T*D) that this implementation keeps as a residual instead.
+def kernel_flops_per_token(T=T_, D=D_):
+    return {
+        "wy_fwd": 8 * T * D,                      # Aqk, Akk, Wp, U
+        "scan_fwd": 2 * T * D + 6 * D * D,        # Aqk v_new; Wp h, Qg h, Kg^T v_new
+        "scan_bwd": 2 * T * D + 6 * D * D,        # Aqk^T dO; Kg dh, Qg^T dO, Wp^T dv_new
+        "bwd_state": 6 * D * D,                   # dQg, dWp, dKg
+        "bwd_wy": 18 * T * D + 4 * T * T,         # dAqk, dA, dkb, dwv, B4; dA A^T, A^T tmp
+    }
+
+
+def canonical_flops(B, H, L, D, T=T_):
+    n = B * H * L
+    return n * (10 * T * D + 6 * D * D), n * (22 * T * D + 12 * D * D + 4 * T * T)
+
+
+def canonical_bytes(B, H, L, D):
+    N = B * H * L * D
+    S = B * H * D * D * 4
+    return 20 * N * 4 + 4 * S
+
+
+def cpu_baseline(threads: int):
+    """Oracle restatement in torch float32 on the host CPU: forward + autograd backward of the
+    same loss on a bounded sample (B=1, H=1, L=2048, D=128: 1/24 of the workload)."""
+    import torch
+    from oracle import gdn2_oracle as O
+    from atomic_gdn2.synthetic import make_inputs_np
+    torch.set_num_threads(threads)
+    arrs, scale = make_inputs_np(1, 1, 2048, 128, seed=0)
+    xs = [torch.from_numpy(a) for a in arrs]
+    cfg = O.OracleCfg(bt=64, score_bs=64, bs2=32, mb=8, wy_eps=0.0)
+    times = []
+    t_end = time.perf_counter() + 20.0
+    for i in range(5):
+        t0 = time.perf_counter()
+        O.grad_ref(*xs, scale, None, cfg)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() > t_end and i >= 1:
+            break
+    sec = sorted(times)[len(times) // 2]
+    f, b = canonical_flops(1, 1, 2048, 128)
+    return {"value": (f + b) / sec / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"B1 H1 L2048 D128 fp32 grad-eval (1/24 of the workload), median of {len(times)}: "
+                      f"{sec * 1e3:.1f} ms", "ms_per_sample": sec * 1e3,
+            "ms_scaled_to_workload": sec * 1e3 * 24}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: every (batch, head) sequence is independent, so a "
+              "multi-GPU run is B/H sharding with no communication (see DESIGN.md); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from atomic_gdn2 import make_cfg, make_blr_trainable, _lib
+    from atomic_gdn2.synthetic import make_inputs
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    (q, k, v, w, b, g), scale = make_inputs(B_, H_, L_, D_, seed=args.seed, device=dev)
+    xs = [t.requires_grad_(True) for t in (q, k, v, w, b, g)]
+    cfg = make_cfg(bt=64, bc=32, score_bs=64, bs2=32, mb=8, wy_eps=0.0, dot_mode="highest",
+                   solve_dot_mode="highest", b3_dot_mode="highest")
+    fn = make_blr_trainable(cfg, scale)
+
+    def step():
+        o, hf = fn(*xs)
+        loss = (o * o).sum() + (hf * hf).sum()
+        return torch.autograd.grad(loss, xs)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    _lib.prof_begin(args.steps * len(_lib.KERNEL_NAMES) + 16)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    prof = _lib.prof_end()
+    ms = dt * 1e3 / args.steps
+
+    # forward-only (no residuals) throughput on the same inputs
+    with torch.no_grad():
+        for _ in range(2):
+            fn(q.detach(), k.detach(), v.detach(), w.detach(), b.detach(), g.detach())
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(args.steps):
+            fn(q.detach(), k.detach(), v.detach(), w.detach(), b.detach(), g.detach())
+        torch.cuda.synchronize()
+        fwd_ms = (time.perf_counter() - t1) * 1e3 / args.steps
+
+    ff, fb = canonical_flops(B_, H_, L_, D_)
+    tflops = (ff + fb) / (ms * 1e-3) / 1e12
+    kf = kernel_flops_per_token()
+    ntok = B_ * H_ * L_
+    kern = {}
+    for name, (tot_ms, cnt) in prof.items():
+        if cnt:
+            avg = tot_ms / cnt
+            kern[name] = {"avg_ms": round(avg, 5), "launches": cnt,
+                          "tflops": round(kf[name] * ntok / (avg * 1e-3) / 1e12, 2)}
+    dom = max(kern, key=lambda n: kern[n]["avg_ms"])
+    ach = kern[dom]["tflops"]
+    traffic = None
+    tf = ROOT / "profiles" / "traffic.json"
+    if tf.exists():
+        traffic = json.loads(tf.read_text()).get(dom)
+
+    out = {
+        "metric": "fwd+bwd ms, TFLOP/s and MFMA % at B4 H6 L2048 D128 fp32; fwd tokens/s",
+        "value": round(tflops, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "config": {"workload": "gdn2 grad-eval (fwd+bwd of sum(o^2)+sum(h_final^2)) B4 H6 L2048 D128 "
+                               "chunk64 wy_eps0 dot=highest", "B": B_, "H": H_, "L": L_, "D": D_, "bt": 64},
+        "fwd_ms": round(fwd_ms, 4), "fwd_tokens_per_s": round(B_ * L_ / (fwd_ms * 1e-3), 1),
+        "canonical_gflop": round((ff + fb) / 1e9, 3),
+        "canonical_gb_per_s": round(canonical_bytes(B_, H_, L_, D_) / (ms * 1e-3) / 1e9, 1),
+        "mfma_frac_of_fp32_peak_step": round(tflops / PEAK_FP32_MFMA, 4),
+        "kernels": kern,
+        "roofline": {"kernel": dom, "bound": "mfma", "achieved": ach, "peak": PEAK_FP32_MFMA,
+                     "unit": "TFLOP/s", "frac": round(ach / PEAK_FP32_MFMA, 4), "traffic": traffic},
+        "reference_tpu_v5e_ms": 2.888,
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(min(16, os.cpu_count() or 1))
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

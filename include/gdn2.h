@@ -1,0 +1,112 @@
+/*
+ * gdn2.h -- C ABI of the MI355X (gfx950) GDN-2 operator library `libgdn2_hip.so`.
+ *
+ * This is the drop-in boundary under the Python API `make_blr_trainable(cfg, scale)`.
+ * Plain pointers and sizes only: every tensor argument is a device pointer to a contiguous
+ * float32 buffer, and `stream` is a `hipStream_t` (NULL = the default stream).  Kernels are
+ * enqueued on `stream`; no call synchronises the device, allocates memory or keeps a
+ * pointer after it returns (except the profiling calls, see below).  Every entry point
+ * returns a gdn2_status; on failure gdn2_last_error() describes the problem.
+ *
+ * Layouts (head-major, as in the reference; a chunk is `bt` consecutive tokens):
+ *   q, k, v, w, b, g, o, dq .. dg   (B, H, L, D)      == (B, H, nc, bt, D), nc = L / bt
+ *   h0, h_final, dh_final, dh0      (B, H, D, D)      rows = key channel, cols = value channel
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   gdn2_fwd  : the custom_vjp forward of one segment, `_fwd` + `core_fwd`
+ *               (atomic_gdn2/pipeline.py:20-36), i.e. build_scores (fwd/scores.py:90-100),
+ *               wy_solve_leafbatched (fwd/solve.py:51-59) and recompute_and_scan_slim
+ *               (fwd/cd_slim.py:34-51).
+ *   gdn2_bwd  : the custom_vjp backward of one segment, `core_bwd` (pipeline.py:38-47),
+ *               i.e. backward_mega (bwd/mega.py:61-79) before `_fin`.
+ *   gdn2_wy_stage : the chunk-parallel stages alone (scores, WY inverse, W/U recompute),
+ *               for stage-level checks (fwd/scores.py:90, fwd/solve.py:51, cd_slim.py:17-21).
+ */
+#ifndef GDN2_H_
+#define GDN2_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GDN2_ABI_VERSION 1
+
+/* Matmul precision modes (atomic_gdn2/precision.py:27-31; config.py:51-53). */
+enum { GDN2_DOT_HIGHEST = 0, GDN2_DOT_BF16X3 = 1, GDN2_DOT_DEFAULT = 2 };
+/* Diagonal-block treatment of the scores (config.py:46). */
+enum { GDN2_DIAG_BTL = 0, GDN2_DIAG_LEAN = 1 };
+/* Status codes. */
+enum { GDN2_OK = 0, GDN2_ERR_INVALID = 1, GDN2_ERR_UNSUPPORTED = 2, GDN2_ERR_HIP = 3 };
+
+/* One segment call.  Field meaning follows BLRConfig (atomic_gdn2/config.py:38-60).
+ * Supported by this build: bt == 64, D in {64, 128}, L % bt == 0, bs2 in {16, 32, 64},
+ * bs2 | score_bs | bt, mb a power of two dividing bt. */
+typedef struct gdn2_desc {
+  int32_t B, H, L, D;
+  int32_t bt, score_bs, bs2, mb;
+  int32_t diag, dot_mode, solve_dot_mode, b3_dot_mode;
+  double scale, wy_eps, clip, diff_clip;
+} gdn2_desc;
+
+/* Residual buffer written by gdn2_fwd and read by gdn2_bwd: sub-buffers at the offsets
+ * reported by gdn2_residual_layout (bytes, 256-aligned).  Shapes (float32):
+ *   AQK, A  (B,H,nc,bt,bt)   gated q.k scores and the WY inverse      (pipeline.py:25)
+ *   HPRE    (B,H,nc,D,D)     state entering each chunk                (cd_slim.py:22)
+ *   VNEW    (B,H,nc,bt,D)    v_new of each chunk                      (cd_slim.py:23)
+ *   WP, KG, QG (B,H,nc,bt,D) W = A(b k e^gc), gated k and q           (cd_slim.py:17-21)
+ *   GL      (B,H,nc,D)       gc of the chunk's last row               (cd_slim.py:19) */
+enum { GDN2_RES_AQK = 0, GDN2_RES_A, GDN2_RES_HPRE, GDN2_RES_VNEW, GDN2_RES_WP, GDN2_RES_KG,
+       GDN2_RES_QG, GDN2_RES_GL, GDN2_RES_COUNT };
+
+int gdn2_abi_version(void);
+const char* gdn2_last_error(void);
+
+/* Validates `d` and reports the residual sub-buffer offsets and total size in bytes. */
+int gdn2_residual_layout(const gdn2_desc* d, size_t offsets[GDN2_RES_COUNT], size_t* total_bytes);
+/* Workspace sizes in bytes (0 on an invalid descriptor). */
+size_t gdn2_fwd_workspace_bytes(const gdn2_desc* d, int with_residual);
+size_t gdn2_bwd_workspace_bytes(const gdn2_desc* d);
+
+/* Forward of one segment.  h0 may be NULL (zero state).  residual may be NULL for a
+ * forward-only call (nothing is kept for a backward pass); otherwise it must hold
+ * gdn2_residual_layout() bytes.  workspace holds gdn2_fwd_workspace_bytes(d, residual!=NULL). */
+int gdn2_fwd(const gdn2_desc* d, const float* q, const float* k, const float* v, const float* w,
+             const float* b, const float* g, const float* h0, float* o, float* h_final,
+             void* residual, void* workspace, void* stream);
+
+/* Backward of one segment: cotangents d_o (B,H,L,D) and d_hf (B,H,D,D) -> the raw
+ * (sanitized at cfg.clip) gradients of q, k, v, w, b, g and h0, all float32. */
+int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v, const float* w,
+             const float* b, const float* g, const void* residual, const float* d_o,
+             const float* d_hf, float* dq, float* dk, float* dv, float* dw, float* db, float* dg,
+             float* dh0, void* workspace, void* stream);
+
+/* Chunk-parallel forward stages only.  Any output may be NULL except u (scratch for W/U),
+ * aqk, wp, kg, qg, gl.  akk is the masked, sanitized Akk before the (1 - wy_eps) factor;
+ * A is the sanitized inverse.  Shapes as in the residual layout. */
+int gdn2_wy_stage(const gdn2_desc* d, const float* q, const float* k, const float* v,
+                  const float* w, const float* b, const float* g, float* aqk, float* akk,
+                  float* A, float* wp, float* u, float* kg, float* qg, float* gl, void* stream);
+
+/* Diagnostics: C[M,N] = A[M,K] B[K,N] (row-major float32) through the kernels' MFMA tile
+ * routine in the given dot mode.  M, N <= 64, K <= 128, all multiples of 16. */
+int gdn2_debug_gemm(int mode, const float* A, const float* B, float* C, int M, int N, int K,
+                    void* stream);
+
+/* Per-kernel timing with HIP events recorded on the launch stream around every kernel.
+ * gdn2_prof_begin(n) starts recording for up to n launches (process-wide, not re-entrant);
+ * gdn2_prof_end synchronises on the recorded events and returns, per kernel id, the summed
+ * duration in milliseconds and the launch count, then stops recording.
+ * Kernel ids: 0 wy_fwd, 1 scan_fwd, 2 scan_bwd, 3 bwd_state, 4 bwd_wy. */
+#define GDN2_NUM_KERNELS 5
+int gdn2_prof_begin(int max_launches);
+int gdn2_prof_end(double ms_sum[GDN2_NUM_KERNELS], int counts[GDN2_NUM_KERNELS]);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN2_H_ */

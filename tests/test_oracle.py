@@ -1,0 +1,331 @@
+"""Pins for the CPU oracle (oracle/gdn2_oracle.py).  CPU only.
+
+Each oracle function is checked against something that does not share its formula:
+  * the reference's stored 80-digit Decimal known answers (D=4, L=256, 3 seeds, 2 objectives);
+  * the token-serial recurrence (chunked WY == serial, any blocking, eps, h0);
+  * brute-force O(T^2 D) scores; scipy's unit-lower triangular solve for the ladder inverse;
+  * finite differences of the token-serial recurrence for the autograd gradients;
+  * agreement of the analytic backward (kernel semantics, B1..B5) with autograd;
+  * B4's closed form (b4_exact_f64_np) against autograd of the two-level scores.
+Planted mistakes at the end show that each pin fails on a plausible slip.
+"""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import scipy.linalg
+import torch
+
+from oracle import gdn2_oracle as O
+
+torch.set_default_dtype(torch.float64)
+GOLD = Path(__file__).resolve().parent / "golden"
+
+
+def t64(x):
+    return torch.as_tensor(np.asarray(x, np.float64))
+
+
+def rand_inputs(B, H, L, D, seed, gscale=0.05, h0=False):
+    rng = np.random.default_rng(seed)
+    sh = (B, H, L, D)
+    q = rng.normal(size=sh) * 0.3
+    k = rng.normal(size=sh) * 0.3
+    v = rng.normal(size=sh)
+    w = rng.uniform(0.2, 1.0, size=sh)
+    b = rng.uniform(0.2, 1.0, size=sh)
+    g = -np.abs(rng.normal(size=sh)) * gscale
+    out = [t64(x) for x in (q, k, v, w, b, g)]
+    out.append(t64(rng.normal(size=(B, H, D, D)) * 0.1) if h0 else None)
+    return out
+
+
+def rel(a, b):
+    return float(torch.linalg.norm((a - b).reshape(-1)) / max(float(torch.linalg.norm(b.reshape(-1))), 1e-300))
+
+
+# ---------------------------------------------------------------- known answers
+KAT = json.loads((GOLD / "kat_d4.json").read_text())
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+@pytest.mark.parametrize("alg", ["serial", "chunked"])
+def test_decimal_known_answers(seed, alg):
+    d = np.load(GOLD / f"kat_d4_seed{seed}.npz", allow_pickle=False)
+    t = {k: t64(d[k]) for k in d.files}
+    cfg = O.OracleCfg(bt=64, score_bs=64, bs2=32, mb=8, wy_eps=0.0)
+    th = torch.zeros((), requires_grad=True)
+    v = t["v"] + th * t["direction"]
+    if alg == "serial":
+        o, hf = O.token_serial_ref(t["q"], t["k"], v, t["g"], t["b"], t["w"], 0.5, t["h0"])
+    else:
+        o, hf = O.forward_ref_blhd(t["q"], t["k"], v, t["w"], t["b"], t["g"], 0.5, t["h0"], cfg)
+    y = torch.cat([o.reshape(-1), hf.reshape(-1)])
+    objs = {"natural": 0.5 * (y * y).sum(), "cancellation_stress": (t["coeff"] * y).sum()}
+    for mode, f in objs.items():
+        (gr,) = torch.autograd.grad(f, th, retain_graph=True)
+        ref = KAT["cases"][f"{seed}/{mode}"]
+        val_ref, grad_ref = float(ref["value"]), float(ref["gradient"])
+        assert abs(float(f) - val_ref) <= 1e-12 * max(1.0, abs(val_ref)), (mode, float(f), val_ref)
+        assert abs(float(gr) - grad_ref) <= 1e-12, (mode, float(gr), grad_ref)
+
+
+# ---------------------------------------------------------------- chunked == serial
+CFGS = [
+    dict(),
+    dict(bs2=16),
+    dict(bs2=64),
+    dict(score_bs=32, bs2=16),
+    dict(score_bs=32, bs2=32, mb=4),
+    dict(mb=16, wy_eps=0.05),
+    dict(diag="lean"),
+]
+
+
+@pytest.mark.parametrize("kw", CFGS)
+def test_chunked_equals_token_serial(kw):
+    cfg = O.OracleCfg(**kw)
+    q, k, v, w, b, g, h0 = rand_inputs(1, 2, 192, 16, 7, h0=True)
+    o, hf = O.forward_ref(q, k, v, w, b, g, 0.25, h0, cfg)
+    sw = lambda x: x.transpose(1, 2)
+    if cfg.wy_eps == 0.0:
+        os_, hs = O.token_serial_ref(sw(q), sw(k), sw(v), sw(g), sw(b), sw(w), 0.25, h0)
+        assert rel(o, sw(os_)) < 1e-10 and rel(hf, hs) < 1e-10
+    # kernel semantics (two-level scores, BTL or lean diagonal) agree with the oracle form
+    kf = O.kernel_forward_ref(q, k, v, w, b, g, 0.25, h0, cfg)
+    assert rel(kf["o"], o) < 1e-10 and rel(kf["h_final"], hf) < 1e-10
+
+
+def test_damping_changes_result_consistently():
+    """wy_eps > 0 is a different operator; both oracle forms must agree on it."""
+    q, k, v, w, b, g, h0 = rand_inputs(1, 1, 128, 16, 3)
+    c0, c1 = O.OracleCfg(), O.OracleCfg(wy_eps=0.1)
+    o0, _ = O.forward_ref(q, k, v, w, b, g, 0.25, h0, c0)
+    o1, _ = O.forward_ref(q, k, v, w, b, g, 0.25, h0, c1)
+    assert rel(o1, o0) > 1e-4
+
+
+# ---------------------------------------------------------------- scores
+def brute_scores(q, k, b, gc, scale):
+    """Triple loop over (i, j, d) in numpy float64 (tests/test_gdn2_full_math_correctness.py:169-183)."""
+    q, k, b, gc = (np.asarray(x) for x in (q, k, b, gc))
+    T, D = q.shape
+    Aq = np.zeros((T, T)); Ak = np.zeros((T, T))
+    for i in range(T):
+        for j in range(i + 1):
+            e = np.exp(gc[i] - gc[j])
+            Aq[i, j] = scale * np.sum(q[i] * k[j] * e)
+            if j < i:
+                Ak[i, j] = np.sum(b[i] * k[i] * k[j] * e)
+    return Aq, Ak
+
+
+@pytest.mark.parametrize("kw", CFGS[:5] + [dict(diag="lean", bs2=16)])
+def test_scores_brute_force(kw):
+    cfg = O.OracleCfg(**kw)
+    rng = np.random.default_rng(11)
+    T, D = 64, 8
+    q, k = rng.normal(size=(T, D)), rng.normal(size=(T, D))
+    b = rng.uniform(0.2, 1, size=(T, D))
+    gc = np.cumsum(-np.abs(rng.normal(size=(T, D))) * 0.2, axis=0)
+    Aq_bf, Ak_bf = brute_scores(q, k, b, gc, 0.3)
+    for fn in (O.blr_scores_ref, O.btl_scores):
+        Aq, Ak = fn(t64(q), t64(k), t64(b), t64(gc), 0.3, cfg)
+        assert np.max(np.abs(Aq.numpy() - Aq_bf)) < 1e-12
+        assert np.max(np.abs(Ak.numpy() - Ak_bf)) < 1e-12
+
+
+def test_btl_overflow_outside_domain():
+    """BTL legs overflow when the half span passes ~88 (domain.py:1-7): the sanitized scores
+    then differ from the exact ones; inside the domain they agree."""
+    rng = np.random.default_rng(0)
+    T, D = 64, 8
+    f32 = lambda x: torch.as_tensor(x, dtype=torch.float32)
+    q, k = f32(rng.normal(size=(T, D)) * 0.3), f32(rng.normal(size=(T, D)) * 0.3)
+    b = f32(np.abs(rng.normal(size=(T, D))) * 0.5)
+    for c, bad in ((0.5, False), (8.0, True)):
+        gc = torch.cumsum(torch.full((T, D), -c, dtype=torch.float32), 0)
+        cb = O.OracleCfg(bs2=32)
+        _, Ab = O.btl_scores(q, k, b, gc, 0.125, cb)
+        _, Al = O.btl_scores(q, k, b, gc, 0.125, cb.with_(diag="lean"))
+        assert (rel(Ab, Al) > 1e-3) == bad
+
+
+# ---------------------------------------------------------------- inverse
+@pytest.mark.parametrize("mb", [2, 4, 8, 16, 32])
+@pytest.mark.parametrize("eps", [0.0, 0.01])
+def test_ladder_inverse_vs_scipy(mb, eps):
+    rng = np.random.default_rng(mb)
+    T = 64
+    S = np.tril(rng.normal(size=(T, T)) * 0.1, -1)
+    A = O.ladder_inverse(t64(S), eps, T, mb, "highest").numpy()
+    M = np.eye(T) + (1 - eps) * S
+    ref = scipy.linalg.solve_triangular(M, np.eye(T), lower=True, unit_diagonal=True)
+    assert np.max(np.abs(A - ref)) < 1e-12
+    assert np.max(np.abs(M @ A - np.eye(T))) < 1e-12
+    assert np.all(np.triu(A, 1) == 0) and np.all(np.diag(A) == 1)
+
+
+def test_micro_inv_brute_force():
+    rng = np.random.default_rng(5)
+    S = np.tril(rng.normal(size=(4, 4)), -1)
+    X = O.micro_inv(t64(S)).numpy()
+    # explicit inverse of a 4x4 unit lower triangular matrix by cofactors (numpy.linalg.inv)
+    assert np.max(np.abs(X - np.linalg.inv(np.eye(4) + S))) < 1e-13
+
+
+# ---------------------------------------------------------------- gradients
+def test_autograd_vs_finite_differences_on_serial():
+    """T1 (tests_gdn2/test_t1_finite_diff.py:12-33), in float64 throughout."""
+    q, k, v, w, b, g, _ = rand_inputs(1, 1, 128, 16, 1)
+    cfg = O.OracleCfg()
+    gr = O.grad_ref(q, k, v, w, b, g, 0.25, None, cfg)
+    rng = np.random.default_rng(1)
+    dirs = [t64(rng.normal(size=q.shape)) for _ in range(6)]
+    an = sum(float((gr[n] * d).sum()) for n, d in zip(("dq", "dk", "dv", "dw", "db", "dg"), dirs))
+    sw = lambda x: x.transpose(1, 2)
+
+    def f(s):
+        qq, kk, vv, ww, bb, gg = (x + s * d for x, d in zip((q, k, v, w, b, g), dirs))
+        o, hf = O.token_serial_ref(sw(qq), sw(kk), sw(vv), sw(gg), sw(bb), sw(ww), 0.25)
+        return float((o * o).sum() + (hf * hf).sum())
+
+    eps = 1e-5
+    fd = (f(eps) - f(-eps)) / (2 * eps)
+    assert abs(an - fd) / abs(fd) < 1e-7, (an, fd)
+
+
+AB_CFGS = [
+    dict(),
+    dict(bs2=16),
+    dict(bs2=64, mb=4),
+    dict(score_bs=32, bs2=16),
+    dict(diag="lean"),
+    dict(wy_eps=0.05),
+]
+
+
+@pytest.mark.parametrize("kw", AB_CFGS)
+def test_analytic_backward_matches_autograd(kw):
+    """The kernel-semantics backward (bwd/mega.py + bwd/b4.py restated) equals autograd of
+    the oracle forward: pins both, and the residual definitions (A, Aqk, h_pre, v_new)."""
+    cfg = O.OracleCfg(**kw)
+    q, k, v, w, b, g, h0 = rand_inputs(1, 2, 192, 16, 9, h0=True)
+    gr = O.grad_ref(q, k, v, w, b, g, 0.25, h0, cfg)
+    kf = O.kernel_forward_ref(q, k, v, w, b, g, 0.25, h0, cfg)
+    ch = lambda t: O.to_chunks(t, cfg.bt)
+    bw = O.backward_mega_ref(*map(ch, (q, k, v, w, b, g)), kf["A"], kf["Aqk"], kf["h_pre"], kf["v_new"],
+                             ch(2 * kf["o"]), 2 * kf["h_final"], 0.25, cfg)
+    for n in ("dq", "dk", "dv", "dw", "db", "dg"):
+        assert rel(O.from_chunks(bw[n]), gr[n]) < 1e-9, n
+    assert rel(bw["dh0"], gr["dh0"]) < 1e-9
+
+
+@pytest.mark.parametrize("kw", [dict(), dict(bs2=16), dict(score_bs=32, bs2=16), dict(bs2=64)])
+def test_b4_closed_form_vs_autograd(kw):
+    cfg = O.OracleCfg(**kw)
+    rng = np.random.default_rng(2)
+    T, D = 64, 8
+    q, k = t64(rng.normal(size=(T, D))), t64(rng.normal(size=(T, D)))
+    b = t64(rng.uniform(0.2, 1, size=(T, D)))
+    gc = t64(np.cumsum(-np.abs(rng.normal(size=(T, D))) * 0.1, axis=0))
+    dAq, dAk = t64(rng.normal(size=(T, T))), t64(rng.normal(size=(T, T)))
+    causal, strict = O.causal_masks(T)
+    dAq, dAk = dAq * causal, dAk * strict
+    leaves = [x.clone().requires_grad_(True) for x in (q, k, b, gc)]
+    Aq, Ak = O.btl_scores(*leaves, 0.3, cfg)
+    gq, gk, gb, ggc = torch.autograd.grad((Aq * dAq).sum() + (Ak * dAk).sum(), leaves)
+    dq, dk, db, dgc = O.b4_exact_f64_np(q, k, b, gc, dAq, dAk, 0.3)
+    for x, y in ((dq, gq), (dk, gk), (db, gb), (dgc, ggc)):
+        assert np.max(np.abs(x - y.numpy())) < 1e-10
+    # and the two-level B4 restatement (bwd/b4.py) agrees with the closed form
+    dq2, dk2, db2, dgc2 = O._b4_2l(q, k, b, gc, dAq, dAk, 0.3, cfg, torch.matmul)
+    for x, y in ((dq, dq2), (dk, dk2), (db, db2), (dgc, dgc2)):
+        assert np.max(np.abs(x - y.numpy())) < 1e-10
+
+
+def test_b5_reverse_cumsum():
+    rng = np.random.default_rng(4)
+    x = t64(rng.normal(size=(64, 8)))
+    triu = torch.triu(torch.ones(64, 64))
+    assert torch.allclose(triu @ x, torch.flip(torch.cumsum(torch.flip(x, [0]), 0), [0]), atol=1e-12)
+
+
+def test_dot_modes():
+    rng = np.random.default_rng(6)
+    a, b = t64(rng.normal(size=(32, 64))), t64(rng.normal(size=(64, 16)))
+    ref = a @ b
+    e3 = rel(O.make_dot("bf16x3")(a, b), ref)
+    e1 = rel(O.make_dot("default")(a, b), ref)
+    assert e3 < 2e-5 and 1e-4 < e1 < 3e-2 and e3 < e1
+    x = torch.tensor([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -3.14159])
+    assert torch.equal(O.bf16_round(x), x.float().bfloat16().double())
+
+
+def test_causality_of_gradient():
+    """T5 causality (tests_gdn2/test_t5_grad_vs_reference.py:41-48): g beyond p does not
+    change dq before p."""
+    q, k, v, w, b, g, _ = rand_inputs(1, 1, 128, 16, 2)
+    cfg = O.OracleCfg()
+    p = 96
+    g2 = g.clone()
+    g2[:, :, p] -= 1.0
+
+    def dq_o_only(gg):       # loss on o only, as in the reference test
+        lv = [x.clone().requires_grad_(True) for x in (q, k, v, w, b, gg)]
+        o, _ = O.forward_ref(*lv, 0.25, None, cfg)
+        return torch.autograd.grad((o * o).sum(), lv[0])[0]
+    assert torch.equal(dq_o_only(g)[:, :, :p], dq_o_only(g2)[:, :, :p])
+
+
+# ---------------------------------------------------------------- planted mistakes
+def test_planted_mistakes_are_caught(monkeypatch):
+    """Each plausible slip in the oracle must fail one of the pins above."""
+    q, k, v, w, b, g, h0 = rand_inputs(1, 1, 128, 16, 8, h0=True)
+    sw = lambda x: x.transpose(1, 2)
+    os_, hs = O.token_serial_ref(sw(q), sw(k), sw(v), sw(g), sw(b), sw(w), 0.25, h0)
+    cfg = O.OracleCfg()
+
+    def fwd_err():
+        o, hf = O.forward_ref(q, k, v, w, b, g, 0.25, h0, cfg)
+        return max(rel(o, sw(os_)), rel(hf, hs))
+
+    assert fwd_err() < 1e-10
+    orig_scan, orig_scores, orig_wy = O.inter_chunk_scan_ref, O.blr_scores_ref, O.recompute_wy_ref
+
+    def scan_sign(Aqk, wp, u, kg, qg, gl, scale, h0_, cfg_, dot=None):     # v_new = u + wp h
+        return orig_scan(Aqk, -wp, u, kg, qg, gl, scale, h0_, cfg_, dot)
+    monkeypatch.setattr(O, "inter_chunk_scan_ref", scan_sign)
+    assert fwd_err() > 1e-3
+    monkeypatch.setattr(O, "inter_chunk_scan_ref", orig_scan)
+
+    def scores_strict(q_, k_, b_, gc, scale, cfg_):                       # Aqk loses its diagonal
+        Aq, Ak = orig_scores(q_, k_, b_, gc, scale, cfg_)
+        return Aq * O.causal_masks(cfg_.bt)[1], Ak
+    monkeypatch.setattr(O, "blr_scores_ref", scores_strict)
+    assert fwd_err() > 1e-3
+    monkeypatch.setattr(O, "blr_scores_ref", orig_scores)
+
+    def wy_nodecay(q_, k_, v_, w_, b_, gc, A, cfg_, dot=None):            # drops e^gc in wp
+        wp, u, kg, qg, gl = orig_wy(q_, k_, v_, w_, b_, gc, A, cfg_, dot)
+        return (A @ (b_ * k_)), u, kg, qg, gl
+    monkeypatch.setattr(O, "recompute_wy_ref", wy_nodecay)
+    assert fwd_err() > 1e-3
+    monkeypatch.setattr(O, "recompute_wy_ref", orig_wy)
+
+    # a transposed leaf in the inverse is caught by the scipy pin
+    S = torch.tril(torch.randn(64, 64, generator=torch.Generator().manual_seed(0)) * 0.1, -1)
+    bad = O.ladder_inverse(S.T.tril(-1) + S.tril(-1) * 0, 0.0, 64, 8)
+    ref = torch.as_tensor(scipy.linalg.solve_triangular((torch.eye(64) + S).numpy(), np.eye(64), lower=True,
+                                                        unit_diagonal=True))
+    assert float((bad - ref).abs().max()) > 1e-3
+
+    # a dropped (1-eps) factor in dAkk is caught by the analytic-vs-autograd pin
+    cfg_e = O.OracleCfg(wy_eps=0.05)
+    gr = O.grad_ref(q, k, v, w, b, g, 0.25, h0, cfg_e)
+    kf = O.kernel_forward_ref(q, k, v, w, b, g, 0.25, h0, cfg_e)
+    ch = lambda t: O.to_chunks(t, 64)
+    bw = O.backward_mega_ref(*map(ch, (q, k, v, w, b, g)), kf["A"], kf["Aqk"], kf["h_pre"], kf["v_new"],
+                             ch(2 * kf["o"]), 2 * kf["h_final"], 0.25, cfg_e.with_(wy_eps=0.0))
+    assert max(rel(O.from_chunks(bw[n]), gr[n]) for n in ("dq", "dk", "db", "dg")) > 1e-4

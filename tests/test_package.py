@@ -1,0 +1,150 @@
+"""CPU tests of the host side: config surface (tests_gdn2/test_t9_package.py), the C ABI
+library (loads, exports every symbol declared in include/gdn2.h, validates descriptors,
+reports layouts), and the Python boundary's argument checks.  No GPU compute."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def test_import_and_prod_preset():
+    from atomic_gdn2 import make_cfg
+    c = make_cfg()
+    assert (c.bt, c.score_bs, c.bs2, c.mb, c.diag) == (128, 128, 32, 8, "btl")
+    assert c.btl_half_span_limit < 88.0
+    assert (c.dot_mode, c.solve_dot_mode, c.b3_dot_mode) == ("highest", "bf16x3", "bf16x3")
+
+
+@pytest.mark.parametrize("bs2", [8, 16, 32, 64, 128])
+def test_gmax_tied_to_bs2(bs2):
+    from atomic_gdn2 import make_cfg
+    assert make_cfg(bs2=bs2).btl_half_span_limit < 88.0
+
+
+def test_bad_config_rejected():
+    from atomic_gdn2 import BLRConfig
+    for kw in (dict(bt=100), dict(bs2=48), dict(mb=6), dict(diag="x"), dict(b3_dot_mode="fp8"),
+               dict(wy_eps=1.0)):
+        with pytest.raises(ValueError):
+            BLRConfig(**kw)
+
+
+def test_with_and_properties():
+    from atomic_gdn2 import make_cfg, PROD
+    c = make_cfg(bt=64, bc=32, score_bs=64, bs2=32)
+    assert c.with_(bs2=16).bs2 == 16 and c.n_sub == 1 and c.n_inner == 2
+    assert PROD is make_cfg
+
+
+def _header_functions():
+    txt = (ROOT / "include" / "gdn2.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(gdn2_\w+)\s*\(", txt, re.M)))
+
+
+def test_library_exports_every_header_symbol():
+    from atomic_gdn2 import _lib
+    L = _lib.lib()
+    names = _header_functions()
+    assert len(names) >= 10, names
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+    assert L.gdn2_abi_version() == 1
+
+
+def test_descriptor_struct_matches_header():
+    from atomic_gdn2 import _lib
+    assert ctypes.sizeof(_lib.Gdn2Desc) == 12 * 4 + 4 * 8
+    assert _lib.Gdn2Desc.scale.offset == 48
+
+
+def _desc(**kw):
+    from atomic_gdn2 import make_cfg, _lib
+    cfg = make_cfg(bt=64, bc=32, score_bs=64, bs2=32, mb=8, wy_eps=0.0)
+    shape = dict(B=4, H=6, L=2048, D=128)
+    shape.update({k: v for k, v in kw.items() if k in shape})
+    cfg = cfg.with_(**{k: v for k, v in kw.items() if k not in shape})
+    return _lib.make_desc(cfg, shape["B"], shape["H"], shape["L"], shape["D"], 128 ** -0.5)
+
+
+def test_residual_layout_and_workspaces():
+    from atomic_gdn2 import _lib
+    offs, tot = _lib.residual_layout(_desc())
+    N = 4 * 6 * 32
+    sizes = [N * 64 * 64 * 4, N * 64 * 64 * 4, N * 128 * 128 * 4] + [N * 64 * 128 * 4] * 4 + [N * 128 * 4]
+    for i, (o, s) in enumerate(zip(offs, sizes)):
+        assert o % 256 == 0
+        nxt = offs[i + 1] if i + 1 < len(offs) else tot
+        assert nxt - o >= s
+    L = _lib.lib()
+    d = _desc()
+    assert L.gdn2_fwd_workspace_bytes(ctypes.byref(d), 1) == N * 64 * 128 * 4
+    assert L.gdn2_bwd_workspace_bytes(ctypes.byref(d)) >= N * (4 * 64 * 128 + 128 * 128 + 128) * 4
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(bt=128, bc=64, score_bs=128), "bt == 64"),
+    (dict(D=96), "D in"),
+    (dict(bs2=8, g_max=20.0), "bs2 >= 16"),
+    (dict(L=2000), "divisible"),
+])
+def test_descriptor_validation(kw, msg):
+    from atomic_gdn2 import _lib
+    with pytest.raises(ValueError, match=msg):
+        _lib.residual_layout(_desc(**kw))
+
+
+def test_null_pointers_rejected_without_gpu_work():
+    from atomic_gdn2 import _lib
+    d = _desc()
+    st = _lib.lib().gdn2_fwd(ctypes.byref(d), *([None] * 12))
+    assert st == 1 and b"null" in _lib.lib().gdn2_last_error()
+
+
+def test_python_boundary_errors():
+    from atomic_gdn2 import make_cfg, make_blr_trainable
+    cfg = make_cfg(bt=64, bc=32, score_bs=64, bs2=32)
+    fn = make_blr_trainable(cfg, 0.125)
+    x = torch.zeros(1, 1, 100, 64)
+    with pytest.raises(ValueError, match="divisible"):
+        fn(x, x, x, x, x, x)
+    y = torch.zeros(1, 1, 128, 64)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        fn(y, y, y, y, y, y)
+    with pytest.raises(ValueError, match="shape"):
+        fn(y, y, y, y, y, torch.zeros(1, 1, 128, 32))
+
+
+def test_synthetic_inputs_recipe():
+    from atomic_gdn2.synthetic import make_inputs_np
+    (q, k, v, w, b, g), scale = make_inputs_np(1, 2, 128, 64, seed=0)
+    assert scale == pytest.approx(1 / 8)
+    for x in (q, k, w):
+        assert np.allclose(np.linalg.norm(x.astype(np.float64), axis=-1), 1, atol=1e-6)
+    assert (b > 0).all() and (b < 1).all() and (g < 0).all()
+    rng = np.random.Generator(np.random.PCG64(0))
+    draws = [rng.standard_normal((1, 2, 128, 64)) for _ in range(3)]   # order q, k, v
+    assert np.array_equal(v, draws[2].astype(np.float32))
+
+
+def test_golden_fixture_inputs_are_reproduced():
+    from atomic_gdn2.synthetic import make_inputs_np, inputs_sha256
+    gold = np.load(ROOT / "tests" / "golden" / "config1_seed0.npz", allow_pickle=False)
+    arrs, _ = make_inputs_np(1, 2, 256, 128, seed=0)
+    assert inputs_sha256(arrs) == str(gold["sha256"])
+
+
+def test_golden_fixture_matches_oracle():
+    """The committed fixture is what the oracle computes today (oracle drift check)."""
+    from atomic_gdn2.synthetic import make_inputs_np
+    from oracle import gdn2_oracle as O
+    gold = np.load(ROOT / "tests" / "golden" / "config1_seed0.npz", allow_pickle=False)
+    arrs, scale = make_inputs_np(1, 2, 256, 128, seed=0)
+    t = [torch.from_numpy(a).double() for a in arrs]
+    gr = O.grad_ref(*t, scale, None, O.OracleCfg(bt=64, score_bs=64, bs2=32, mb=8, wy_eps=0.0))
+    for n in ("o", "h_final", "dq", "dk", "dv", "dw", "db", "dg"):
+        assert O.rel_l2(gold[n], gr[n]) < 1e-6, n
