@@ -20,9 +20,14 @@ OUT = HERE / "atomic_gdn2" / "_lib" / "libgdn2_hip.so"
 ARCH = os.environ.get("GDN2_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops: keep the compiler from emitting packed fp32 VALU ops.
+# -amdgpu-mfma-vgpr-form: keep MFMA accumulators in VGPRs.  With accumulators in AGPRs the
+#   compiler placed ~8 wait states between the last v_mfma_f32_16x16x4_f32 of a chain and the
+#   v_accvgpr_read of its 4th result register, and that register came back stale on gfx950
+#   (only accumulator element 3 wrong, only where the last k-step contributes).
 HIPFLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
     f"-I{HERE.parent / 'include'}",
 ]

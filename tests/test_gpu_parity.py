@@ -166,6 +166,61 @@ def test_wy_stage_config1(cfg1):
     assert float((M @ A.double() - I).abs().max()) < 1e-4
 
 
+def test_forward_residuals_config1(cfg1):
+    """gdn2_fwd through the C ABI: every residual sub-buffer and o / h_final per chunk vs
+    the kernel-semantics oracle (localises a forward error to a stage and a chunk)."""
+    from atomic_gdn2 import _lib
+    from oracle import gdn2_oracle as O
+    arrs, scale, _ = cfg1
+    banner("fwd residuals config1")
+    cfg = base_cfg()
+    xs = to_dev(arrs)
+    B, H, L, D = arrs[0].shape
+    nc = L // 64
+    desc = _lib.make_desc(cfg, B, H, L, D, scale)
+    offs, tot = _lib.residual_layout(desc)
+    res = torch.zeros(tot, dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(_lib.lib().gdn2_fwd_workspace_bytes(ctypes.byref(desc), 1), dtype=torch.uint8, device="cuda")
+    o = torch.empty(B, H, L, D, device="cuda")
+    hf = torch.empty(B, H, D, D, device="cuda")
+    h0 = torch.zeros(B, H, D, D, device="cuda")
+    _lib.check(_lib.lib().gdn2_fwd(ctypes.byref(desc), *map(_lib.ptr, xs), _lib.ptr(h0), _lib.ptr(o), _lib.ptr(hf),
+                                   _lib.ptr(res), _lib.ptr(ws), _lib.stream_handle()), "gdn2_fwd")
+    torch.cuda.synchronize()
+    shapes = dict(aqk=(B, H, nc, 64, 64), A=(B, H, nc, 64, 64), h_pre=(B, H, nc, D, D), v_new=(B, H, nc, 64, D),
+                  wp=(B, H, nc, 64, D), kg=(B, H, nc, 64, D), qg=(B, H, nc, 64, D), gl=(B, H, nc, D))
+    got = {}
+    for n, off in zip(_lib.RES_NAMES, offs):
+        cnt = int(np.prod(shapes[n]))
+        got[n] = res[off:off + 4 * cnt].view(torch.float32).reshape(shapes[n]).cpu()
+    t = [torch.from_numpy(a).double() for a in arrs]
+    oc = O.OracleCfg.from_cfg(cfg)
+    st = O.wy_stage_ref(*t, scale, oc)
+    kf = O.kernel_forward_ref(*t, scale, None, oc)
+    ref = dict(aqk=st["Aqk"], A=st["A"], wp=st["wp"], kg=st["kg"], qg=st["qg"], gl=st["gc_last"],
+               h_pre=kf["h_pre"], v_new=kf["v_new"])
+    errs = {n: [rel_l2(got[n][:, :, c], ref[n][:, :, c]) for c in range(nc)] for n in ref}
+    oc_ = O.to_chunks(o.cpu(), 64)
+    ro = O.to_chunks(kf["o"], 64)
+    errs["o"] = [rel_l2(oc_[:, :, c], ro[:, :, c]) for c in range(nc)]
+    errs["h_final"] = [rel_l2(hf, kf["h_final"])]
+    banner("per-chunk rel-L2: " + "; ".join(f"{n}: " + ",".join(f"{e:.1e}" for e in v) for n, v in errs.items()))
+    # error map of o, chunk 0, head 0: rows in 16-row tiles x columns in 16-column slices
+    d0 = (oc_[0, 0, 0] - ro[0, 0, 0]).abs()
+    emap = d0.reshape(4, 16, D // 16, 16).amax(dim=(1, 3))
+    banner("o chunk0 max-abs error by (row tile, col slice):\n" + "\n".join(
+        " ".join(f"{x:.1e}" for x in row) for row in emap.tolist()))
+    d1 = (got["h_pre"][0, 0, 1] - ref["h_pre"][0, 0, 1]).abs()
+    emap = d1.reshape(D // 16, 16, D // 16, 16).amax(dim=(1, 3))
+    banner("h after chunk0 max-abs error by (row tile, col slice):\n" + "\n".join(
+        " ".join(f"{x:.1e}" for x in row) for row in emap.tolist()))
+    banner("o chunk0 per-row max-abs error: " + " ".join(f"{x:.0e}" for x in d0.amax(dim=1).tolist()))
+    banner("h after chunk0 per-row max-abs error: " + " ".join(f"{x:.0e}" for x in d1.amax(dim=1).tolist()))
+    banner("h after chunk0 per-col max-abs error: " + " ".join(f"{x:.0e}" for x in d1.amax(dim=0).tolist()))
+    bad = {n: v for n, v in errs.items() if max(v[1:] if n == "h_pre" else v) > 1e-5}
+    assert not bad, bad
+
+
 def test_forward_and_grads_config1(cfg1):
     arrs, scale, gold = cfg1
     banner("fwd+bwd config1")
