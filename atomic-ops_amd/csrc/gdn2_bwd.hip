@@ -2,11 +2,7 @@
 // one reverse loop per (batch, head), bwd/mega.py:9-58; here the sequential part and the
 // chunk-parallel part are separate launches so that the chunk-parallel part fills the GPU).
 //
-//   scan_bwd_kernel  one workgroup per (batch, head, 16-column value slice); reverse over
-//                    chunks with the dh slice resident in LDS:
-//                      dv_new = san(Aqk^T dO + Kg dh)                      (mega.py:33)
-//                      dh     = san(Qg^T (s dO) + e^gamma dh - Wp^T dv_new) (mega.py:36)
-//                    and stores dv_new and the incoming dh (dh_next) per chunk.
+//   (the reverse state scan, dv_new and dh_next per chunk, is in gdn2_scan.hip)
 //   bwd_state_kernel one workgroup per chunk: the reductions over the value dimension
 //                      dQg = (s dO) h_pre^T, dWp = -dv_new h_pre^T, dKg = v_new dh_next^T
 //                    and the row sums sum_v dh_next * h_pre                 (mega.py:38-40,50)
@@ -18,17 +14,6 @@
 
 namespace gdn2 {
 
-template <int D>
-struct ScanBLayout {
-  static constexpr int DVB = 16, LD = D + 4, LT = T + 4, LV = DVB + 4;
-  static constexpr int OFF_WP = 0, OFF_QG = T * LD, OFF_KG = 2 * T * LD, OFF_AQ = 3 * T * LD;
-  static constexpr int OFF_DO = OFF_AQ + T * LT;
-  static constexpr int OFF_DH = OFF_DO + T * LV;
-  static constexpr int OFF_DV = OFF_DH + D * LV;
-  static constexpr int OFF_GAM = OFF_DV + T * LV;
-  static constexpr int TOTAL = OFF_GAM + D;
-};
-
 template <int LD>
 __device__ __forceinline__ void load_rows(float* dst, const float* __restrict__ src, int rows, int cols,
                                           int tid, int nt) {
@@ -36,85 +21,6 @@ __device__ __forceinline__ void load_rows(float* dst, const float* __restrict__ 
   for (int e = tid; e < rows * cols / 4; e += nt) {
     const int i = (4 * e) / cols, d = (4 * e) % cols;
     *reinterpret_cast<float4*>(dst + i * LD + d) = s4p[e];
-  }
-}
-
-template <int D>
-__global__ __launch_bounds__(256) void scan_bwd_kernel(ScanBwdArgs a) {
-  using Lay = ScanBLayout<D>;
-  constexpr int DVB = Lay::DVB, NVB = D / DVB, LD = Lay::LD, LT = Lay::LT, LV = Lay::LV, NT = 256;
-  __shared__ float smem[Lay::TOTAL];
-  float* sWp = smem + Lay::OFF_WP;
-  float* sQg = smem + Lay::OFF_QG;
-  float* sKg = smem + Lay::OFF_KG;
-  float* sAq = smem + Lay::OFF_AQ;
-  float* sdO = smem + Lay::OFF_DO;
-  float* sDH = smem + Lay::OFF_DH;
-  float* sDV = smem + Lay::OFF_DV;
-  float* sGam = smem + Lay::OFF_GAM;
-  const Cfg& cf = a.cfg;
-  const int mode = cf.b3_mode;
-  const float clip = cf.clip;
-  const int vb = blockIdx.x % NVB, bh = blockIdx.x / NVB;
-  const int tid = threadIdx.x, w = wave_id();
-  const int c0 = vb * DVB;
-
-  for (int e = tid; e < D * DVB; e += NT) {
-    const int i = e / DVB, j = e % DVB;
-    sDH[i * LV + j] = a.dhf[(size_t)bh * D * D + i * D + c0 + j];
-  }
-  for (int c = a.nc - 1; c >= 0; --c) {
-    const size_t ch = (size_t)bh * a.nc + c;
-    const size_t tb = ch * T * D;
-    load_rows<LD>(sWp, a.wp + tb, T, D, tid, NT);
-    load_rows<LD>(sQg, a.qg + tb, T, D, tid, NT);
-    load_rows<LD>(sKg, a.kg + tb, T, D, tid, NT);
-    load_rows<LT>(sAq, a.aqk + ch * T * T, T, T, tid, NT);
-    for (int e = tid; e < T * DVB; e += NT) {
-      const int i = e / DVB, j = e % DVB;
-      sdO[i * LV + j] = a.dout[tb + i * D + c0 + j];
-    }
-    for (int e = tid; e < D; e += NT) sGam[e] = a.gl[ch * D + e];
-    // dh entering this chunk's step (mega.py:35 dh_next = dh)
-    for (int e = tid; e < D * DVB; e += NT) {
-      const int i = e / DVB, j = e % DVB;
-      a.dh_next[ch * D * D + (size_t)i * D + c0 + j] = sDH[i * LV + j];
-    }
-    __syncthreads();
-
-    // dv_new = san(Aqk^T dO + Kg dh): row tile w
-    {
-      f4 x1 = {0.f, 0.f, 0.f, 0.f}, x2 = {0.f, 0.f, 0.f, 0.f};
-      mma_tile(mode, x1, tr(sAq, LT).shift(16 * w, 0), rm(sdO, LV), T);
-      mma_tile(mode, x2, rm(sKg, LD).shift(16 * w, 0), rm(sDH, LV), D);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 16 * w + tile_row(r), j = tile_col();
-        const float x = sanitize(x1[r] + x2[r], clip);
-        sDV[i * LV + j] = x;
-        a.dv_new[tb + i * D + c0 + j] = x;
-      }
-    }
-    __syncthreads();
-    // dh = san(Qg^T (s dO) + dh e^{min(gamma,0)} - Wp^T dv_new); wave w owns D/4 rows
-#pragma unroll
-    for (int tt = 0; tt < D / 64; ++tt) {
-      const int i0 = w * (D / 4) + tt * 16;
-      f4 y1 = {0.f, 0.f, 0.f, 0.f}, y2 = {0.f, 0.f, 0.f, 0.f};
-      mma_tile(mode, y1, tr(sQg, LD).shift(i0, 0), rm(sdO, LV, cf.scale), T);
-      mma_tile(mode, y2, tr(sWp, LD).shift(i0, 0), rm(sDV, LV), T);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = i0 + tile_row(r), j = tile_col();
-        const float dh = sDH[i * LV + j];
-        sDH[i * LV + j] = sanitize((y1[r] + dh * exp_nonpos(sGam[i])) - y2[r], clip);
-      }
-    }
-    __syncthreads();
-  }
-  for (int e = tid; e < D * DVB; e += NT) {
-    const int i = e / DVB, j = e % DVB;
-    a.dh0[(size_t)bh * D * D + i * D + c0 + j] = sDH[i * LV + j];
   }
 }
 
@@ -127,7 +33,7 @@ struct StateLayout {
   static constexpr int TOTAL = OFF_DH + RB * LD;
 };
 
-template <int D>
+template <int D, int B3>
 __global__ __launch_bounds__(512) void bwd_state_kernel(BwdStateArgs a) {
   using Lay = StateLayout<D>;
   constexpr int LD = Lay::LD, RB = Lay::RB, NT = 512, NW = 8;
@@ -138,7 +44,6 @@ __global__ __launch_bounds__(512) void bwd_state_kernel(BwdStateArgs a) {
   float* sHp = smem + Lay::OFF_HP;
   float* sDH = smem + Lay::OFF_DH;
   const Cfg& cf = a.cfg;
-  const int mode = cf.b3_mode;
   const int chunk = blockIdx.x, tid = threadIdx.x, wv = wave_id();
   const size_t tb = (size_t)chunk * T * D, hb = (size_t)chunk * D * D;
   load_rows<LD>(sdO, a.dout + tb, T, D, tid, NT);
@@ -155,7 +60,7 @@ __global__ __launch_bounds__(512) void bwd_state_kernel(BwdStateArgs a) {
       f4 acc = {0.f, 0.f, 0.f, 0.f};
       const View A = mat == 0 ? rm(sdO, LD, cf.scale) : (mat == 1 ? rm(sDV, LD, -1.f) : rm(sVn, LD));
       const View B = tr(mat == 2 ? sDH : sHp, LD);
-      mma_tile(mode, acc, A.shift(ti * 16, 0), B.shift(0, tj * 16), D);
+      mma_tile<B3>(acc, A.shift(ti * 16, 0), B.shift(0, tj * 16), D);
       float* out = mat == 0 ? a.dqg : (mat == 1 ? a.dwp : a.dkg);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -197,7 +102,7 @@ struct Strip {
   __device__ static int rtile(int w, int m) { return w / NS + m * STEP; }
 };
 
-template <int D>
+template <int D, int B3>
 __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   using Lay = BwdWyLayout<D>;
   using St = Strip<D>;
@@ -211,7 +116,6 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   float* sA = smem + Lay::OFF_A;
   float* sCol = smem + Lay::OFF_COL;
   const Cfg& cf = a.cfg;
-  const int m3 = cf.b3_mode;
   const float clip = cf.clip, scale = cf.scale;
   const int chunk = blockIdx.x, tid = threadIdx.x, wv = wave_id();
   const size_t tb = (size_t)chunk * T * D, sb = (size_t)chunk * T * T;
@@ -233,7 +137,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   for (int t = wv; t < 16; t += NW) {
     const int ti = t / 4, tj = t % 4;
     f4 acc = {0.f, 0.f, 0.f, 0.f};
-    mma_tile(m3, acc, rm(sX, LD).shift(ti * 16, 0), tr(sY, LD).shift(0, tj * 16), D);
+    mma_tile<B3>(acc, rm(sX, LD).shift(ti * 16, 0), tr(sY, LD).shift(0, tj * 16), D);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = ti * 16 + tile_row(r), j = tj * 16 + tile_col();
@@ -255,7 +159,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
 #pragma unroll
   for (int m = 0; m < 2; ++m) {
     const int t = wv + 8 * m, ti = t / 4, tj = t % 4;
-    mma_tile(m3, accA[m], rm(sX, LD).shift(ti * 16, 0), tr(sY, LD).shift(0, tj * 16), D);
+    mma_tile<B3>(accA[m], rm(sX, LD).shift(ti * 16, 0), tr(sY, LD).shift(0, tj * 16), D);
   }
   __syncthreads();
   load_rows<LD>(sX, a.dv_new + tb, T, D, tid, NT);
@@ -268,7 +172,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   for (int m = 0; m < 2; ++m) {
     const int t = wv + 8 * m, ti = t / 4, tj = t % 4;
     f4 acc2 = {0.f, 0.f, 0.f, 0.f};
-    mma_tile(m3, acc2, rm(sX, LD).shift(ti * 16, 0), tr(sY, LD).shift(0, tj * 16), D);
+    mma_tile<B3>(acc2, rm(sX, LD).shift(ti * 16, 0), tr(sY, LD).shift(0, tj * 16), D);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = ti * 16 + tile_row(r), j = tj * 16 + tile_col();
@@ -282,7 +186,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   for (int t = wv; t < 16; t += NW) {
     const int ti = t / 4, tj = t % 4;
     f4 acc = {0.f, 0.f, 0.f, 0.f};
-    mma_tile(m3, acc, rm(sDA, LT).shift(ti * 16, 0), tr(sA, LT).shift(0, tj * 16), T);
+    mma_tile<B3>(acc, rm(sDA, LT).shift(ti * 16, 0), tr(sA, LT).shift(0, tj * 16), T);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = ti * 16 + tile_row(r), j = tj * 16 + tile_col();
@@ -296,7 +200,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     for (int m = 0; m < 2; ++m) {
       const int t = wv + 8 * m, ti = t / 4, tj = t % 4;
       accK[m] = f4{0.f, 0.f, 0.f, 0.f};
-      mma_tile(m3, accK[m], tr(sA, LT).shift(ti * 16, 0), rm(sTmp, LT).shift(0, tj * 16), T);
+      mma_tile<B3>(accK[m], tr(sA, LT).shift(ti * 16, 0), rm(sTmp, LT).shift(0, tj * 16), T);
     }
     __syncthreads();   // all reads of sDA (tmp GEMM) and sTmp done before overwriting
 #pragma unroll
@@ -359,8 +263,8 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
         if (r0 >= pc.row0 && r0 < pc.row0 + P) {     // rows of the piece: dq, dbk
           const int lr = r0 - pc.row0;
           f4 dqt = {0.f, 0.f, 0.f, 0.f}, dbt = {0.f, 0.f, 0.f, 0.f};
-          mma_tile(DOT_HIGHEST, dqt, rm(sDAq, LT).shift(r0, pc.col0), rm(sKt, LD).shift(0, strip * 16), P);
-          mma_tile(DOT_HIGHEST, dbt, rm(sDA, LT).shift(r0, pc.col0), rm(sKt, LD).shift(0, strip * 16), P);
+          mma_tile<DOT_HIGHEST>(dqt, rm(sDAq, LT).shift(r0, pc.col0), rm(sKt, LD).shift(0, strip * 16), P);
+          mma_tile<DOT_HIGHEST>(dbt, rm(sDA, LT).shift(r0, pc.col0), rm(sKt, LD).shift(0, strip * 16), P);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int i = r0 + tile_row(r), il = lr + tile_row(r), d = dcol;
@@ -374,8 +278,8 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
         if (r0 >= pc.col0 && r0 < pc.col0 + P) {     // columns of the piece: dk
           const int lc = r0 - pc.col0;
           f4 k1 = {0.f, 0.f, 0.f, 0.f}, k2 = {0.f, 0.f, 0.f, 0.f};
-          mma_tile(DOT_HIGHEST, k1, tr(sDAq + pc.row0 * LT, LT).shift(r0, 0), rm(sQt, LD).shift(0, strip * 16), P);
-          mma_tile(DOT_HIGHEST, k2, tr(sDA + pc.row0 * LT, LT).shift(r0, 0), rm(sBt, LD).shift(0, strip * 16), P);
+          mma_tile<DOT_HIGHEST>(k1, tr(sDAq + pc.row0 * LT, LT).shift(r0, 0), rm(sQt, LD).shift(0, strip * 16), P);
+          mma_tile<DOT_HIGHEST>(k2, tr(sDA + pc.row0 * LT, LT).shift(r0, 0), rm(sBt, LD).shift(0, strip * 16), P);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int j = r0 + tile_row(r), jl = lc + tile_row(r), d = dcol;
@@ -438,8 +342,8 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     f4 dkb = {0.f, 0.f, 0.f, 0.f}, dwv = {0.f, 0.f, 0.f, 0.f};
     // A^T is upper triangular: rows of tile rt only see k >= 16*rt
     const int k0 = 16 * rt;
-    mma_tile(m3, dkb, tr(sA, LT).shift(16 * rt, k0), rm(sX, LD).shift(k0, strip * 16), T - k0);
-    mma_tile(m3, dwv, tr(sA, LT).shift(16 * rt, k0), rm(sY, LD).shift(k0, strip * 16), T - k0);
+    mma_tile<B3>(dkb, tr(sA, LT).shift(16 * rt, k0), rm(sX, LD).shift(k0, strip * 16), T - k0);
+    mma_tile<B3>(dwv, tr(sA, LT).shift(16 * rt, k0), rm(sY, LD).shift(k0, strip * 16), T - k0);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = 16 * rt + tile_row(r), d = dcol, e = i * D + d;
@@ -499,21 +403,23 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   }
 }
 
-hipError_t launch_scan_bwd(int D, const ScanBwdArgs& a, hipStream_t s) {
-  if (D == 128) hipLaunchKernelGGL(scan_bwd_kernel<128>, dim3(a.n_bh * 8), dim3(256), 0, s, a);
-  else hipLaunchKernelGGL(scan_bwd_kernel<64>, dim3(a.n_bh * 4), dim3(256), 0, s, a);
-  return hipGetLastError();
-}
-
 hipError_t launch_bwd_state(int D, const BwdStateArgs& a, hipStream_t s) {
-  if (D == 128) hipLaunchKernelGGL(bwd_state_kernel<128>, dim3(a.n_chunks), dim3(512), 0, s, a);
-  else hipLaunchKernelGGL(bwd_state_kernel<64>, dim3(a.n_chunks), dim3(512), 0, s, a);
+  dispatch_mode(a.cfg.b3_mode, [&](auto m) {
+    constexpr int M = decltype(m)::value;
+    if (D == 128) hipLaunchKernelGGL((bwd_state_kernel<128, M>), dim3(a.n_chunks), dim3(512), 0, s, a);
+    else hipLaunchKernelGGL((bwd_state_kernel<64, M>), dim3(a.n_chunks), dim3(512), 0, s, a);
+    return 0;
+  });
   return hipGetLastError();
 }
 
 hipError_t launch_bwd_wy(int D, const BwdWyArgs& a, hipStream_t s) {
-  if (D == 128) hipLaunchKernelGGL(bwd_wy_kernel<128>, dim3(a.n_chunks), dim3(512), 0, s, a);
-  else hipLaunchKernelGGL(bwd_wy_kernel<64>, dim3(a.n_chunks), dim3(512), 0, s, a);
+  dispatch_mode(a.cfg.b3_mode, [&](auto m) {
+    constexpr int M = decltype(m)::value;
+    if (D == 128) hipLaunchKernelGGL((bwd_wy_kernel<128, M>), dim3(a.n_chunks), dim3(512), 0, s, a);
+    else hipLaunchKernelGGL((bwd_wy_kernel<64, M>), dim3(a.n_chunks), dim3(512), 0, s, a);
+    return 0;
+  });
   return hipGetLastError();
 }
 

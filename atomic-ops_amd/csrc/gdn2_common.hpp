@@ -14,6 +14,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace gdn2 {
 
 constexpr int T = 64;        // chunk length (cfg.bt) supported by the kernels
@@ -59,13 +61,64 @@ struct View {
 __device__ __forceinline__ View rm(const float* p, int ld, float mul = 1.f) { return View{p, ld, 1, mul}; }
 __device__ __forceinline__ View tr(const float* p, int ld, float mul = 1.f) { return View{p, 1, ld, mul}; }
 
+// ---- MFMA issue -----------------------------------------------------------------------
+// MFMAs are issued from inline asm with the accumulator tied in place ("+v"): SrcC is always
+// the destination, so no other value can be allocated into an in-flight MFMA's SrcC
+// registers, and the compiler's own MFMA wait-state tables are never relied on.  On gfx950
+// those tables were too short for v_mfma_f32_16x16x4_f32 in two ways: the 4th result
+// register read through v_accvgpr_read ~8 wait states after the last MFMA came back stale,
+// and VALU writes ~11 wait states after an MFMA whose SrcC differed from its destination
+// corrupted result elements 2-3.  Rules used here:
+//   * each asm block starts with s_nop 1 (VALU-written A/B operand -> MFMA read);
+//   * back-to-back MFMAs accumulating in place into the same registers are interlocked by
+//     the hardware (measured: 36 clk per dependent 16x16x4 f32 MFMA vs 32 independent);
+//   * before any non-MFMA instruction reads an accumulator, drain() holds 24 wait states
+//     and takes the accumulator as an operand, so no read can be scheduled above it.
+__device__ __forceinline__ void mfma_f32x1(f4& acc, float a, float b) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_16x16x4_f32 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma_f32x4(f4& acc, const float4& a, const float4& b) {
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_mfma_f32_16x16x4_f32 %0, %1, %5, %0\n\t"
+      "v_mfma_f32_16x16x4_f32 %0, %2, %6, %0\n\t"
+      "v_mfma_f32_16x16x4_f32 %0, %3, %7, %0\n\t"
+      "v_mfma_f32_16x16x4_f32 %0, %4, %8, %0"
+      : "+v"(acc)
+      : "v"(a.x), "v"(a.y), "v"(a.z), "v"(a.w), "v"(b.x), "v"(b.y), "v"(b.z), "v"(b.w));
+}
+__device__ __forceinline__ void mfma_bf16x1(f4& acc, const s4& a, const s4& b) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_16x16x16_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma_bf16x3(f4& acc, const s4& ah, const s4& al, const s4& bh, const s4& bl) {
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_mfma_f32_16x16x16_bf16 %0, %1, %3, %0\n\t"
+      "v_mfma_f32_16x16x16_bf16 %0, %1, %4, %0\n\t"
+      "v_mfma_f32_16x16x16_bf16 %0, %2, %3, %0"
+      : "+v"(acc)
+      : "v"(ah), "v"(al), "v"(bh), "v"(bl));
+}
+__device__ __forceinline__ void drain(f4& a) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(a));
+}
+__device__ __forceinline__ void drain(f4& a, f4& b) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void drain(f4& a, f4& b, f4& c) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(a), "+v"(b), "+v"(c));
+}
+__device__ __forceinline__ void drain(f4& a, f4& b, f4& c, f4& d) {
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+}
+
 // ---- one 16x16 output tile: acc += A[0:16, 0:K] * B[0:K, 0:16] ------------------------
-// A and B are views already shifted to the tile origin.  K % 16 == 0.
+// A and B are views already shifted to the tile origin.  K % 16 == 0.  The tile routines
+// end with drain(acc): the accumulator is ready for ordinary code when they return.
 __device__ __forceinline__ void mma_tile_f32(f4& acc, const View& A, const View& B, int K) {
   const int l = lane_id(), r = l & 15, g = l >> 4;
 #pragma unroll 4
-  for (int k0 = 0; k0 < K; k0 += 4)
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A.at(r, k0 + g), B.at(k0 + g, r), acc, 0, 0, 0);
+  for (int k0 = 0; k0 < K; k0 += 4) mfma_f32x1(acc, A.at(r, k0 + g), B.at(k0 + g, r));
 }
 
 template <bool THREE>
@@ -85,18 +138,68 @@ __device__ __forceinline__ void mma_tile_bf16(f4& acc, const View& A, const View
         bl[e] = (short)bf16_bits(b - bf16_val(hb));
       }
     }
-    acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bh, acc, 0, 0, 0);
-    if (THREE) {
-      acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bl, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, bh, acc, 0, 0, 0);
-    }
+    if (THREE) mfma_bf16x3(acc, ah, al, bh, bl);
+    else mfma_bf16x1(acc, ah, bh);
   }
 }
 
-__device__ __forceinline__ void mma_tile(int mode, f4& acc, const View& A, const View& B, int K) {
-  if (mode == DOT_HIGHEST) mma_tile_f32(acc, A, B, K);
-  else if (mode == DOT_BF16X3) mma_tile_bf16<true>(acc, A, B, K);
-  else mma_tile_bf16<false>(acc, A, B, K);
+// ---- one 16-wide k block with register operands ----------------------------------------
+// k-permuted mapping: within a 16-wide block, lane group g = l/16 owns k = 4g + e, e = 0..3,
+// so a lane supplies a = A[l%16][4g .. 4g+3] and b = B[4g .. 4g+3][l%16] as two float4.
+// highest: 4 fp32 MFMAs (step e pairs a[e] with b[e]); bf16 modes: one 16x16x16 bf16 MFMA
+// whose lane layout is exactly this (bf16x3: hi*hi + hi*lo + lo*hi).
+// The 16x16 result layout (lane l holds rows 4g..4g+3 of column l%16) is the B-operand
+// layout of the next k block, so a tile produced by one MFMA chain feeds another directly.
+// mma16 does not drain: callers chain several and drain() before reading the result.
+__device__ __forceinline__ void split4(const float4& x, s4& hi, s4& lo) {
+  const float v[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t h = bf16_bits(v[e]);
+    hi[e] = (short)h;
+    lo[e] = (short)bf16_bits(v[e] - bf16_val(h));
+  }
+}
+__device__ __forceinline__ s4 round4(const float4& x) {
+  s4 h;
+  h[0] = (short)bf16_bits(x.x); h[1] = (short)bf16_bits(x.y);
+  h[2] = (short)bf16_bits(x.z); h[3] = (short)bf16_bits(x.w);
+  return h;
+}
+// The dot mode is a template parameter everywhere an MFMA is issued: a runtime switch would
+// put branches between the MFMAs of a chain, and at the merge points the compiler copies
+// the accumulator right after the (opaque) asm MFMA -- a read it cannot know to delay.
+template <int MODE>
+__device__ __forceinline__ void mma16(f4& acc, const float4& a, const float4& b) {
+  if constexpr (MODE == DOT_HIGHEST) {
+    mfma_f32x4(acc, a, b);
+  } else if constexpr (MODE == DOT_BF16X3) {
+    s4 ah, al, bh, bl;
+    split4(a, ah, al);
+    split4(b, bh, bl);
+    mfma_bf16x3(acc, ah, al, bh, bl);
+  } else {
+    mfma_bf16x1(acc, round4(a), round4(b));
+  }
+}
+__device__ __forceinline__ float4 f4_to_float4(const f4& x) { return make_float4(x[0], x[1], x[2], x[3]); }
+__device__ __forceinline__ float4 scale4(const float4& x, float s) { return make_float4(s * x.x, s * x.y, s * x.z, s * x.w); }
+__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ void st4(float* p, const float4& x) { *reinterpret_cast<float4*>(p) = x; }
+
+template <int MODE>
+__device__ __forceinline__ void mma_tile(f4& acc, const View& A, const View& B, int K) {
+  if constexpr (MODE == DOT_HIGHEST) mma_tile_f32(acc, A, B, K);
+  else mma_tile_bf16<MODE == DOT_BF16X3>(acc, A, B, K);
+  drain(acc);
+}
+
+// Calls f(std::integral_constant<int, mode>) for a runtime dot mode.
+template <class F>
+inline auto dispatch_mode(int mode, F&& f) {
+  if (mode == DOT_HIGHEST) return f(std::integral_constant<int, DOT_HIGHEST>{});
+  if (mode == DOT_BF16X3) return f(std::integral_constant<int, DOT_BF16X3>{});
+  return f(std::integral_constant<int, DOT_DEFAULT>{});
 }
 
 // Scalar dot product of length n under a dot mode (used by the small ladder merges).

@@ -6,10 +6,7 @@
 //                   forward substitution + block doubling in LDS, then Wp = A (b*k*e^gc) and
 //                   U = A (w*v) on MFMA, plus the gated Kg, Qg and gamma = gc[T-1].
 //                   Semantics: fwd/scores.py:42-87, fwd/solve.py:9-48, fwd/cd_slim.py:14-21.
-//   scan_fwd_kernel one workgroup per (batch, head, 16-column slice of the value dim): the
-//                   D x 16 state slice stays in LDS across all chunks; per chunk
-//                   v_new = U - Wp h, o = s Qg h + Aqk v_new, h = e^gamma h + Kg^T v_new.
-//                   Semantics: fwd/cd_slim.py:12-30.
+//   (the forward state scan is in gdn2_scan.hip)
 #include "gdn2_kernels.hpp"
 
 namespace gdn2 {
@@ -28,7 +25,7 @@ struct WyFwdLayout {
   static_assert(R1 >= T * LD && R1 >= T * LT, "staging region too small");
 };
 
-template <int D>
+template <int D, int DOT>
 __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
   using Lay = WyFwdLayout<D>;
   constexpr int LD = Lay::LD, LT = Lay::LT, NT = 512, NW = NT / WAVE;
@@ -85,7 +82,7 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
       for (int t = wv; t < 2 * ntm; t += NW) {
         const int mat = t / ntm, ti = (t % ntm) / nt1, tj = t % nt1;
         f4 acc = {0.f, 0.f, 0.f, 0.f};
-        mma_tile(cf.dot_mode, acc, rm(mat == 0 ? sQs : sBs, LD).shift(ti * 16, 0),
+        mma_tile<DOT>(acc, rm(mat == 0 ? sQs : sBs, LD).shift(ti * 16, 0),
                  tr(sKs, LD).shift(0, tj * 16), D);
         float* out = mat == 0 ? sS : sK;
 #pragma unroll
@@ -188,7 +185,7 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
     for (int t = wv; t < 2 * NTM; t += NW) {
       const int mat = t / NTM, ti = (t % NTM) / NTJ, tj = t % NTJ;
       f4 acc = {0.f, 0.f, 0.f, 0.f};
-      mma_tile(cf.dot_mode, acc, rm(sI, LT).shift(ti * 16, 0), rm(mat ? sY : sX, LD).shift(0, tj * 16),
+      mma_tile<DOT>(acc, rm(sI, LT).shift(ti * 16, 0), rm(mat ? sY : sX, LD).shift(0, tj * 16),
                (ti + 1) * 16);
       float* out = mat ? a.u : a.wp;
 #pragma unroll
@@ -201,123 +198,11 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
 }
 
 // ------------------------------------------------------------------------------------
-// forward state scan
-// ------------------------------------------------------------------------------------
-template <int D>
-struct ScanLayout {
-  static constexpr int DVB = 16, LD = D + 4, LT = T + 4, LV = DVB + 4;
-  static constexpr int OFF_A = 0, OFF_B = T * LD, OFF_C = 2 * T * LD, OFF_S = 3 * T * LD;
-  static constexpr int OFF_X = OFF_S + T * LT;       // T x LV   (u / dO slice)
-  static constexpr int OFF_H = OFF_X + T * LV;       // D x LV   state slice
-  static constexpr int OFF_V = OFF_H + D * LV;       // T x LV   v_new / dv_new slice
-  static constexpr int OFF_GAM = OFF_V + T * LV;     // D
-  static constexpr int TOTAL = OFF_GAM + D;
-};
-
-template <int LD>
-__device__ __forceinline__ void load_tile_TxD(float* dst, const float* __restrict__ src, int D, int tid, int nt) {
-  const float4* s4p = reinterpret_cast<const float4*>(src);
-  for (int e = tid; e < T * D / 4; e += nt) {
-    const int i = (4 * e) / D, d = (4 * e) % D;
-    const float4 x = s4p[e];
-    *reinterpret_cast<float4*>(dst + i * LD + d) = x;
-  }
-}
-
-template <int D>
-__global__ __launch_bounds__(256) void scan_fwd_kernel(ScanFwdArgs a) {
-  using Lay = ScanLayout<D>;
-  constexpr int DVB = Lay::DVB, NVB = D / DVB, LD = Lay::LD, LT = Lay::LT, LV = Lay::LV, NT = 256;
-  __shared__ float smem[Lay::TOTAL];
-  float* sWp = smem + Lay::OFF_A;
-  float* sQg = smem + Lay::OFF_B;
-  float* sKg = smem + Lay::OFF_C;
-  float* sAq = smem + Lay::OFF_S;
-  float* sU = smem + Lay::OFF_X;
-  float* sH = smem + Lay::OFF_H;
-  float* sVn = smem + Lay::OFF_V;
-  float* sGam = smem + Lay::OFF_GAM;
-  const Cfg& cf = a.cfg;
-  const int mode = cf.dot_mode;
-  const float clip = cf.clip;
-  const int vb = blockIdx.x % NVB, bh = blockIdx.x / NVB;
-  const int tid = threadIdx.x, w = wave_id();
-  const int c0 = vb * DVB;
-
-  for (int e = tid; e < D * DVB; e += NT) {
-    const int i = e / DVB, j = e % DVB;
-    sH[i * LV + j] = a.h0 ? a.h0[(size_t)bh * D * D + i * D + c0 + j] : 0.f;
-  }
-  for (int c = 0; c < a.nc; ++c) {
-    const size_t ch = (size_t)bh * a.nc + c;
-    const size_t tb = ch * T * D;
-    load_tile_TxD<LD>(sWp, a.wp + tb, D, tid, NT);
-    load_tile_TxD<LD>(sQg, a.qg + tb, D, tid, NT);
-    load_tile_TxD<LD>(sKg, a.kg + tb, D, tid, NT);
-    {
-      const float4* s4p = reinterpret_cast<const float4*>(a.aqk + ch * T * T);
-      for (int e = tid; e < T * T / 4; e += NT) {
-        const int i = (4 * e) / T, j = (4 * e) % T;
-        *reinterpret_cast<float4*>(sAq + i * LT + j) = s4p[e];
-      }
-    }
-    for (int e = tid; e < T * DVB; e += NT) {
-      const int i = e / DVB, j = e % DVB;
-      sU[i * LV + j] = a.u[tb + i * D + c0 + j];
-    }
-    for (int e = tid; e < D; e += NT) sGam[e] = a.gl[ch * D + e];
-    __syncthreads();
-
-    // v_new = u - Wp h ; part of o: Qg h  (row tile w of the T x 16 slice)
-    f4 vn = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
-    mma_tile(mode, vn, rm(sWp, LD).shift(16 * w, 0), rm(sH, LV), D);
-    mma_tile(mode, o1, rm(sQg, LD).shift(16 * w, 0), rm(sH, LV), D);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = 16 * w + tile_row(r), j = tile_col();
-      const float x = sU[i * LV + j] - vn[r];
-      sVn[i * LV + j] = x;
-      if (a.v_new) a.v_new[tb + i * D + c0 + j] = x;
-    }
-    __syncthreads();
-
-    // o = san(s Qg h + Aqk v_new)
-    {
-      f4 o2 = {0.f, 0.f, 0.f, 0.f};
-      mma_tile(mode, o2, rm(sAq, LT).shift(16 * w, 0), rm(sVn, LV), T);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 16 * w + tile_row(r), j = tile_col();
-        a.o[tb + i * D + c0 + j] = sanitize(cf.scale * o1[r] + o2[r], clip);
-      }
-    }
-    // h = san(h e^{min(gamma,0)} + Kg^T v_new); wave w owns rows [w*D/4, (w+1)*D/4)
-#pragma unroll
-    for (int tt = 0; tt < D / 64; ++tt) {
-      const int i0 = w * (D / 4) + tt * 16;
-      f4 hn = {0.f, 0.f, 0.f, 0.f};
-      mma_tile(mode, hn, tr(sKg, LD).shift(i0, 0), rm(sVn, LV), T);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = i0 + tile_row(r), j = tile_col();
-        const float hold = sH[i * LV + j];
-        if (a.h_pre) a.h_pre[ch * D * D + (size_t)i * D + c0 + j] = hold;
-        sH[i * LV + j] = sanitize(hold * exp_nonpos(sGam[i]) + hn[r], clip);
-      }
-    }
-    __syncthreads();
-  }
-  for (int e = tid; e < D * DVB; e += NT) {
-    const int i = e / DVB, j = e % DVB;
-    a.hf[(size_t)bh * D * D + i * D + c0 + j] = sH[i * LV + j];
-  }
-}
-
-// ------------------------------------------------------------------------------------
 // diagnostics: plain GEMM through the MFMA tile routine
 // ------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void gemm_probe_kernel(int mode, const float* A, const float* B, float* C,
-                                                         int M, int N, int K) {
+template <int MODE>
+__global__ __launch_bounds__(256) void gemm_probe_kernel(const float* A, const float* B, float* C, int M, int N,
+                                                         int K) {
   __shared__ float sA[64 * 132];
   __shared__ float sB[128 * 68];
   const int tid = threadIdx.x;
@@ -328,7 +213,7 @@ __global__ __launch_bounds__(256) void gemm_probe_kernel(int mode, const float* 
   for (int t = wave_id(); t < nti * ntj; t += 4) {
     const int ti = t / ntj, tj = t % ntj;
     f4 acc = {0.f, 0.f, 0.f, 0.f};
-    mma_tile(mode, acc, rm(sA, 132).shift(ti * 16, 0), rm(sB, 68).shift(0, tj * 16), K);
+    mma_tile<MODE>(acc, rm(sA, 132).shift(ti * 16, 0), rm(sB, 68).shift(0, tj * 16), K);
 #pragma unroll
     for (int r = 0; r < 4; ++r) C[(ti * 16 + tile_row(r)) * N + tj * 16 + tile_col()] = acc[r];
   }
@@ -336,19 +221,20 @@ __global__ __launch_bounds__(256) void gemm_probe_kernel(int mode, const float* 
 
 hipError_t launch_gemm_probe(int mode, const float* A, const float* B, float* C, int M, int N, int K,
                              hipStream_t s) {
-  hipLaunchKernelGGL(gemm_probe_kernel, dim3(1), dim3(256), 0, s, mode, A, B, C, M, N, K);
+  dispatch_mode(mode, [&](auto m) {
+    hipLaunchKernelGGL(gemm_probe_kernel<decltype(m)::value>, dim3(1), dim3(256), 0, s, A, B, C, M, N, K);
+    return 0;
+  });
   return hipGetLastError();
 }
 
 hipError_t launch_wy_fwd(int D, const WyFwdArgs& a, hipStream_t s) {
-  if (D == 128) hipLaunchKernelGGL(wy_fwd_kernel<128>, dim3(a.n_chunks), dim3(512), 0, s, a);
-  else hipLaunchKernelGGL(wy_fwd_kernel<64>, dim3(a.n_chunks), dim3(512), 0, s, a);
-  return hipGetLastError();
-}
-
-hipError_t launch_scan_fwd(int D, const ScanFwdArgs& a, hipStream_t s) {
-  if (D == 128) hipLaunchKernelGGL(scan_fwd_kernel<128>, dim3(a.n_bh * 8), dim3(256), 0, s, a);
-  else hipLaunchKernelGGL(scan_fwd_kernel<64>, dim3(a.n_bh * 4), dim3(256), 0, s, a);
+  dispatch_mode(a.cfg.dot_mode, [&](auto m) {
+    constexpr int M = decltype(m)::value;
+    if (D == 128) hipLaunchKernelGGL((wy_fwd_kernel<128, M>), dim3(a.n_chunks), dim3(512), 0, s, a);
+    else hipLaunchKernelGGL((wy_fwd_kernel<64, M>), dim3(a.n_chunks), dim3(512), 0, s, a);
+    return 0;
+  });
   return hipGetLastError();
 }
 
