@@ -17,7 +17,7 @@ LIB_PATH = Path(os.environ.get("GDN2_LIB", Path(__file__).resolve().parent / "_l
 
 DOT_IDS = {"highest": 0, "bf16x3": 1, "default": 2}
 DIAG_IDS = {"btl": 0, "lean": 1}
-RES_NAMES = ("aqk", "A", "h_pre", "v_new", "wp", "kg", "qg", "gl")
+RES_NAMES = ("aqkT", "A", "h_pre", "v_new", "wpT", "kg", "qgT", "gl")
 KERNEL_NAMES = ("wy_fwd", "scan_fwd", "scan_bwd", "bwd_state", "bwd_wy")
 STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported configuration", 3: "HIP error"}
 

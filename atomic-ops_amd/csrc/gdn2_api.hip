@@ -97,13 +97,13 @@ Dims dims(const gdn2_desc* d) {
 
 void residual_sizes(const gdn2_desc* d, size_t sz[GDN2_RES_COUNT]) {
   const Dims x = dims(d);
-  sz[GDN2_RES_AQK] = x.n_chunks * x.tT * 4;
+  sz[GDN2_RES_AQKT] = x.n_chunks * x.tT * 4;
   sz[GDN2_RES_A] = x.n_chunks * x.tT * 4;
   sz[GDN2_RES_HPRE] = x.n_chunks * x.DD * 4;
   sz[GDN2_RES_VNEW] = x.n_chunks * x.tD * 4;
-  sz[GDN2_RES_WP] = x.n_chunks * x.tD * 4;
+  sz[GDN2_RES_WPT] = x.n_chunks * x.tD * 4;
   sz[GDN2_RES_KG] = x.n_chunks * x.tD * 4;
-  sz[GDN2_RES_QG] = x.n_chunks * x.tD * 4;
+  sz[GDN2_RES_QGT] = x.n_chunks * x.tD * 4;
   sz[GDN2_RES_GL] = x.n_chunks * x.D * 4;
 }
 
@@ -168,17 +168,12 @@ int gdn2_residual_layout(const gdn2_desc* d, size_t offsets[GDN2_RES_COUNT], siz
   return GDN2_OK;
 }
 
-// forward workspace: [u] or, without a residual buffer, [u | aqk | wp | kg | qg | gl]
+// forward workspace: [U^T | Aqk | Wp | Qg | Kg^T | gl]  (gl is used only without a residual)
 size_t gdn2_fwd_workspace_bytes(const gdn2_desc* d, int with_residual) {
   if (validate(d)) return 0;
   const Dims x = dims(d);
-  size_t n = align_up(x.n_chunks * x.tD * 4);
-  if (!with_residual) {
-    n += align_up(x.n_chunks * x.tT * 4);
-    n += 3 * align_up(x.n_chunks * x.tD * 4);
-    n += align_up(x.n_chunks * x.D * 4);
-  }
-  return n;
+  (void)with_residual;
+  return 4 * align_up(x.n_chunks * x.tD * 4) + align_up(x.n_chunks * x.tT * 4) + align_up(x.n_chunks * x.D * 4);
 }
 
 // backward workspace: [dv_new | dh_next | dqg | dwp | dkg | dlast]
@@ -200,33 +195,36 @@ int gdn2_fwd(const gdn2_desc* d, const float* q, const float* k, const float* v,
   const gdn2::Cfg cfg = make_cfg(d);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 
-  float *aqk, *A = nullptr, *hpre = nullptr, *vnew = nullptr, *wp, *kg, *qg, *gl;
-  float* u = at<float>(workspace, 0);
+  // chunk-parallel outputs the scan reads (row-major Wp, Qg, Aqk; transposed Kg, U)
+  size_t o2 = 0;
+  float* uT = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
+  float* aqk = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tT * 4);
+  float* wp = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
+  float* qg = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
+  float* kgT = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
+  float* gl = at<float>(workspace, o2);
+  // residuals for the backward (transposed Aqk, Wp, Qg; row-major Kg) -- training only
+  float *aqkT = nullptr, *A = nullptr, *hpre = nullptr, *vnew = nullptr, *wpT = nullptr, *kg = nullptr,
+        *qgT = nullptr;
   if (residual) {
     size_t off[GDN2_RES_COUNT], tot;
     residual_offsets(d, off, &tot);
-    aqk = at<float>(residual, off[GDN2_RES_AQK]);
+    aqkT = at<float>(residual, off[GDN2_RES_AQKT]);
     A = at<float>(residual, off[GDN2_RES_A]);
     hpre = at<float>(residual, off[GDN2_RES_HPRE]);
     vnew = at<float>(residual, off[GDN2_RES_VNEW]);
-    wp = at<float>(residual, off[GDN2_RES_WP]);
+    wpT = at<float>(residual, off[GDN2_RES_WPT]);
     kg = at<float>(residual, off[GDN2_RES_KG]);
-    qg = at<float>(residual, off[GDN2_RES_QG]);
+    qgT = at<float>(residual, off[GDN2_RES_QGT]);
     gl = at<float>(residual, off[GDN2_RES_GL]);
-  } else {
-    size_t o2 = align_up(x.n_chunks * x.tD * 4);
-    aqk = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tT * 4);
-    wp = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
-    kg = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
-    qg = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
-    gl = at<float>(workspace, o2);
   }
 
-  gdn2::WyFwdArgs wa{q, k, v, w, b, g, aqk, A, wp, u, kg, qg, gl, nullptr, (int)x.n_chunks, cfg};
+  gdn2::WyFwdArgs wa{q,  k,  v,   w,   b,   g,   aqk,     aqkT,       A, wp, wpT, nullptr, uT,
+                     kg, kgT, qg, qgT, gl, nullptr, (int)x.n_chunks, cfg};
   hipError_t e = timed(0, s, [&] { return gdn2::launch_wy_fwd(d->D, wa, s); });
   if (e != hipSuccess) return hip_fail(e, "wy_fwd launch");
 
-  gdn2::ScanFwdArgs sa{wp, u, kg, qg, gl, aqk, h0, o, h_final, hpre, vnew, (int)x.nc, (int)x.n_bh, cfg};
+  gdn2::ScanFwdArgs sa{wp, uT, kgT, qg, gl, aqk, h0, o, h_final, hpre, vnew, (int)x.nc, (int)x.n_bh, cfg};
   e = timed(1, s, [&] { return gdn2::launch_scan_fwd(d->D, sa, s); });
   if (e != hipSuccess) return hip_fail(e, "scan_fwd launch");
   return GDN2_OK;
@@ -247,13 +245,13 @@ int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v,
   size_t off[GDN2_RES_COUNT], tot;
   residual_offsets(d, off, &tot);
   void* res = const_cast<void*>(residual);
-  const float* aqk = at<float>(res, off[GDN2_RES_AQK]);
+  const float* aqkT = at<float>(res, off[GDN2_RES_AQKT]);
   const float* A = at<float>(res, off[GDN2_RES_A]);
   const float* hpre = at<float>(res, off[GDN2_RES_HPRE]);
   const float* vnew = at<float>(res, off[GDN2_RES_VNEW]);
-  const float* wp = at<float>(res, off[GDN2_RES_WP]);
+  const float* wpT = at<float>(res, off[GDN2_RES_WPT]);
   const float* kg = at<float>(res, off[GDN2_RES_KG]);
-  const float* qg = at<float>(res, off[GDN2_RES_QG]);
+  const float* qgT = at<float>(res, off[GDN2_RES_QGT]);
   const float* gl = at<float>(res, off[GDN2_RES_GL]);
 
   size_t o2 = 0;
@@ -264,7 +262,7 @@ int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v,
   float* dkg = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
   float* dlast = at<float>(workspace, o2);
 
-  gdn2::ScanBwdArgs sa{wp, kg, qg, gl, aqk, d_o, d_hf, dvn, dhn, dh0, (int)x.nc, (int)x.n_bh, cfg};
+  gdn2::ScanBwdArgs sa{wpT, kg, qgT, gl, aqkT, d_o, d_hf, dvn, dhn, dh0, (int)x.nc, (int)x.n_bh, cfg};
   hipError_t e = timed(2, s, [&] { return gdn2::launch_scan_bwd(d->D, sa, s); });
   if (e != hipSuccess) return hip_fail(e, "scan_bwd launch");
 
@@ -272,7 +270,7 @@ int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v,
   e = timed(3, s, [&] { return gdn2::launch_bwd_state(d->D, ba, s); });
   if (e != hipSuccess) return hip_fail(e, "bwd_state launch");
 
-  gdn2::BwdWyArgs wa{q, k, v, w, b, g, A, aqk, d_o, vnew, dvn, dqg, dwp, dkg, dlast,
+  gdn2::BwdWyArgs wa{q, k, v, w, b, g, A, aqkT, d_o, vnew, dvn, dqg, dwp, dkg, dlast,
                      dq, dk, dv, dw, db, dg, (int)x.n_chunks, cfg};
   e = timed(4, s, [&] { return gdn2::launch_bwd_wy(d->D, wa, s); });
   if (e != hipSuccess) return hip_fail(e, "bwd_wy launch");
@@ -288,7 +286,8 @@ int gdn2_wy_stage(const gdn2_desc* d, const float* q, const float* k, const floa
     return fail(GDN2_ERR_INVALID, "null tensor pointer");
   const Dims x = dims(d);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  gdn2::WyFwdArgs wa{q, k, v, w, b, g, aqk, A, wp, u, kg, qg, gl, akk, (int)x.n_chunks, make_cfg(d)};
+  gdn2::WyFwdArgs wa{q,  k,       v,       w,       b,       g,  aqk, nullptr, A, wp, nullptr, u, nullptr,
+                     kg, nullptr, qg, nullptr, gl, akk, (int)x.n_chunks, make_cfg(d)};
   hipError_t e = timed(0, s, [&] { return gdn2::launch_wy_fwd(d->D, wa, s); });
   if (e != hipSuccess) return hip_fail(e, "wy_fwd launch");
   return GDN2_OK;

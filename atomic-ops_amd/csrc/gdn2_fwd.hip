@@ -50,12 +50,23 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
   // 1. gc = cumsum(g) inside the chunk
   chunk_cumsum<D, LD, NT>(a.g + tb, sG);
 
-  // 2. gated k / q and gamma (cd_slim.py:17-21): kg = san(k e^{min(gl-gc,0)}), qg = san(q e^{min(gc,0)})
-  for (int e = tid; e < T * D; e += NT) {
-    const int i = e / D, d = e % D;
-    const float gi = sG[i * LD + d], gl = sG[(T - 1) * LD + d];
-    a.kg[tb + e] = sanitize(k[e] * exp_nonpos(gl - gi), clip);
-    a.qg[tb + e] = sanitize(q[e] * exp_nonpos(gi), clip);
+  // 2. gated k / q and gamma (cd_slim.py:17-21): kg = san(k e^{min(gl-gc,0)}), qg = san(q e^{min(gc,0)});
+  //    each thread does 4 consecutive rows of one column (row-major and transposed stores)
+  for (int e = tid; e < (T / 4) * D; e += NT) {
+    const int d = e % D, i0 = 4 * (e / D);
+    const float gl = sG[(T - 1) * LD + d];
+    float kv[4], qv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = i0 + r;
+      const float gi = sG[i * LD + d];
+      kv[r] = sanitize(k[i * D + d] * exp_nonpos(gl - gi), clip);
+      qv[r] = sanitize(q[i * D + d] * exp_nonpos(gi), clip);
+      if (a.kg) a.kg[tb + i * D + d] = kv[r];
+      if (a.qg) a.qg[tb + i * D + d] = qv[r];
+    }
+    if (a.kgT) st4(a.kgT + tb + (size_t)d * T + i0, make_float4(kv[0], kv[1], kv[2], kv[3]));
+    if (a.qgT) st4(a.qgT + tb + (size_t)d * T + i0, make_float4(qv[0], qv[1], qv[2], qv[3]));
   }
   if (tid < D) a.gl[(size_t)chunk * D + tid] = sG[(T - 1) * LD + tid];
 
@@ -112,15 +123,22 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
   }
 
   // 4. masks + sanitize (scores.py:84-87); Se = (1-eps) Akk for the solve (solve.py:25)
-  for (int e = tid; e < T * T; e += NT) {
-    const int i = e / T, j = e % T;
-    const float aq = j <= i ? sanitize(sS[i * LT + j], clip) : 0.f;
-    const float ak = j < i ? sanitize(sK[i * LT + j], clip) : 0.f;
-    sS[i * LT + j] = aq;
-    a.aqk[sb + e] = aq;
-    if (a.akk) a.akk[sb + e] = ak;
-    sK[i * LT + j] = ak * cf.ome;
-    sI[i * LT + j] = 0.f;
+  for (int e = tid; e < T * (T / 4); e += NT) {
+    const int j = e % T, i0 = 4 * (e / T);
+    float av[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = i0 + r;
+      const float aq = j <= i ? sanitize(sS[i * LT + j], clip) : 0.f;
+      const float ak = j < i ? sanitize(sK[i * LT + j], clip) : 0.f;
+      av[r] = aq;
+      sS[i * LT + j] = aq;
+      if (a.aqk) a.aqk[sb + i * T + j] = aq;
+      if (a.akk) a.akk[sb + i * T + j] = ak;
+      sK[i * LT + j] = ak * cf.ome;
+      sI[i * LT + j] = 0.f;
+    }
+    if (a.aqkT) st4(a.aqkT + sb + (size_t)j * T + i0, make_float4(av[0], av[1], av[2], av[3]));
   }
   __syncthreads();
 
@@ -188,11 +206,17 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
       mma_tile<DOT>(acc, rm(sI, LT).shift(ti * 16, 0), rm(mat ? sY : sX, LD).shift(0, tj * 16),
                (ti + 1) * 16);
       float* out = mat ? a.u : a.wp;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = ti * 16 + tile_row(r), d = tj * 16 + tile_col();
-        out[tb + i * D + d] = sanitize(acc[r], clip);
+      float* outT = mat ? a.uT : a.wpT;
+      const float4 x = make_float4(sanitize(acc[0], clip), sanitize(acc[1], clip), sanitize(acc[2], clip),
+                                   sanitize(acc[3], clip));
+      const int i0 = ti * 16 + tile_row(0), d = tj * 16 + tile_col();
+      if (out) {
+        out[tb + (i0 + 0) * D + d] = x.x;
+        out[tb + (i0 + 1) * D + d] = x.y;
+        out[tb + (i0 + 2) * D + d] = x.z;
+        out[tb + (i0 + 3) * D + d] = x.w;
       }
+      if (outT) st4(outT + tb + (size_t)d * T + i0, x);     // the 4 rows of a lane are consecutive
     }
   }
 }

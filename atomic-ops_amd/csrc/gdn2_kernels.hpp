@@ -25,23 +25,26 @@ struct Cfg {
   PieceList pieces;
 };
 
+// Per-chunk outputs of the WY build.  Row-major tiles are (T x D) / (T x T); the "T"
+// variants are the same tiles transposed, (D x T) / (T x T), written for the scans so that
+// all their A-operands are contiguous float4 loads.  Any pointer may be null (not written).
 struct WyFwdArgs {
   const float *q, *k, *v, *w, *b, *g;
-  float *aqk, *A, *wp, *u, *kg, *qg, *gl;
-  float* akk;          // optional: masked, sanitized Akk (before the (1-eps) factor)
+  float *aqk, *aqkT, *A, *wp, *wpT, *u, *uT, *kg, *kgT, *qg, *qgT, *gl;
+  float* akk;          // masked, sanitized Akk (before the (1-eps) factor)
   int n_chunks;        // B*H*nc
   Cfg cfg;
 };
 
 struct ScanFwdArgs {
-  const float *wp, *u, *kg, *qg, *gl, *aqk, *h0;
-  float *o, *hf, *h_pre, *v_new;   // h_pre / v_new may be null (forward-only)
+  const float *wp, *uT, *kgT, *qg, *gl, *aqk, *h0;
+  float *o, *hf, *h_pre, *v_new;   // h_pre / v_new null for a forward-only call
   int nc, n_bh;
   Cfg cfg;
 };
 
 struct ScanBwdArgs {
-  const float *wp, *kg, *qg, *gl, *aqk, *dout, *dhf;
+  const float *wpT, *kg, *qgT, *gl, *aqkT, *dout, *dhf;
   float *dv_new, *dh_next, *dh0;
   int nc, n_bh;
   Cfg cfg;

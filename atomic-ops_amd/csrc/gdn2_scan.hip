@@ -12,9 +12,12 @@
 // key rows across waves: each wave multiplies with its own state rows and writes a 16x16
 // partial tile per output row tile to LDS; a fixed-order sum over waves finishes them.
 // Products over the chunk's time axis (Kg^T v_new, Aqk v_new, Qg^T dO, Wp^T dv_new) read
-// v_new / dv_new from a transposed LDS slice with ds_read_b128.  A-operands stream from
-// global memory as float4 (or 4 scalars for transposed access) and are prefetched one chunk
-// ahead.  Per chunk: two workgroup barriers.
+// v_new / dv_new (and dO) from transposed LDS slices with ds_read_b128.  A-operands stream
+// from global memory as float4 (the WY kernel writes the transposed tiles Kg^T, Wp^T, Qg^T,
+// Aqk^T, U^T for this) and are prefetched one chunk ahead into the second of two register
+// sets; the chunk loop is unrolled by two so the sets never need copying, and all prefetch
+// loads are unconditional so the compiler's vmcnt waits stay exact.  Per chunk: two
+// workgroup barriers.
 //
 // Forward (fwd/cd_slim.py:12-30):  v_new = U - Wp h;  o = san(s Qg h + Aqk v_new);
 //                                  h = san(e^gamma h + Kg^T v_new)
@@ -37,13 +40,13 @@ template <int D>
 struct FwdOps {
   float4 wp[4];    // Wp[16ti + r][16w + 4g .. +3]            ti = 0..3
   float4 qg[4];    // Qg[16ti + r][16w + 4g .. +3]
-  float4 kg[4];    // {Kg[16u + 4g + e][16w + r]}_e            u = 0..3  (Kg^T block)
-  float4 aq[4];    // Aqk[16to + r][16u + 4g .. +3]            (o-tile waves)
-  float4 gm;       // gamma[16w + 4g + e]
-  float4 uu;       // U[16ti_p + 4g_p + e][c0 + j_p]           (v_new reduction pair)
+  float4 kg[4];    // Kg^T[16w + r][16u + 4g .. +3]           u = 0..3
+  float4 aq[4];    // Aqk[16to + r][16u + 4g .. +3]           (used by the o-tile waves)
+  float4 gm;       // gamma[16w + 4g .. +3]
+  float4 uu;       // U^T[c0 + j_p][16t_p + 4g_p .. +3]       (v_new reduction pair)
 };
 
-template <int D, int MODE>
+template <int D, int MODE, bool RES>
 __global__ __launch_bounds__(D / 16 * WAVE) void scan_fwd_kernel(ScanFwdArgs a) {
   constexpr int NW = D / 16, NT = NW * WAVE, NVB = D / 16, NP = 512 / NT;
   __shared__ float4 sPv[NW * 4 * WAVE];
@@ -52,12 +55,13 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_fwd_kernel(ScanFwdArgs a) 
   __shared__ float4 sO1[4 * WAVE];
   const Cfg& cf = a.cfg;
   const float clip = cf.clip, scale = cf.scale;
+  const int nc = a.nc;
   const int lin = xcd_remap(gridDim.x);
   const int vb = lin % NVB, bh = lin / NVB, c0 = 16 * vb;
   const int tid = threadIdx.x, l = lane_id(), r = l & 15, g = l >> 4, w = wave_id();
   const bool o_role = NW == 8 ? (w >= 4) : true;
-  const int to = NW == 8 ? w - 4 : w;
-  // the v_new reduction pair of this thread (tid < 256): output tile tp, lane lp of its layout
+  const int to = NW == 8 ? (w >= 4 ? w - 4 : 0) : w;
+  // the reduction pair of this thread: output tile tp, lane lp of its MFMA layout
   const int tp = (tid & 255) >> 6, lp = tid & 63, gp = lp >> 4, jp = lp & 15;
 
   f4 h;
@@ -65,38 +69,26 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_fwd_kernel(ScanFwdArgs a) 
   for (int e = 0; e < 4; ++e)
     h[e] = a.h0 ? a.h0[(size_t)bh * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r] : 0.f;
 
-  auto load = [&](FwdOps<D>& op, size_t ch) {
-    const size_t tb = ch * T * D;
+  auto load = [&](FwdOps<D>& op, int c) {
+    const size_t ch = (size_t)bh * nc + (c < nc ? c : nc - 1), tb = ch * T * D;
     const float* pw = a.wp + tb + (size_t)r * D + 16 * w + 4 * g;
     const float* pq = a.qg + tb + (size_t)r * D + 16 * w + 4 * g;
+    const float* pk = a.kgT + tb + (size_t)(16 * w + r) * T + 4 * g;
+    const float* pa = a.aqk + ch * T * T + (size_t)(16 * to + r) * T + 4 * g;
 #pragma unroll
-    for (int ti = 0; ti < 4; ++ti) {
-      op.wp[ti] = ld4(pw + 16 * ti * D);
-      op.qg[ti] = ld4(pq + 16 * ti * D);
-    }
-    const float* pk = a.kg + tb + (size_t)(4 * g) * D + 16 * w + r;
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-      op.kg[u] = make_float4(pk[(16 * u) * D], pk[(16 * u + 1) * D], pk[(16 * u + 2) * D], pk[(16 * u + 3) * D]);
-    if (o_role) {
-      const float* pa = a.aqk + ch * T * T + (size_t)(16 * to + r) * T + 4 * g;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) op.aq[u] = ld4(pa + 16 * u);
+    for (int i = 0; i < 4; ++i) {
+      op.wp[i] = ld4(pw + 16 * i * D);
+      op.qg[i] = ld4(pq + 16 * i * D);
+      op.kg[i] = ld4(pk + 16 * i);
+      op.aq[i] = ld4(pa + 16 * i);
     }
     op.gm = ld4(a.gl + ch * D + 16 * w + 4 * g);
-    if (tid < 256) {
-      const float* pu = a.u + tb + (size_t)(16 * tp + 4 * gp) * D + c0 + jp;
-      op.uu = make_float4(pu[0], pu[D], pu[2 * D], pu[3 * D]);
-    }
+    op.uu = ld4(a.uT + tb + (size_t)(c0 + jp) * T + 16 * tp + 4 * gp);
   };
 
-  FwdOps<D> op, nx;
-  load(op, (size_t)bh * a.nc);
-  for (int c = 0; c < a.nc; ++c) {
-    const size_t ch = (size_t)bh * a.nc + c;
-    const size_t tb = ch * T * D;
-    if (c + 1 < a.nc) load(nx, ch + 1);
-    if (a.h_pre) {
+  auto step = [&](const FwdOps<D>& op, int c) {
+    const size_t ch = (size_t)bh * nc + c, tb = ch * T * D;
+    if constexpr (RES) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) a.h_pre[ch * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r] = h[e];
     }
@@ -132,9 +124,9 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_fwd_kernel(ScanFwdArgs a) 
       if (mat == 0) {
         const float4 vn = make_float4(op.uu.x - s.x, op.uu.y - s.y, op.uu.z - s.z, op.uu.w - s.w);
         st4(&sVT[jp * LVT + 16 * tp + 4 * gp], vn);
-        if (a.v_new) {
-          float* pv = a.v_new + tb + (size_t)(16 * tp + 4 * gp) * D + c0 + jp;
-          pv[0] = vn.x; pv[D] = vn.y; pv[2 * D] = vn.z; pv[3 * D] = vn.w;
+        if constexpr (RES) {
+          float* pv2 = a.v_new + tb + (size_t)(16 * tp + 4 * gp) * D + c0 + jp;
+          pv2[0] = vn.x; pv2[D] = vn.y; pv2[2 * D] = vn.z; pv2[3 * D] = vn.w;
         }
       } else {
         sO1[pi] = s;
@@ -155,27 +147,36 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_fwd_kernel(ScanFwdArgs a) 
       drain(acc);
       const float4 o1 = sO1[to * WAVE + l];
       const float ov[4] = {o1.x, o1.y, o1.z, o1.w};
-      float* po = a.o + tb + (size_t)(16 * to + 4 * g) * D + c0 + r;
+      float* po2 = a.o + tb + (size_t)(16 * to + 4 * g) * D + c0 + r;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) po[e * D] = sanitize(scale * ov[e] + acc[e], clip);
+      for (int e = 0; e < 4; ++e) po2[e * D] = sanitize(scale * ov[e] + acc[e], clip);
     }
     drain(hn);
     const float gmv[4] = {op.gm.x, op.gm.y, op.gm.z, op.gm.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) h[e] = sanitize(h[e] * exp_nonpos(gmv[e]) + hn[e], clip);
-    op = nx;
+  };
+
+  FwdOps<D> A, B;
+  load(A, 0);
+  int c = 0;
+  for (; c + 1 < nc; c += 2) {
+    load(B, c + 1);
+    step(A, c);
+    load(A, c + 2);
+    step(B, c + 1);
   }
+  if (c < nc) step(A, c);
 #pragma unroll
   for (int e = 0; e < 4; ++e) a.hf[(size_t)bh * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r] = h[e];
 }
 
 template <int D>
 struct BwdOps {
-  float4 kg[4];    // Kg[16ti + r][16w + 4g .. +3]            ti = 0..3
-  float4 aqT[16 / (D / 16)];   // {Aqk[16u + 4g + e][16ta + r]}_e  for this wave's (ta, u) pairs
-  float4 qgT[4];   // {Qg[16u + 4g + e][16w + r]}_e
-  float4 wpT[4];   // {Wp[16u + 4g + e][16w + r]}_e
-  float4 dob[4];   // {dO[16u + 4g + e][c0 + r]}_e
+  float4 kg[4];              // Kg[16ti + r][16w + 4g .. +3]         ti = 0..3
+  float4 aqT[16 / (D / 16)]; // Aqk^T[16ta + r][16u + 4g .. +3]      for this wave's (ta, u) pairs
+  float4 qgT[4];             // Qg^T[16w + r][16u + 4g .. +3]
+  float4 wpT[4];             // Wp^T[16w + r][16u + 4g .. +3]
   float4 gm;
 };
 
@@ -184,75 +185,81 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
   constexpr int NW = D / 16, NT = NW * WAVE, NVB = D / 16, PA = 16 / NW;
   __shared__ float4 sP[NW * 4 * WAVE];
   __shared__ float sDVT[16 * LVT];
+  __shared__ float sDOT[2][16 * LVT];        // dO slice of the chunk, transposed, double-buffered
   const Cfg& cf = a.cfg;
   const float clip = cf.clip, scale = cf.scale;
+  const int nc = a.nc;
   const int lin = xcd_remap(gridDim.x);
   const int vb = lin % NVB, bh = lin / NVB, c0 = 16 * vb;
   const int tid = threadIdx.x, l = lane_id(), r = l & 15, g = l >> 4, w = wave_id();
   const int ta = (w * PA) / 4, ua = (w * PA) % 4;    // Aqk^T dO pairs (ta, ua .. ua+PA-1)
   const int tp = (tid & 255) >> 6, lp = tid & 63, gp = lp >> 4, jp = lp & 15;
+  // dO staging: thread t < 256 moves dO[t/4][c0 + 4(t%4) .. +3] of a chunk
+  const int srow = (tid & 255) >> 2, scol = 4 * (tid & 3);
 
   f4 dh;
 #pragma unroll
   for (int e = 0; e < 4; ++e) dh[e] = a.dhf[(size_t)bh * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r];
 
-  auto load = [&](BwdOps<D>& op, size_t ch) {
-    const size_t tb = ch * T * D;
+  // step s processes chunk nc-1-s; loads for a step past the last are clamped (unused)
+  auto chunk = [&](int s) { return (size_t)bh * nc + (s < nc ? nc - 1 - s : 0); };
+  auto load = [&](BwdOps<D>& op, int s) {
+    const size_t ch = chunk(s), tb = ch * T * D;
     const float* pk = a.kg + tb + (size_t)r * D + 16 * w + 4 * g;
+    const float* pa = a.aqkT + ch * T * T + (size_t)(16 * ta + r) * T + 4 * g;
+    const float* pq = a.qgT + tb + (size_t)(16 * w + r) * T + 4 * g;
+    const float* pw = a.wpT + tb + (size_t)(16 * w + r) * T + 4 * g;
 #pragma unroll
-    for (int ti = 0; ti < 4; ++ti) op.kg[ti] = ld4(pk + 16 * ti * D);
-    const float* pa = a.aqk + ch * T * T + (size_t)(4 * g) * T + 16 * ta + r;
-#pragma unroll
-    for (int q = 0; q < PA; ++q) {
-      const int u = ua + q;
-      op.aqT[q] = make_float4(pa[(16 * u) * T], pa[(16 * u + 1) * T], pa[(16 * u + 2) * T], pa[(16 * u + 3) * T]);
+    for (int i = 0; i < 4; ++i) {
+      op.kg[i] = ld4(pk + 16 * i * D);
+      op.qgT[i] = ld4(pq + 16 * i);
+      op.wpT[i] = ld4(pw + 16 * i);
     }
-    const float* pq = a.qg + tb + (size_t)(4 * g) * D + 16 * w + r;
-    const float* pw = a.wp + tb + (size_t)(4 * g) * D + 16 * w + r;
-    const float* pd = a.dout + tb + (size_t)(4 * g) * D + c0 + r;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      op.qgT[u] = make_float4(pq[(16 * u) * D], pq[(16 * u + 1) * D], pq[(16 * u + 2) * D], pq[(16 * u + 3) * D]);
-      op.wpT[u] = make_float4(pw[(16 * u) * D], pw[(16 * u + 1) * D], pw[(16 * u + 2) * D], pw[(16 * u + 3) * D]);
-      op.dob[u] = make_float4(pd[(16 * u) * D], pd[(16 * u + 1) * D], pd[(16 * u + 2) * D], pd[(16 * u + 3) * D]);
-    }
+    for (int q = 0; q < PA; ++q) op.aqT[q] = ld4(pa + 16 * (ua + q));
     op.gm = ld4(a.gl + ch * D + 16 * w + 4 * g);
   };
+  auto load_do = [&](int s) { return ld4(a.dout + chunk(s) * T * D + (size_t)srow * D + c0 + scol); };
+  auto stage_do = [&](int buf, const float4& x) {
+    if (tid < 256) {
+      sDOT[buf][(scol + 0) * LVT + srow] = x.x;
+      sDOT[buf][(scol + 1) * LVT + srow] = x.y;
+      sDOT[buf][(scol + 2) * LVT + srow] = x.z;
+      sDOT[buf][(scol + 3) * LVT + srow] = x.w;
+    }
+  };
 
-  BwdOps<D> op, nx;
-  load(op, (size_t)bh * a.nc + a.nc - 1);
-  for (int c = a.nc - 1; c >= 0; --c) {
-    const size_t ch = (size_t)bh * a.nc + c;
-    const size_t tb = ch * T * D;
-    if (c > 0) load(nx, ch - 1);
+  auto step = [&](const BwdOps<D>& op, int s) {
+    const int buf = s & 1;
+    const size_t ch = chunk(s), tb = ch * T * D;
+    const float4 dnext = load_do(s + 1);           // dO of the next step, staged below
     // dh entering this chunk's step (mega.py:35)
 #pragma unroll
     for (int e = 0; e < 4; ++e) a.dh_next[ch * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r] = dh[e];
-    // partial dv_new tiles: Kg[:, own rows] dh_own (+ this wave's share of Aqk^T dO)
+    float4 dob[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) dob[u] = ld4(&sDOT[buf][r * LVT + 16 * u + 4 * g]);
     const float4 db = f4_to_float4(dh);
-    // this wave's share of Aqk^T dO lands in partial tile ta: select its dO blocks with
-    // compile-time indices (a straight-line chain, no per-wave branch between MFMAs)
-    float4 dsel[PA];
-#pragma unroll
-    for (int q = 0; q < PA; ++q) {
-      dsel[q] = op.dob[0];
-#pragma unroll
-      for (int u = 1; u < 4; ++u)
-        if (u == ua + q) dsel[q] = op.dob[u];
-    }
     f4 p[4];
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) {
       p[ti] = f4{0.f, 0.f, 0.f, 0.f};
       mma16<MODE>(p[ti], op.kg[ti], db);
     }
+    // this wave's share of Aqk^T dO (partial tile ta); dO blocks picked with compile-time indices
     f4 pa = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int q = 0; q < PA; ++q) mma16<MODE>(pa, op.aqT[q], dsel[q]);
+    for (int q = 0; q < PA; ++q) {
+      float4 dsel = dob[0];
+#pragma unroll
+      for (int u = 1; u < 4; ++u)
+        if (u == ua + q) dsel = dob[u];
+      mma16<MODE>(pa, op.aqT[q], dsel);
+    }
     // Qg^T (s dO) for the own rows
     f4 y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < 4; ++u) mma16<MODE>(y, op.qgT[u], scale4(op.dob[u], scale));
+    for (int u = 0; u < 4; ++u) mma16<MODE>(y, op.qgT[u], scale4(dob[u], scale));
     drain(p[0], p[1], p[2], p[3]);
     drain(pa, y);
 #pragma unroll
@@ -263,17 +270,19 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
     }
     __syncthreads();
     if (tid < 256) {
-      float4 s = sP[tid];
+      float4 sm = sP[tid];
 #pragma unroll
       for (int w2 = 1; w2 < NW; ++w2) {
         const float4 x = sP[w2 * 4 * WAVE + tid];
-        s.x += x.x; s.y += x.y; s.z += x.z; s.w += x.w;
+        sm.x += x.x; sm.y += x.y; sm.z += x.z; sm.w += x.w;
       }
-      const float4 dv = make_float4(sanitize(s.x, clip), sanitize(s.y, clip), sanitize(s.z, clip), sanitize(s.w, clip));
+      const float4 dv = make_float4(sanitize(sm.x, clip), sanitize(sm.y, clip), sanitize(sm.z, clip),
+                                    sanitize(sm.w, clip));
       st4(&sDVT[jp * LVT + 16 * tp + 4 * gp], dv);
       float* pv = a.dv_new + tb + (size_t)(16 * tp + 4 * gp) * D + c0 + jp;
       pv[0] = dv.x; pv[D] = dv.y; pv[2 * D] = dv.z; pv[3 * D] = dv.w;
     }
+    stage_do(buf ^ 1, dnext);
     __syncthreads();
     f4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -282,17 +291,35 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
     const float gmv[4] = {op.gm.x, op.gm.y, op.gm.z, op.gm.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) dh[e] = sanitize((y[e] + dh[e] * exp_nonpos(gmv[e])) - z[e], clip);
-    op = nx;
+  };
+
+  stage_do(0, load_do(0));
+  BwdOps<D> A, B;
+  load(A, 0);
+  __syncthreads();
+  int s = 0;
+  for (; s + 1 < nc; s += 2) {
+    load(B, s + 1);
+    step(A, s);
+    load(A, s + 2);
+    step(B, s + 1);
   }
+  if (s < nc) step(A, s);
 #pragma unroll
   for (int e = 0; e < 4; ++e) a.dh0[(size_t)bh * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r] = dh[e];
 }
 
 hipError_t launch_scan_fwd(int D, const ScanFwdArgs& a, hipStream_t s) {
+  const bool res = a.h_pre != nullptr;
   dispatch_mode(a.cfg.dot_mode, [&](auto m) {
     constexpr int M = decltype(m)::value;
-    if (D == 128) hipLaunchKernelGGL((scan_fwd_kernel<128, M>), dim3(a.n_bh * 8), dim3(512), 0, s, a);
-    else hipLaunchKernelGGL((scan_fwd_kernel<64, M>), dim3(a.n_bh * 4), dim3(256), 0, s, a);
+    if (D == 128) {
+      if (res) hipLaunchKernelGGL((scan_fwd_kernel<128, M, true>), dim3(a.n_bh * 8), dim3(512), 0, s, a);
+      else hipLaunchKernelGGL((scan_fwd_kernel<128, M, false>), dim3(a.n_bh * 8), dim3(512), 0, s, a);
+    } else {
+      if (res) hipLaunchKernelGGL((scan_fwd_kernel<64, M, true>), dim3(a.n_bh * 4), dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((scan_fwd_kernel<64, M, false>), dim3(a.n_bh * 4), dim3(256), 0, s, a);
+    }
     return 0;
   });
   return hipGetLastError();

@@ -52,14 +52,18 @@ typedef struct gdn2_desc {
 } gdn2_desc;
 
 /* Residual buffer written by gdn2_fwd and read by gdn2_bwd: sub-buffers at the offsets
- * reported by gdn2_residual_layout (bytes, 256-aligned).  Shapes (float32):
- *   AQK, A  (B,H,nc,bt,bt)   gated q.k scores and the WY inverse      (pipeline.py:25)
- *   HPRE    (B,H,nc,D,D)     state entering each chunk                (cd_slim.py:22)
- *   VNEW    (B,H,nc,bt,D)    v_new of each chunk                      (cd_slim.py:23)
- *   WP, KG, QG (B,H,nc,bt,D) W = A(b k e^gc), gated k and q           (cd_slim.py:17-21)
- *   GL      (B,H,nc,D)       gc of the chunk's last row               (cd_slim.py:19) */
-enum { GDN2_RES_AQK = 0, GDN2_RES_A, GDN2_RES_HPRE, GDN2_RES_VNEW, GDN2_RES_WP, GDN2_RES_KG,
-       GDN2_RES_QG, GDN2_RES_GL, GDN2_RES_COUNT };
+ * reported by gdn2_residual_layout (bytes, 256-aligned).  Shapes (float32), per chunk:
+ *   AQKT  (B,H,nc,bt,bt)  gated q.k scores, transposed: AQKT[j][i] = Aqk[i][j]  (pipeline.py:25)
+ *   A     (B,H,nc,bt,bt)  the WY inverse (I + (1-eps) Akk)^-1                  (pipeline.py:25)
+ *   HPRE  (B,H,nc,D,D)    state entering each chunk                            (cd_slim.py:22)
+ *   VNEW  (B,H,nc,bt,D)   v_new of each chunk                                  (cd_slim.py:23)
+ *   WPT   (B,H,nc,D,bt)   W = A (b k e^gc), transposed                         (cd_slim.py:17)
+ *   KG    (B,H,nc,bt,D)   gated k                                              (cd_slim.py:20)
+ *   QGT   (B,H,nc,D,bt)   gated q, transposed                                  (cd_slim.py:21)
+ *   GL    (B,H,nc,D)      gc of the chunk's last row                           (cd_slim.py:19)
+ * Transposed tiles are what the reverse state scan reads as contiguous MFMA operands. */
+enum { GDN2_RES_AQKT = 0, GDN2_RES_A, GDN2_RES_HPRE, GDN2_RES_VNEW, GDN2_RES_WPT, GDN2_RES_KG,
+       GDN2_RES_QGT, GDN2_RES_GL, GDN2_RES_COUNT };
 
 int gdn2_abi_version(void);
 const char* gdn2_last_error(void);

@@ -82,7 +82,8 @@ def test_residual_layout_and_workspaces():
         assert nxt - o >= s
     L = _lib.lib()
     d = _desc()
-    assert L.gdn2_fwd_workspace_bytes(ctypes.byref(d), 1) == N * 64 * 128 * 4
+    # [U^T | Aqk | Wp | Qg | Kg^T | gl]
+    assert L.gdn2_fwd_workspace_bytes(ctypes.byref(d), 1) == N * (4 * 64 * 128 + 64 * 64 + 128) * 4
     assert L.gdn2_bwd_workspace_bytes(ctypes.byref(d)) >= N * (4 * 64 * 128 + 128 * 128 + 128) * 4
 
 
