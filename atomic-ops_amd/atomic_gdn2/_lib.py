@@ -18,7 +18,13 @@ LIB_PATH = Path(os.environ.get("GDN2_LIB", Path(__file__).resolve().parent / "_l
 DOT_IDS = {"highest": 0, "bf16x3": 1, "default": 2}
 DIAG_IDS = {"btl": 0, "lean": 1}
 RES_NAMES = ("aqkT", "A", "h_pre", "v_new", "wpT", "kg", "qgT", "gl")
-KERNEL_NAMES = ("wy_fwd", "scan_fwd", "scan_bwd", "bwd_state", "bwd_wy")
+# per residual: (rows, cols) of the stored matrix per chunk (T = bt, D = head dim), whether it
+# is stored in fragment layout, and whether it is the transpose of the named quantity
+RES_STORAGE = {"aqkT": ("T", "T", True, True), "A": ("T", "T", False, False),
+               "h_pre": ("D", "D", True, True), "v_new": ("D", "T", True, True),
+               "wpT": ("D", "T", True, True), "kg": ("T", "D", True, False),
+               "qgT": ("D", "T", True, True), "gl": (None, "D", False, False)}
+KERNEL_NAMES = ("wy_fwd", "scan_fwd", "scan_bwd", "bwd_state", "bwd_wy", "out_fwd")
 STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported configuration", 3: "HIP error"}
 
 _c_int, _c_dbl, _c_size, _vp = ctypes.c_int32, ctypes.c_double, ctypes.c_size_t, ctypes.c_void_p
@@ -89,6 +95,20 @@ def residual_layout(desc: Gdn2Desc):
     tot = _c_size()
     check(lib().gdn2_residual_layout(ctypes.byref(desc), offs, ctypes.byref(tot)), "gdn2_residual_layout")
     return list(offs), tot.value
+
+
+def decode_residual(name, flat, B, H, nc, T, D):
+    """Row-major (B, H, nc, rows, cols) tensor of one residual sub-buffer (``flat`` float32),
+    un-transposed: aqkT -> Aqk, wpT -> Wp, qgT -> Qg, h_pre / v_new in their natural layout."""
+    from .layout import from_frag
+    R, C, frag, transposed = RES_STORAGE[name]
+    dim = {"T": T, "D": D}
+    if R is None:
+        return flat[:B * H * nc * dim[C]].reshape(B, H, nc, dim[C])
+    R, C = dim[R], dim[C]
+    t = flat[:B * H * nc * R * C].reshape(B, H, nc, R * C)
+    t = from_frag(t, R, C) if frag else t.reshape(B, H, nc, R, C)
+    return t.transpose(-1, -2) if transposed else t
 
 
 def ptr(t):

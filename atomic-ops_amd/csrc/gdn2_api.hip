@@ -168,12 +168,15 @@ int gdn2_residual_layout(const gdn2_desc* d, size_t offsets[GDN2_RES_COUNT], siz
   return GDN2_OK;
 }
 
-// forward workspace: [U^T | Aqk | Wp | Qg | Kg^T | gl]  (gl is used only without a residual)
+// forward workspace (fragment layouts): [Wp | U^T | Kg^T | Qg | Aqk], and without a residual
+// also [gl | h_pre | v_new] (the scan's per-chunk outputs that the output kernel reads).
 size_t gdn2_fwd_workspace_bytes(const gdn2_desc* d, int with_residual) {
   if (validate(d)) return 0;
   const Dims x = dims(d);
-  (void)with_residual;
-  return 4 * align_up(x.n_chunks * x.tD * 4) + align_up(x.n_chunks * x.tT * 4) + align_up(x.n_chunks * x.D * 4);
+  size_t n = 4 * align_up(x.n_chunks * x.tD * 4) + align_up(x.n_chunks * x.tT * 4);
+  if (!with_residual)
+    n += align_up(x.n_chunks * x.D * 4) + align_up(x.n_chunks * x.DD * 4) + align_up(x.n_chunks * x.tD * 4);
+  return n;
 }
 
 // backward workspace: [dv_new | dh_next | dqg | dwp | dkg | dlast]
@@ -195,17 +198,16 @@ int gdn2_fwd(const gdn2_desc* d, const float* q, const float* k, const float* v,
   const gdn2::Cfg cfg = make_cfg(d);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 
-  // chunk-parallel outputs the scan reads (row-major Wp, Qg, Aqk; transposed Kg, U)
+  // operands of the scan and the output kernel, all in fragment layout
   size_t o2 = 0;
-  float* uT = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
-  float* aqk = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tT * 4);
-  float* wp = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
-  float* qg = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
-  float* kgT = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
-  float* gl = at<float>(workspace, o2);
-  // residuals for the backward (transposed Aqk, Wp, Qg; row-major Kg) -- training only
-  float *aqkT = nullptr, *A = nullptr, *hpre = nullptr, *vnew = nullptr, *wpT = nullptr, *kg = nullptr,
-        *qgT = nullptr;
+  auto take = [&](size_t bytes) { float* p = at<float>(workspace, o2); o2 += align_up(bytes); return p; };
+  float* wp = take(x.n_chunks * x.tD * 4);
+  float* uT = take(x.n_chunks * x.tD * 4);
+  float* kgT = take(x.n_chunks * x.tD * 4);
+  float* qg = take(x.n_chunks * x.tD * 4);
+  float* aqk = take(x.n_chunks * x.tT * 4);
+  // residuals for the backward -- training only; otherwise gl / h_pre / v_new live in the workspace
+  float *aqkT = nullptr, *A = nullptr, *wpT = nullptr, *kg = nullptr, *qgT = nullptr, *gl, *hpre, *vnew;
   if (residual) {
     size_t off[GDN2_RES_COUNT], tot;
     residual_offsets(d, off, &tot);
@@ -217,16 +219,28 @@ int gdn2_fwd(const gdn2_desc* d, const float* q, const float* k, const float* v,
     kg = at<float>(residual, off[GDN2_RES_KG]);
     qgT = at<float>(residual, off[GDN2_RES_QGT]);
     gl = at<float>(residual, off[GDN2_RES_GL]);
+  } else {
+    gl = take(x.n_chunks * x.D * 4);
+    hpre = take(x.n_chunks * x.DD * 4);
+    vnew = take(x.n_chunks * x.tD * 4);
   }
 
-  gdn2::WyFwdArgs wa{q,  k,  v,   w,   b,   g,   aqk,     aqkT,       A, wp, wpT, nullptr, uT,
-                     kg, kgT, qg, qgT, gl, nullptr, (int)x.n_chunks, cfg};
+  gdn2::WyFwdArgs wa{};
+  wa.q = q; wa.k = k; wa.v = v; wa.w = w; wa.b = b; wa.g = g;
+  wa.wp_f = wp; wa.wpT_f = wpT; wa.uT_f = uT; wa.kg_f = kg; wa.kgT_f = kgT; wa.qg_f = qg; wa.qgT_f = qgT;
+  wa.aqk_f = aqk; wa.aqkT_f = aqkT; wa.A = A; wa.gl = gl;
+  wa.n_chunks = (int)x.n_chunks;
+  wa.cfg = cfg;
   hipError_t e = timed(0, s, [&] { return gdn2::launch_wy_fwd(d->D, wa, s); });
   if (e != hipSuccess) return hip_fail(e, "wy_fwd launch");
 
-  gdn2::ScanFwdArgs sa{wp, uT, kgT, qg, gl, aqk, h0, o, h_final, hpre, vnew, (int)x.nc, (int)x.n_bh, cfg};
+  gdn2::ScanFwdArgs sa{wp, kgT, uT, gl, h0, h_final, hpre, vnew, (int)x.nc, (int)x.n_bh, cfg};
   e = timed(1, s, [&] { return gdn2::launch_scan_fwd(d->D, sa, s); });
   if (e != hipSuccess) return hip_fail(e, "scan_fwd launch");
+
+  gdn2::OutFwdArgs oa{qg, aqk, hpre, vnew, o, (int)x.n_chunks, cfg};
+  e = timed(5, s, [&] { return gdn2::launch_out_fwd(d->D, oa, s); });
+  if (e != hipSuccess) return hip_fail(e, "out_fwd launch");
   return GDN2_OK;
 }
 
@@ -270,7 +284,7 @@ int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v,
   e = timed(3, s, [&] { return gdn2::launch_bwd_state(d->D, ba, s); });
   if (e != hipSuccess) return hip_fail(e, "bwd_state launch");
 
-  gdn2::BwdWyArgs wa{q, k, v, w, b, g, A, aqkT, d_o, vnew, dvn, dqg, dwp, dkg, dlast,
+  gdn2::BwdWyArgs wa{q, k, v, w, b, g, A, d_o, vnew, dvn, dqg, dwp, dkg, dlast,
                      dq, dk, dv, dw, db, dg, (int)x.n_chunks, cfg};
   e = timed(4, s, [&] { return gdn2::launch_bwd_wy(d->D, wa, s); });
   if (e != hipSuccess) return hip_fail(e, "bwd_wy launch");
@@ -286,8 +300,11 @@ int gdn2_wy_stage(const gdn2_desc* d, const float* q, const float* k, const floa
     return fail(GDN2_ERR_INVALID, "null tensor pointer");
   const Dims x = dims(d);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  gdn2::WyFwdArgs wa{q,  k,       v,       w,       b,       g,  aqk, nullptr, A, wp, nullptr, u, nullptr,
-                     kg, nullptr, qg, nullptr, gl, akk, (int)x.n_chunks, make_cfg(d)};
+  gdn2::WyFwdArgs wa{};
+  wa.q = q; wa.k = k; wa.v = v; wa.w = w; wa.b = b; wa.g = g;
+  wa.A = A; wa.gl = gl; wa.aqk = aqk; wa.akk = akk; wa.wp = wp; wa.u = u; wa.kg = kg; wa.qg = qg;
+  wa.n_chunks = (int)x.n_chunks;
+  wa.cfg = make_cfg(d);
   hipError_t e = timed(0, s, [&] { return gdn2::launch_wy_fwd(d->D, wa, s); });
   if (e != hipSuccess) return hip_fail(e, "wy_fwd launch");
   return GDN2_OK;

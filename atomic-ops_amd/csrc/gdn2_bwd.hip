@@ -47,12 +47,12 @@ __global__ __launch_bounds__(512) void bwd_state_kernel(BwdStateArgs a) {
   const int chunk = blockIdx.x, tid = threadIdx.x, wv = wave_id();
   const size_t tb = (size_t)chunk * T * D, hb = (size_t)chunk * D * D;
   load_rows<LD>(sdO, a.dout + tb, T, D, tid, NT);
-  load_rows<LD>(sDV, a.dv_new + tb, T, D, tid, NT);
-  load_rows<LD>(sVn, a.v_new + tb, T, D, tid, NT);
+  load_fragT<LD>(sDV, a.dv_new_f + tb, D, T, 0, T, tid, NT);
+  load_fragT<LD>(sVn, a.v_new_f + tb, D, T, 0, T, tid, NT);
   for (int rb = 0; rb < D / RB; ++rb) {
     if (rb) __syncthreads();
-    load_rows<LD>(sHp, a.h_pre + hb + (size_t)rb * RB * D, RB, D, tid, NT);
-    load_rows<LD>(sDH, a.dh_next + hb + (size_t)rb * RB * D, RB, D, tid, NT);
+    load_fragT<LD>(sHp, a.h_pre_f + hb, D, D, rb * RB, RB, tid, NT);
+    load_fragT<LD>(sDH, a.dh_next_f + hb, D, D, rb * RB, RB, tid, NT);
     __syncthreads();
     // 3 outputs x 4 row tiles x 2 column tiles (this block of RB key rows)
     for (int t = wv; t < 24; t += NW) {
@@ -131,7 +131,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
 
   // dAqk = (dO v_new^T) * causal                                     (mega.py:32)
   load_rows<LD>(sX, a.dout + tb, T, D, tid, NT);
-  load_rows<LD>(sY, a.v_new + tb, T, D, tid, NT);
+  load_fragT<LD>(sY, a.v_new_f + tb, D, T, 0, T, tid, NT);
   load_rows<LT>(sA, a.A + sb, T, T, tid, NT);
   __syncthreads();
   for (int t = wv; t < 16; t += NW) {
@@ -162,7 +162,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     mma_tile<B3>(accA[m], rm(sX, LD).shift(ti * 16, 0), tr(sY, LD).shift(0, tj * 16), D);
   }
   __syncthreads();
-  load_rows<LD>(sX, a.dv_new + tb, T, D, tid, NT);
+  load_fragT<LD>(sX, a.dv_new_f + tb, D, T, 0, T, tid, NT);
   for (int e = tid; e < T * D; e += NT) {
     const int i = e / D, d = e % D;
     sY[i * LD + d] = w[e] * v[e];
@@ -333,7 +333,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   // dkb = A^T dWp, dwv = A^T dv_new (mega.py:42), the gate gradients dq3/dk3/db3/dgc3
   // (mega.py:45-51), and the combine with B4 (mega.py:52-59), tile by tile.
   load_rows<LD>(sX, a.dwp + tb, T, D, tid, NT);
-  load_rows<LD>(sY, a.dv_new + tb, T, D, tid, NT);
+  load_fragT<LD>(sY, a.dv_new_f + tb, D, T, 0, T, tid, NT);
   __syncthreads();
   f4 dgcT[NTW];
 #pragma unroll

@@ -194,6 +194,14 @@ __device__ __forceinline__ void mma_tile(f4& acc, const View& A, const View& B, 
   drain(acc);
 }
 
+// mma_tile under a runtime dot mode: the branch encloses whole tiles, each ending in drain(),
+// so no accumulator copy can land next to an in-flight MFMA.
+__device__ __forceinline__ void mma_tile_rt(int mode, f4& acc, const View& A, const View& B, int K) {
+  if (mode == DOT_HIGHEST) mma_tile<DOT_HIGHEST>(acc, A, B, K);
+  else if (mode == DOT_BF16X3) mma_tile<DOT_BF16X3>(acc, A, B, K);
+  else mma_tile<DOT_DEFAULT>(acc, A, B, K);
+}
+
 // Calls f(std::integral_constant<int, mode>) for a runtime dot mode.
 template <class F>
 inline auto dispatch_mode(int mode, F&& f) {
@@ -233,33 +241,73 @@ __device__ __forceinline__ float dot_mode_scalar(int mode, int lo, int hi, FA a,
 __device__ __forceinline__ int tile_row(int r) { return 4 * (lane_id() >> 4) + r; }
 __device__ __forceinline__ int tile_col() { return lane_id() & 15; }
 
+__device__ __forceinline__ float4 add4(const float4& a, const float4& b) {
+  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+__device__ __forceinline__ float4 sub4(const float4& a, const float4& b) {
+  return make_float4(a.x - b.x, a.y - b.y, a.z - b.z, a.w - b.w);
+}
+__device__ __forceinline__ float4 mul4(const float4& a, const float4& b) {
+  return make_float4(a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w);
+}
+__device__ __forceinline__ float4 san4(const float4& a, float c) {
+  return make_float4(sanitize(a.x, c), sanitize(a.y, c), sanitize(a.z, c), sanitize(a.w, c));
+}
+__device__ __forceinline__ float4 expnp4(const float4& a) {
+  return make_float4(exp_nonpos(a.x), exp_nonpos(a.y), exp_nonpos(a.z), exp_nonpos(a.w));
+}
+
+// ---- fragment-blocked tiles --------------------------------------------------------------
+// An R x C tile in "fragment" layout is stored as 16x16 blocks in row-major block order
+// (C/16 blocks per block row); inside a block the float4 of lane l = r + 16 g holds
+// M[16 bi + r][16 bj + 4 g .. 4 g + 3].  A wave moves a block with one coalesced 1 KB float4
+// access, and lane l's float4 is exactly its operand for one 16-wide k block of mma16 with
+// rows = M rows and k = M columns (A operand), or columns = M rows and k = M columns
+// (B operand of M^T).  The accumulator of an MFMA tile P (lane l holds P[4 g + e][l % 16])
+// is therefore block (bj, bi) of P^T in fragment layout, stored without any shuffle.
+__device__ __forceinline__ int frag_blk(int bi, int bj, int C) { return (bi * (C >> 4) + bj) << 8; }
+__device__ __forceinline__ int frag_off(int i, int j, int C) {
+  return frag_blk(i >> 4, j >> 4, C) + (((i & 15) + ((j & 15) >> 2) * 16) << 2) + (j & 3);
+}
+
+// dst[m - m0][n] (row stride LD) = M[m][n] for m in [m0, m0 + nm), n in [0, NR), read from
+// src = M^T (NR x NC) in fragment layout.  nm and m0 are multiples of 16.
+template <int LD>
+__device__ __forceinline__ void load_fragT(float* dst, const float* __restrict__ src, int NR, int NC,
+                                           int m0, int nm, int tid, int nt) {
+  const int nbm = nm >> 4, nbc = NC >> 4, total = (NR >> 4) * nbm * 64;
+  for (int f = tid; f < total; f += nt) {
+    const int lane = f & 63, blk = f >> 6, bn = blk / nbm, bm = (m0 >> 4) + blk % nbm;
+    const float4 x = ld4(src + ((bn * nbc + bm) << 8) + 4 * lane);
+    const int n = 16 * bn + (lane & 15), m = 16 * bm + 4 * (lane >> 4) - m0;
+    dst[(m + 0) * LD + n] = x.x;
+    dst[(m + 1) * LD + n] = x.y;
+    dst[(m + 2) * LD + n] = x.z;
+    dst[(m + 3) * LD + n] = x.w;
+  }
+}
+
 // In-chunk cumulative sum of g over the T rows of a (T x D) tile, into LDS sG (ld = LD).
-// Column d is owned by NSEG threads, each summing a contiguous run of rows, followed by an
-// offset pass.  Same code in every kernel, so every kernel sees bit-identical gc.
+// Thread t owns float4 column t % (D/4) over a run of RUN consecutive rows: it sums its run,
+// then adds the totals of the runs above it in order.  Same code in every kernel, so every
+// kernel sees bit-identical gc.
 template <int D, int LD, int NTHREADS>
 __device__ __forceinline__ void chunk_cumsum(const float* __restrict__ g, float* sG) {
-  constexpr int NSEG = NTHREADS / D;          // segments per column
-  constexpr int RUN = T / NSEG;               // rows per segment
-  static_assert(NTHREADS % D == 0 && T % NSEG == 0, "cumsum split");
-  const int t = threadIdx.x, d = t % D, s = t / D;
-  float acc = 0.f;
-#pragma unroll 4
-  for (int i = 0; i < RUN; ++i) {
-    const int row = s * RUN + i;
-    acc += g[row * D + d];
-    sG[row * LD + d] = acc;
-  }
+  constexpr int NQ = D / 4, NSEG = NTHREADS / NQ, RUN = T / NSEG;
+  static_assert(NTHREADS % NQ == 0 && T % NSEG == 0 && RUN >= 1, "cumsum split");
+  const int t = threadIdx.x, d = 4 * (t % NQ), s = t / NQ;
+  float4 x[RUN];
+#pragma unroll
+  for (int i = 0; i < RUN; ++i) x[i] = ld4(g + (s * RUN + i) * D + d);
+#pragma unroll
+  for (int i = 1; i < RUN; ++i) x[i] = add4(x[i - 1], x[i]);
+  st4(sG + (s * RUN + RUN - 1) * LD + d, x[RUN - 1]);
   __syncthreads();
-  // offset pass: segment s adds the totals of segments 0..s-1 (sequential order)
-  float off = 0.f;
-  for (int s2 = 0; s2 < s; ++s2) off += sG[(s2 * RUN + RUN - 1) * LD + d];
+  float4 off = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s2 = 0; s2 < s; ++s2) off = add4(off, ld4(sG + (s2 * RUN + RUN - 1) * LD + d));
   __syncthreads();
-  if (s > 0) {
-    for (int i = 0; i < RUN; ++i) {
-      const int row = s * RUN + i;
-      sG[row * LD + d] += off;
-    }
-  }
+#pragma unroll
+  for (int i = 0; i < RUN; ++i) st4(sG + (s * RUN + i) * LD + d, add4(off, x[i]));
   __syncthreads();
 }
 

@@ -1,12 +1,18 @@
-// Forward kernels of the GDN-2 operator on gfx950.
+// Forward chunk-parallel kernels of the GDN-2 operator on gfx950.
 //
-//   wy_fwd_kernel   one workgroup per chunk (B*H*nc of them): in-chunk cumulative decay gc,
-//                   gated scores Aqk / Akk (two-level block-local rescaling, BTL or lean
-//                   diagonal), unit-lower-triangular inverse A = (I + (1-eps) Akk)^-1 by leaf
-//                   forward substitution + block doubling in LDS, then Wp = A (b*k*e^gc) and
-//                   U = A (w*v) on MFMA, plus the gated Kg, Qg and gamma = gc[T-1].
+//   wy_fwd_kernel   one workgroup (8 waves) per chunk: in-chunk cumulative decay gc, gated
+//                   Kg / Qg, gated scores Aqk / Akk (two-level block-local rescaling, BTL or
+//                   lean diagonal) on MFMA with the rescaling legs applied to the operands as
+//                   they are loaded, unit-lower-triangular inverse A = (I + (1-eps) Akk)^-1 by
+//                   leaf forward substitution in registers + block doubling (MFMA for blocks
+//                   of 16 and up), then Wp = A (b k e^gc) and U = A (w v) on MFMA.
 //                   Semantics: fwd/scores.py:42-87, fwd/solve.py:9-48, fwd/cd_slim.py:14-21.
+//   out_fwd_kernel  one workgroup per chunk after the state scan:
+//                   o = san(s Qg h_pre + Aqk v_new)                   (fwd/cd_slim.py:24-27)
 //   (the forward state scan is in gdn2_scan.hip)
+//
+// Every tile the scans read is written in fragment layout (gdn2_common.hpp), so the scans
+// load each operand block with one coalesced float4 access per lane.
 #include "gdn2_kernels.hpp"
 
 namespace gdn2 {
@@ -15,23 +21,76 @@ namespace gdn2 {
 // WY build
 // ------------------------------------------------------------------------------------
 template <int D>
-struct WyFwdLayout {
+struct WyLayout {
   static constexpr int LD = D + 4, LT = T + 4;
-  static constexpr int R0 = T * LD;          // gc, later w*v
-  static constexpr int R1 = 3 * 32 * LD;     // piece staging, later b*k*e^gc, merge temp
-  static constexpr int OFF_G = 0, OFF_ST = R0, OFF_S = R0 + R1;
-  static constexpr int OFF_K = OFF_S + T * LT, OFF_I = OFF_K + T * LT;
+  // gc | b*k (later X = b*k*e^gc) | w*v | S (scores, then merge temp, then transposes) | Akk | inverse
+  static constexpr int OFF_G = 0, OFF_BK = T * LD, OFF_Y = 2 * T * LD;
+  static constexpr int OFF_S = 3 * T * LD, OFF_K = OFF_S + T * LT, OFF_I = OFF_K + T * LT;
   static constexpr int TOTAL = OFF_I + T * LT;
-  static_assert(R1 >= T * LD && R1 >= T * LT, "staging region too small");
+  static_assert(T * LT >= 8 * 16 * 20, "transpose scratch must fit in S");
 };
+
+// One 16x16 score tile of a piece: acc += sum_d (src[i][d] ra(i,d)) (k[j][d] cb(j,d)), where i
+// (j) is the A row (B column) of the calling lane.  Legs (fwd/scores.py:42-75):
+//   KIND 0 (off-diagonal, anchor a): ra = e^{min(gc_i - gc_a, 0)}, cb = e^{min(gc_a - gc_j, 0)}
+//   KIND 1 (BTL diagonal block [s0, s1)): r = gc_s0, half = (gc_s0 - gc_{s1-1}) / 2,
+//          ra = e^{(gc_i - r) + half}, cb = e^{(r - gc_j) - half}
+template <int D, int LD, int DOT, int KIND>
+__device__ __forceinline__ void score_tile(f4& acc, const float* src, int sld, const float* __restrict__ kk,
+                                           const float* sG, const Piece& pc, int i, int j) {
+  const int g = lane_id() >> 4;
+  const float* gi = sG + i * LD;
+  const float* gj = sG + j * LD;
+  const float* ga = sG + (KIND == 0 ? pc.anchor : pc.s0) * LD;
+  const float* gz = sG + (KIND == 0 ? pc.anchor : pc.s1 - 1) * LD;
+  const float* si = src + i * sld;
+  const float* kj = kk + j * D;
+#pragma unroll 2
+  for (int kb = 0; kb < D / 16; ++kb) {
+    const int d = 16 * kb + 4 * g;
+    const float4 vi = ld4(gi + d), vj = ld4(gj + d), va = ld4(ga + d);
+    float4 ra, cb;
+    if constexpr (KIND == 0) {
+      ra = expnp4(sub4(vi, va));
+      cb = expnp4(sub4(va, vj));
+    } else {
+      const float4 h = scale4(sub4(va, ld4(gz + d)), 0.5f);
+      ra = make_float4(expf((vi.x - va.x) + h.x), expf((vi.y - va.y) + h.y), expf((vi.z - va.z) + h.z),
+                       expf((vi.w - va.w) + h.w));
+      cb = make_float4(expf((va.x - vj.x) - h.x), expf((va.y - vj.y) - h.y), expf((va.z - vj.z) - h.z),
+                       expf((va.w - vj.w) - h.w));
+    }
+    mma16<DOT>(acc, mul4(ld4(si + d), ra), mul4(ld4(kj + d), cb));
+  }
+  drain(acc);
+}
+
+// Leaf inverses of the mb x mb diagonal blocks of (I + Se) by forward substitution
+// (fwd/solve.py:9-18): thread (leaf, c) keeps column c of its leaf in registers.
+template <int MB, int LT>
+__device__ __forceinline__ void leaf_solve(const float* sSe, float* sI, int tid) {
+  const int base = (tid / MB) * MB, c = tid % MB;
+  float x[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) {
+    const float* srow = sSe + (base + i) * LT + base;
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < i; ++j) s = fmaf(srow[j], x[j], s);
+    x[i] = (i == c ? 1.f : 0.f) - s;
+  }
+#pragma unroll
+  for (int i = 0; i < MB; ++i) sI[(base + i) * LT + base + c] = x[i];
+}
 
 template <int D, int DOT>
 __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
-  using Lay = WyFwdLayout<D>;
-  constexpr int LD = Lay::LD, LT = Lay::LT, NT = 512, NW = NT / WAVE;
-  __shared__ float smem[Lay::TOTAL];
+  using Lay = WyLayout<D>;
+  constexpr int LD = Lay::LD, LT = Lay::LT, NT = 512, NW = NT / WAVE, NKB = D / 16;
+  __shared__ __attribute__((aligned(16))) float smem[Lay::TOTAL];
   float* sG = smem + Lay::OFF_G;
-  float* sSt = smem + Lay::OFF_ST;
+  float* sBK = smem + Lay::OFF_BK;
+  float* sY = smem + Lay::OFF_Y;
   float* sS = smem + Lay::OFF_S;
   float* sK = smem + Lay::OFF_K;
   float* sI = smem + Lay::OFF_I;
@@ -45,178 +104,284 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
   const float* __restrict__ b = a.b + tb;
   const float* __restrict__ w = a.w + tb;
   const float* __restrict__ v = a.v + tb;
-  const int tid = threadIdx.x, wv = wave_id();
+  const int tid = threadIdx.x, wv = wave_id(), l = lane_id(), r = l & 15, g = l >> 4;
 
   // 1. gc = cumsum(g) inside the chunk
   chunk_cumsum<D, LD, NT>(a.g + tb, sG);
 
-  // 2. gated k / q and gamma (cd_slim.py:17-21): kg = san(k e^{min(gl-gc,0)}), qg = san(q e^{min(gc,0)});
-  //    each thread does 4 consecutive rows of one column (row-major and transposed stores)
-  for (int e = tid; e < (T / 4) * D; e += NT) {
-    const int d = e % D, i0 = 4 * (e / D);
-    const float gl = sG[(T - 1) * LD + d];
-    float kv[4], qv[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = i0 + r;
-      const float gi = sG[i * LD + d];
-      kv[r] = sanitize(k[i * D + d] * exp_nonpos(gl - gi), clip);
-      qv[r] = sanitize(q[i * D + d] * exp_nonpos(gi), clip);
-      if (a.kg) a.kg[tb + i * D + d] = kv[r];
-      if (a.qg) a.qg[tb + i * D + d] = qv[r];
+  // 2a. row fragments (cd_slim.py:17-21): FA(Kg) with kg = san(k e^{min(gl-gc,0)}),
+  //     FA(Qg) with qg = san(q e^{min(gc,0)}); b*k and w*v into LDS.  Item f is lane f%64 of
+  //     block f/64, so the fragment stores are contiguous.
+  for (int f = tid; f < T * D / 4; f += NT) {
+    const int blk = f >> 6, ln = f & 63;
+    const int i = 16 * (blk / NKB) + (ln & 15), d = 16 * (blk % NKB) + 4 * (ln >> 4);
+    const float4 gc = ld4(sG + i * LD + d);
+    const float4 kv = ld4(k + i * D + d);
+    st4(sBK + i * LD + d, mul4(ld4(b + i * D + d), kv));
+    st4(sY + i * LD + d, mul4(ld4(w + i * D + d), ld4(v + i * D + d)));
+    if (a.kg_f || a.kg) {
+      const float4 kg = san4(mul4(kv, expnp4(sub4(ld4(sG + (T - 1) * LD + d), gc))), clip);
+      if (a.kg_f) st4(a.kg_f + tb + 4 * f, kg);
+      if (a.kg) st4(a.kg + tb + i * D + d, kg);
     }
-    if (a.kgT) st4(a.kgT + tb + (size_t)d * T + i0, make_float4(kv[0], kv[1], kv[2], kv[3]));
-    if (a.qgT) st4(a.qgT + tb + (size_t)d * T + i0, make_float4(qv[0], qv[1], qv[2], qv[3]));
+    if (a.qg_f || a.qg) {
+      const float4 qg = san4(mul4(ld4(q + i * D + d), expnp4(gc)), clip);
+      if (a.qg_f) st4(a.qg_f + tb + 4 * f, qg);
+      if (a.qg) st4(a.qg + tb + i * D + d, qg);
+    }
   }
-  if (tid < D) a.gl[(size_t)chunk * D + tid] = sG[(T - 1) * LD + tid];
-
-  // 3. scores, piece by piece (scores.py:42-75)
-  for (int pi = 0; pi < cf.pieces.n; ++pi) {
-    const Piece pc = cf.pieces.p[pi];
-    const int P = pc.P;
-    const bool lean = (pc.kind == 1 && cf.diag == DIAG_LEAN);
-    float* sQs = sSt;
-    float* sBs = sSt + 32 * LD;
-    float* sKs = sSt + 64 * LD;
-    for (int e = tid; e < P * D; e += NT) {
-      const int i = e / D, d = e % D;
-      const int row = pc.row0 + i, col = pc.col0 + i;
-      const float ra = lean ? 1.f : piece_row_leg(pc, sG, LD, row, d);
-      const float cb = lean ? 1.f : piece_col_leg(pc, sG, LD, col, d);
-      sQs[i * LD + d] = q[row * D + d] * ra;
-      sBs[i * LD + d] = (b[row * D + d] * k[row * D + d]) * ra;
-      sKs[i * LD + d] = k[col * D + d] * cb;
-    }
-    __syncthreads();
-    if (!lean) {
-      const int nt1 = P / 16, ntm = nt1 * nt1;
-      for (int t = wv; t < 2 * ntm; t += NW) {
-        const int mat = t / ntm, ti = (t % ntm) / nt1, tj = t % nt1;
-        f4 acc = {0.f, 0.f, 0.f, 0.f};
-        mma_tile<DOT>(acc, rm(mat == 0 ? sQs : sBs, LD).shift(ti * 16, 0),
-                 tr(sKs, LD).shift(0, tj * 16), D);
-        float* out = mat == 0 ? sS : sK;
+  // 2b. column fragments FA(Kg^T), FA(Qg^T) (D x T): lane ln of block (key block, token block)
+  //     holds 4 consecutive tokens of one key channel.
+  if (a.kgT_f || a.qgT_f) {
+    for (int f = tid; f < T * D / 4; f += NT) {
+      const int blk = f >> 6, ln = f & 63;
+      const int d = 16 * (blk >> 2) + (ln & 15), i0 = 16 * (blk & 3) + 4 * (ln >> 4);
+      const float gl = sG[(T - 1) * LD + d];
+      float kt[4], qt[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int i = pc.row0 + ti * 16 + tile_row(r), j = pc.col0 + tj * 16 + tile_col();
-          out[i * LT + j] = mat == 0 ? cf.scale * acc[r] : acc[r];
-        }
+      for (int e = 0; e < 4; ++e) {
+        const int i = i0 + e;
+        const float gi = sG[i * LD + d];
+        kt[e] = sanitize(k[i * D + d] * exp_nonpos(gl - gi), clip);
+        qt[e] = sanitize(q[i * D + d] * exp_nonpos(gi), clip);
       }
-    } else {
+      if (a.kgT_f) st4(a.kgT_f + tb + 4 * f, make_float4(kt[0], kt[1], kt[2], kt[3]));
+      if (a.qgT_f) st4(a.qgT_f + tb + 4 * f, make_float4(qt[0], qt[1], qt[2], qt[3]));
+    }
+  }
+  if (a.gl && tid < D) a.gl[(size_t)chunk * D + tid] = sG[(T - 1) * LD + tid];
+  __syncthreads();
+
+  // 3. scores, all pieces at once (scores.py:42-75): Aqk = s (q ra)(k cb)^T, Akk = (bk ra)(k cb)^T
+  {
+    const int np = cf.pieces.n, P = cf.pieces.p[0].P, nb = P / 16, tpm = nb * nb, tpp = 2 * tpm;
+    const bool lean = cf.diag == DIAG_LEAN;
+    for (int t = wv; t < np * tpp; t += NW) {
+      const Piece pc = cf.pieces.p[t / tpp];
+      if (pc.kind == 1 && lean) continue;
+      const int rem = t % tpp, mat = rem / tpm, ti = (rem % tpm) / nb, tj = rem % nb;
+      const int i = pc.row0 + 16 * ti + r, j = pc.col0 + 16 * tj + r;
+      f4 acc = {0.f, 0.f, 0.f, 0.f};
+      if (mat == 0) {
+        if (pc.kind == 0) score_tile<D, LD, DOT, 0>(acc, q, D, k, sG, pc, i, j);
+        else score_tile<D, LD, DOT, 1>(acc, q, D, k, sG, pc, i, j);
+      } else {
+        if (pc.kind == 0) score_tile<D, LD, DOT, 0>(acc, sBK, LD, k, sG, pc, i, j);
+        else score_tile<D, LD, DOT, 1>(acc, sBK, LD, k, sG, pc, i, j);
+      }
+      float* out = mat ? sK : sS;
+      const float mul = mat ? 1.f : cf.scale;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[(pc.row0 + 16 * ti + 4 * g + e) * LT + pc.col0 + 16 * tj + r] = mul * acc[e];
+    }
+    if (lean) {
       // lean diagonal (scores.py:34-39): exact exp(clip(gc_i - gc_j, +-diff_clip)) per element
       const float dc = cf.diff_clip;
-      for (int e = tid; e < P * P; e += NT) {
-        const int i = e / P, j = e % P;
-        const int row = pc.row0 + i, col = pc.col0 + j;
-        float sq = 0.f, sk = 0.f;
-        for (int d = 0; d < D; ++d) {
-          const float E = expf(fminf(fmaxf(sG[row * LD + d] - sG[col * LD + d], -dc), dc));
-          const float kj = sKs[j * LD + d];
-          sq += (sQs[i * LD + d] * E) * kj;
-          sk += (sBs[i * LD + d] * E) * kj;
+      for (int pi = 0; pi < np; ++pi) {
+        const Piece pc = cf.pieces.p[pi];
+        if (pc.kind != 1) continue;
+        for (int e = tid; e < P * P; e += NT) {
+          const int row = pc.row0 + e / P, col = pc.col0 + e % P;
+          float sq = 0.f, sk = 0.f;
+          for (int d = 0; d < D; ++d) {
+            const float E = expf(fminf(fmaxf(sG[row * LD + d] - sG[col * LD + d], -dc), dc));
+            const float kj = k[col * D + d];
+            sq += (q[row * D + d] * E) * kj;
+            sk += (sBK[row * LD + d] * E) * kj;
+          }
+          sS[row * LT + col] = cf.scale * sq;
+          sK[row * LT + col] = sk;
         }
-        sS[row * LT + col] = cf.scale * sq;
-        sK[row * LT + col] = sk;
       }
     }
-    __syncthreads();
   }
+  __syncthreads();
 
   // 4. masks + sanitize (scores.py:84-87); Se = (1-eps) Akk for the solve (solve.py:25)
-  for (int e = tid; e < T * (T / 4); e += NT) {
-    const int j = e % T, i0 = 4 * (e / T);
-    float av[4];
+  for (int f = tid; f < T * T / 4; f += NT) {
+    const int i = f / (T / 4), j = 4 * (f % (T / 4));
+    const float4 s4v = ld4(sS + i * LT + j), k4v = ld4(sK + i * LT + j);
+    const float sv[4] = {s4v.x, s4v.y, s4v.z, s4v.w}, kv[4] = {k4v.x, k4v.y, k4v.z, k4v.w};
+    float aq[4], ak[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = i0 + r;
-      const float aq = j <= i ? sanitize(sS[i * LT + j], clip) : 0.f;
-      const float ak = j < i ? sanitize(sK[i * LT + j], clip) : 0.f;
-      av[r] = aq;
-      sS[i * LT + j] = aq;
-      if (a.aqk) a.aqk[sb + i * T + j] = aq;
-      if (a.akk) a.akk[sb + i * T + j] = ak;
-      sK[i * LT + j] = ak * cf.ome;
-      sI[i * LT + j] = 0.f;
+    for (int e = 0; e < 4; ++e) {
+      aq[e] = j + e <= i ? sanitize(sv[e], clip) : 0.f;
+      ak[e] = j + e < i ? sanitize(kv[e], clip) : 0.f;
     }
-    if (a.aqkT) st4(a.aqkT + sb + (size_t)j * T + i0, make_float4(av[0], av[1], av[2], av[3]));
+    const float4 aq4 = make_float4(aq[0], aq[1], aq[2], aq[3]), ak4 = make_float4(ak[0], ak[1], ak[2], ak[3]);
+    st4(sS + i * LT + j, aq4);
+    st4(sK + i * LT + j, scale4(ak4, cf.ome));
+    st4(sI + i * LT + j, make_float4(0.f, 0.f, 0.f, 0.f));
+    if (a.aqk) st4(a.aqk + sb + i * T + j, aq4);
+    if (a.akk) st4(a.akk + sb + i * T + j, ak4);
   }
   __syncthreads();
 
-  // 5. inverse of (I + Se): leaves by forward substitution (solve.py:9-18) ...
-  const int mb = cf.mb;
+  // 5a. FA(Aqk), FA(Aqk^T); X = b k e^{min(gc,0)} in place (cd_slim.py:17); leaf inverses
+  for (int f = tid; f < T * T / 4; f += NT) {
+    const int blk = f >> 6, ln = f & 63, bi = blk >> 2, bj = blk & 3, rr = ln & 15, gg = ln >> 4;
+    if (a.aqk_f) st4(a.aqk_f + sb + 4 * f, ld4(sS + (16 * bi + rr) * LT + 16 * bj + 4 * gg));
+    if (a.aqkT_f) {
+      const float* p = sS + (16 * bj + 4 * gg) * LT + 16 * bi + rr;
+      st4(a.aqkT_f + sb + 4 * f, make_float4(p[0], p[LT], p[2 * LT], p[3 * LT]));
+    }
+  }
+  for (int f = tid; f < T * D / 4; f += NT) {
+    const int i = f / (D / 4), d = 4 * (f % (D / 4));
+    st4(sBK + i * LD + d, mul4(ld4(sBK + i * LD + d), expnp4(ld4(sG + i * LD + d))));
+  }
   if (tid < T) {
-    const int base = (tid / mb) * mb, c = tid % mb;
-    for (int i = 0; i < mb; ++i) {
-      float s = 0.f;
-      for (int j = 0; j < i; ++j) s = fmaf(sK[(base + i) * LT + base + j], sI[(base + j) * LT + base + c], s);
-      sI[(base + i) * LT + base + c] = (i == c ? 1.f : 0.f) - s;
+    switch (cf.mb) {
+      case 1: leaf_solve<1, LT>(sK, sI, tid); break;
+      case 2: leaf_solve<2, LT>(sK, sI, tid); break;
+      case 4: leaf_solve<4, LT>(sK, sI, tid); break;
+      case 8: leaf_solve<8, LT>(sK, sI, tid); break;
+      case 16: leaf_solve<16, LT>(sK, sI, tid); break;
+      default: {
+        // mb = 32 / 64: column c of the leaf in LDS (same arithmetic order as above)
+        const int mb = cf.mb, base = (tid / mb) * mb, c = tid % mb;
+        for (int i = 0; i < mb; ++i) {
+          float s = 0.f;
+          for (int j = 0; j < i; ++j) s = fmaf(sK[(base + i) * LT + base + j], sI[(base + j) * LT + base + c], s);
+          sI[(base + i) * LT + base + c] = (i == c ? 1.f : 0.f) - s;
+        }
+      }
     }
-  }
-  __syncthreads();
-  // ... then block doubling X <- [[top, 0], [-bot (S_l top), bot]] (solve.py:30-43)
-  float* sM = sSt;
-  for (int bb = mb; bb < T; bb *= 2) {
-    const int nm = T / (2 * bb), per = bb * bb;
-    for (int e = tid; e < nm * per; e += NT) {
-      const int m = e / per, i = (e % per) / bb, j = e % bb, i0 = m * 2 * bb;
-      const float* srow = sK + (i0 + bb + i) * LT + i0;
-      const float* tcol = sI + i0 * LT + i0 + j;
-      sM[(i0 + bb + i) * LT + i0 + j] = dot_mode_scalar(
-          cf.solve_mode, j, bb, [&](int kk) { return srow[kk]; }, [&](int kk) { return tcol[kk * LT]; });
-    }
-    __syncthreads();
-    for (int e = tid; e < nm * per; e += NT) {
-      const int m = e / per, i = (e % per) / bb, j = e % bb, i0 = m * 2 * bb;
-      const float* brow = sI + (i0 + bb + i) * LT + i0 + bb;
-      const float* mcol = sM + (i0 + bb) * LT + i0 + j;
-      sI[(i0 + bb + i) * LT + i0 + j] = -dot_mode_scalar(
-          cf.solve_mode, 0, i + 1, [&](int kk) { return brow[kk]; }, [&](int kk) { return mcol[kk * LT]; });
-    }
-    __syncthreads();
-  }
-  for (int e = tid; e < T * T; e += NT) {
-    const int i = e / T, j = e % T;
-    const float x = sanitize(sI[i * LT + j], clip);
-    sI[i * LT + j] = x;
-    if (a.A) a.A[sb + e] = x;
   }
   __syncthreads();
 
-  // 6. WY operands: b*k*e^{min(gc,0)} and w*v (cd_slim.py:17-18)
-  float* sX = sSt;
-  float* sY = sG;
-  for (int e = tid; e < T * D; e += NT) {
-    const int i = e / D, d = e % D;
-    sX[i * LD + d] = (b[e] * k[e]) * exp_nonpos(sG[i * LD + d]);
+  // 5b. block doubling X <- [[X11, 0], [-X22 (S21 X11), X22]] (solve.py:30-43), products in the
+  //     solve dot mode: MFMA tiles for blocks of 16 and up, scalar below.
+  float* sM = sS;
+  for (int bb = cf.mb; bb < T; bb *= 2) {
+    const int nm = T / (2 * bb);
+    if (bb < 16) {
+      const int per = bb * bb;
+      for (int e = tid; e < nm * per; e += NT) {
+        const int m = e / per, i = (e % per) / bb, j = e % bb, i0 = m * 2 * bb;
+        const float* srow = sK + (i0 + bb + i) * LT + i0;
+        const float* tcol = sI + i0 * LT + i0 + j;
+        sM[(i0 + bb + i) * LT + i0 + j] = dot_mode_scalar(
+            cf.solve_mode, j, bb, [&](int kk) { return srow[kk]; }, [&](int kk) { return tcol[kk * LT]; });
+      }
+      __syncthreads();
+      for (int e = tid; e < nm * per; e += NT) {
+        const int m = e / per, i = (e % per) / bb, j = e % bb, i0 = m * 2 * bb;
+        const float* brow = sI + (i0 + bb + i) * LT + i0 + bb;
+        const float* mcol = sM + (i0 + bb) * LT + i0 + j;
+        sI[(i0 + bb + i) * LT + i0 + j] = -dot_mode_scalar(
+            cf.solve_mode, 0, i + 1, [&](int kk) { return brow[kk]; }, [&](int kk) { return mcol[kk * LT]; });
+      }
+      __syncthreads();
+    } else {
+      const int nt = bb / 16, tpm = nt * nt;
+      for (int t = wv; t < nm * tpm; t += NW) {
+        const int m = t / tpm, ti = (t % tpm) / nt, tj = t % nt, i0 = 2 * bb * m;
+        f4 acc = {0.f, 0.f, 0.f, 0.f};
+        mma_tile_rt(cf.solve_mode, acc, rm(sK, LT).shift(i0 + bb + 16 * ti, i0), rm(sI, LT).shift(i0, i0 + 16 * tj), bb);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sM[(i0 + bb + 16 * ti + 4 * g + e) * LT + i0 + 16 * tj + r] = acc[e];
+      }
+      __syncthreads();
+      for (int t = wv; t < nm * tpm; t += NW) {
+        const int m = t / tpm, ti = (t % tpm) / nt, tj = t % nt, i0 = 2 * bb * m;
+        f4 acc = {0.f, 0.f, 0.f, 0.f};
+        mma_tile_rt(cf.solve_mode, acc, rm(sI, LT).shift(i0 + bb + 16 * ti, i0 + bb),
+                    rm(sM, LT).shift(i0 + bb, i0 + 16 * tj), bb);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sI[(i0 + bb + 16 * ti + 4 * g + e) * LT + i0 + 16 * tj + r] = -acc[e];
+      }
+      __syncthreads();
+    }
   }
-  __syncthreads();
-  for (int e = tid; e < T * D; e += NT) {
-    const int i = e / D, d = e % D;
-    sY[i * LD + d] = w[e] * v[e];
+  // 5c. A = san(inverse)
+  for (int f = tid; f < T * T / 4; f += NT) {
+    const int i = f / (T / 4), j = 4 * (f % (T / 4));
+    const float4 x = san4(ld4(sI + i * LT + j), clip);
+    st4(sI + i * LT + j, x);
+    if (a.A) st4(a.A + sb + i * T + j, x);
   }
   __syncthreads();
 
-  // 7. Wp = san(A kb), U = san(A wv); A is unit lower triangular so row tile ti only needs
-  //    the first (ti+1)*16 columns of A.
+  // 6. Wp = san(A X), U = san(A (w v)); A is unit lower triangular, so row tile ti only needs
+  //    k blocks 0..ti.  Lane l's accumulator is lane l of FA(P^T) block (tj, ti); FA(Wp) goes
+  //    through a per-wave 16x16 transpose in LDS.
   {
+    float* sW = sS + wv * (16 * 20);
     constexpr int NTJ = D / 16, NTM = (T / 16) * NTJ;
+    const bool want_w = a.wp_f || a.wpT_f || a.wp, want_u = a.uT_f || a.u;
     for (int t = wv; t < 2 * NTM; t += NW) {
       const int mat = t / NTM, ti = (t % NTM) / NTJ, tj = t % NTJ;
+      if (mat ? !want_u : !want_w) continue;
+      const float* X = mat ? sY : sBK;
       f4 acc = {0.f, 0.f, 0.f, 0.f};
-      mma_tile<DOT>(acc, rm(sI, LT).shift(ti * 16, 0), rm(mat ? sY : sX, LD).shift(0, tj * 16),
-               (ti + 1) * 16);
-      float* out = mat ? a.u : a.wp;
-      float* outT = mat ? a.uT : a.wpT;
-      const float4 x = make_float4(sanitize(acc[0], clip), sanitize(acc[1], clip), sanitize(acc[2], clip),
-                                   sanitize(acc[3], clip));
-      const int i0 = ti * 16 + tile_row(0), d = tj * 16 + tile_col();
-      if (out) {
-        out[tb + (i0 + 0) * D + d] = x.x;
-        out[tb + (i0 + 1) * D + d] = x.y;
-        out[tb + (i0 + 2) * D + d] = x.z;
-        out[tb + (i0 + 3) * D + d] = x.w;
+      for (int kb = 0; kb <= ti; ++kb) {
+        const float4 av = ld4(sI + (16 * ti + r) * LT + 16 * kb + 4 * g);
+        const float* xb = X + (16 * kb + 4 * g) * LD + 16 * tj + r;
+        mma16<DOT>(acc, av, make_float4(xb[0], xb[LD], xb[2 * LD], xb[3 * LD]));
       }
-      if (outT) st4(outT + tb + (size_t)d * T + i0, x);     // the 4 rows of a lane are consecutive
+      drain(acc);
+      const float4 p = san4(f4_to_float4(acc), clip);     // p.e = P[16 ti + 4 g + e][16 tj + r]
+      float* rowmaj = mat ? a.u : a.wp;
+      if (rowmaj) {
+        float* o = rowmaj + tb + (size_t)(16 * ti + 4 * g) * D + 16 * tj + r;
+        o[0] = p.x; o[D] = p.y; o[2 * D] = p.z; o[3 * D] = p.w;
+      }
+      float* fT = mat ? a.uT_f : a.wpT_f;
+      if (fT) st4(fT + tb + frag_blk(tj, ti, T) + 4 * l, p);
+      if (mat == 0 && a.wp_f) {
+        sW[(4 * g + 0) * 20 + r] = p.x;
+        sW[(4 * g + 1) * 20 + r] = p.y;
+        sW[(4 * g + 2) * 20 + r] = p.z;
+        sW[(4 * g + 3) * 20 + r] = p.w;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        st4(a.wp_f + tb + frag_blk(ti, tj, D) + 4 * l, ld4(sW + r * 20 + 4 * g));
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// o = san(s Qg h_pre + Aqk v_new), computed as o^T tiles: o^T = s h_pre^T Qg^T + v_new^T Aqk^T.
+// A operands FA(h_pre^T), FA(v_new^T) come straight from the scan's fragment stores; B
+// operands FA(Qg), FA(Aqk) are staged once per chunk in LDS.  The accumulator of tile
+// (value block cb, token block tq) holds o[16 tq + l%16][16 cb + 4 g .. +3]: one float4 store.
+// ------------------------------------------------------------------------------------
+template <int D, int DOT>
+__global__ __launch_bounds__(256) void out_fwd_kernel(OutFwdArgs a) {
+  constexpr int NW = 4, NKB = D / 16;
+  __shared__ float4 sQ[T * D / 4];
+  __shared__ float4 sA[T * T / 4];
+  const int chunk = blockIdx.x, tid = threadIdx.x, w = wave_id(), l = lane_id(), r = l & 15, g = l >> 4;
+  const size_t tb = (size_t)chunk * T * D, sb = (size_t)chunk * T * T, hb = (size_t)chunk * D * D;
+  const float4* q4 = reinterpret_cast<const float4*>(a.qg_f + tb);
+  const float4* a4 = reinterpret_cast<const float4*>(a.aqk_f + sb);
+  for (int f = tid; f < T * D / 4; f += NW * WAVE) sQ[f] = q4[f];
+  for (int f = tid; f < T * T / 4; f += NW * WAVE) sA[f] = a4[f];
+  __syncthreads();
+  const float scale = a.cfg.scale, clip = a.cfg.clip;
+  for (int cb = w; cb < D / 16; cb += NW) {
+    float4 hT[NKB], vT[4];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) hT[kb] = ld4(a.h_pre_f + hb + frag_blk(cb, kb, D) + 4 * l);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) vT[u] = ld4(a.v_new_f + tb + frag_blk(cb, u, T) + 4 * l);
+#pragma unroll
+    for (int tq = 0; tq < 4; ++tq) {
+      f4 acc1 = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) mma16<DOT>(acc1, hT[kb], sQ[(tq * NKB + kb) * WAVE + l]);
+#pragma unroll
+      for (int u = 0; u <= tq; ++u) mma16<DOT>(acc2, vT[u], sA[(tq * 4 + u) * WAVE + l]);
+      drain(acc1, acc2);
+      const float4 ov = make_float4(sanitize(scale * acc1[0] + acc2[0], clip), sanitize(scale * acc1[1] + acc2[1], clip),
+                                    sanitize(scale * acc1[2] + acc2[2], clip), sanitize(scale * acc1[3] + acc2[3], clip));
+      st4(a.o + tb + (size_t)(16 * tq + r) * D + 16 * cb + 4 * g, ov);
     }
   }
 }
@@ -257,6 +422,16 @@ hipError_t launch_wy_fwd(int D, const WyFwdArgs& a, hipStream_t s) {
     constexpr int M = decltype(m)::value;
     if (D == 128) hipLaunchKernelGGL((wy_fwd_kernel<128, M>), dim3(a.n_chunks), dim3(512), 0, s, a);
     else hipLaunchKernelGGL((wy_fwd_kernel<64, M>), dim3(a.n_chunks), dim3(512), 0, s, a);
+    return 0;
+  });
+  return hipGetLastError();
+}
+
+hipError_t launch_out_fwd(int D, const OutFwdArgs& a, hipStream_t s) {
+  dispatch_mode(a.cfg.dot_mode, [&](auto m) {
+    constexpr int M = decltype(m)::value;
+    if (D == 128) hipLaunchKernelGGL((out_fwd_kernel<128, M>), dim3(a.n_chunks), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((out_fwd_kernel<64, M>), dim3(a.n_chunks), dim3(256), 0, s, a);
     return 0;
   });
   return hipGetLastError();

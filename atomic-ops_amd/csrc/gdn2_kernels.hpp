@@ -25,40 +25,57 @@ struct Cfg {
   PieceList pieces;
 };
 
-// Per-chunk outputs of the WY build.  Row-major tiles are (T x D) / (T x T); the "T"
-// variants are the same tiles transposed, (D x T) / (T x T), written for the scans so that
-// all their A-operands are contiguous float4 loads.  Any pointer may be null (not written).
+// Per-chunk outputs of the WY build.  "_f" outputs are in fragment layout (gdn2_common.hpp):
+//   wp_f FA(Wp) (T x D), wpT_f FA(Wp^T) (D x T), uT_f FA(U^T) (D x T), kg_f FA(Kg) (T x D),
+//   kgT_f FA(Kg^T) (D x T), qg_f FA(Qg) (T x D), qgT_f FA(Qg^T) (D x T), aqk_f FA(Aqk) (T x T),
+//   aqkT_f FA(Aqk^T) (T x T).  A (T x T) and gl (D) are row-major.  The plain row-major
+//   aqk / akk / wp / u / kg / qg are written only for the stage-level entry point.  Any
+//   pointer may be null (not written).
 struct WyFwdArgs {
   const float *q, *k, *v, *w, *b, *g;
-  float *aqk, *aqkT, *A, *wp, *wpT, *u, *uT, *kg, *kgT, *qg, *qgT, *gl;
-  float* akk;          // masked, sanitized Akk (before the (1-eps) factor)
-  int n_chunks;        // B*H*nc
+  float *wp_f, *wpT_f, *uT_f, *kg_f, *kgT_f, *qg_f, *qgT_f, *aqk_f, *aqkT_f;
+  float *A, *gl;
+  float *aqk, *akk, *wp, *u, *kg, *qg;
+  int n_chunks;
   Cfg cfg;
 };
 
+// Forward state scan: reads FA(Wp), FA(Kg^T), FA(U^T), gl; writes per chunk the entering state
+// h_pre as FA(h_pre^T) (D x D) and v_new as FA(v_new^T) (D x T), and the final state hf
+// (row-major D x D).
 struct ScanFwdArgs {
-  const float *wp, *uT, *kgT, *qg, *gl, *aqk, *h0;
-  float *o, *hf, *h_pre, *v_new;   // h_pre / v_new null for a forward-only call
+  const float *wp_f, *kgT_f, *uT_f, *gl, *h0;
+  float *hf, *h_pre_f, *v_new_f;
   int nc, n_bh;
   Cfg cfg;
 };
 
+// Chunk-parallel output: o = san(s Qg h_pre + Aqk v_new), o row-major (T x D per chunk).
+struct OutFwdArgs {
+  const float *qg_f, *aqk_f, *h_pre_f, *v_new_f;
+  float* o;
+  int n_chunks;
+  Cfg cfg;
+};
+
+// Reverse state scan: reads FA(Wp^T), FA(Kg), FA(Qg^T), FA(Aqk^T), gl, dO (row-major); writes
+// dv_new as FA(dv_new^T) (D x T), dh_next as FA(dh_next^T) (D x D), dh0 row-major.
 struct ScanBwdArgs {
-  const float *wpT, *kg, *qgT, *gl, *aqkT, *dout, *dhf;
-  float *dv_new, *dh_next, *dh0;
+  const float *wpT_f, *kg_f, *qgT_f, *gl, *aqkT_f, *dout, *dhf;
+  float *dv_new_f, *dh_next_f, *dh0;
   int nc, n_bh;
   Cfg cfg;
 };
 
 struct BwdStateArgs {
-  const float *dout, *dv_new, *v_new, *h_pre, *dh_next;
+  const float *dout, *dv_new_f, *v_new_f, *h_pre_f, *dh_next_f;
   float *dqg, *dwp, *dkg, *dlast;
   int n_chunks;
   Cfg cfg;
 };
 
 struct BwdWyArgs {
-  const float *q, *k, *v, *w, *b, *g, *A, *aqk, *dout, *v_new, *dv_new;
+  const float *q, *k, *v, *w, *b, *g, *A, *dout, *v_new_f, *dv_new_f;
   const float *dqg, *dwp, *dkg, *dlast;
   float *dq, *dk, *dv, *dw, *db, *dg;
   int n_chunks;
@@ -67,6 +84,7 @@ struct BwdWyArgs {
 
 hipError_t launch_wy_fwd(int D, const WyFwdArgs& a, hipStream_t s);
 hipError_t launch_scan_fwd(int D, const ScanFwdArgs& a, hipStream_t s);
+hipError_t launch_out_fwd(int D, const OutFwdArgs& a, hipStream_t s);
 hipError_t launch_scan_bwd(int D, const ScanBwdArgs& a, hipStream_t s);
 hipError_t launch_bwd_state(int D, const BwdStateArgs& a, hipStream_t s);
 hipError_t launch_bwd_wy(int D, const BwdWyArgs& a, hipStream_t s);

@@ -6,21 +6,23 @@
 // registers for the whole sequence, in the MFMA result layout (lane l holds rows
 // 16w + 4(l/16) + e, e = 0..3, of column l%16).  With the k-permuted operand mapping of
 // mma16 that layout is also the B-operand layout, so the state feeds the next chunk's
-// products without any data movement.
+// products without any data movement, and it is lane l of block (slice, w) of the
+// transposed state in fragment layout, so saving it is one float4 store per lane.
 //
-// Products whose contraction runs over the key dimension (Wp h, Qg h, Kg dh) are split by
-// key rows across waves: each wave multiplies with its own state rows and writes a 16x16
-// partial tile per output row tile to LDS; a fixed-order sum over waves finishes them.
-// Products over the chunk's time axis (Kg^T v_new, Aqk v_new, Qg^T dO, Wp^T dv_new) read
-// v_new / dv_new (and dO) from transposed LDS slices with ds_read_b128.  A-operands stream
-// from global memory as float4 (the WY kernel writes the transposed tiles Kg^T, Wp^T, Qg^T,
-// Aqk^T, U^T for this) and are prefetched one chunk ahead into the second of two register
-// sets; the chunk loop is unrolled by two so the sets never need copying, and all prefetch
-// loads are unconditional so the compiler's vmcnt waits stay exact.  Per chunk: two
-// workgroup barriers.
+// Products whose contraction runs over the key dimension (Wp h, Kg dh) are split by key
+// rows across waves: each wave multiplies with its own state rows and writes a 16x16 partial
+// tile per output row tile to LDS; a fixed-order sum over waves finishes them.  Products
+// over the chunk's time axis (Kg^T v_new, Wp^T dv_new, Aqk^T dO, Qg^T dO) read v_new / dv_new
+// / dO from LDS in B-operand layout.  A-operands stream from global memory as one coalesced
+// float4 per lane and block (fragment layout, written by the WY kernel) and are prefetched
+// one chunk ahead into the second of two register sets; the chunk loop is unrolled by two so
+// the sets never need copying, and all prefetch loads are unconditional so the compiler's
+// vmcnt waits stay exact.  Per chunk: two workgroup barriers.
 //
-// Forward (fwd/cd_slim.py:12-30):  v_new = U - Wp h;  o = san(s Qg h + Aqk v_new);
-//                                  h = san(e^gamma h + Kg^T v_new)
+// The forward scan carries only the chain h -> v_new -> h; the output o, which needs h_pre
+// and v_new but feeds nothing back, is computed chunk-parallel afterwards (gdn2_fwd.hip).
+//
+// Forward (fwd/cd_slim.py:12-30):  v_new = U - Wp h;  h = san(e^gamma h + Kg^T v_new)
 // Reverse (bwd/mega.py:33-36):     dv_new = san(Aqk^T dO + Kg dh);
 //                                  dh = san(Qg^T (s dO) + e^gamma dh - Wp^T dv_new)
 #include "gdn2_kernels.hpp"
@@ -34,130 +36,79 @@ __device__ __forceinline__ int xcd_remap(int nblk) {
   return (nblk % 8) ? b : (b % 8) * (nblk / 8) + b / 8;
 }
 
-constexpr int LVT = T + 4;     // row stride of the transposed v_new slice [16][T]
+constexpr int LVT = T + 4;     // row stride of the transposed dO / dv_new slices [16][T]
 
-template <int D>
 struct FwdOps {
-  float4 wp[4];    // Wp[16ti + r][16w + 4g .. +3]            ti = 0..3
-  float4 qg[4];    // Qg[16ti + r][16w + 4g .. +3]
-  float4 kg[4];    // Kg^T[16w + r][16u + 4g .. +3]           u = 0..3
-  float4 aq[4];    // Aqk[16to + r][16u + 4g .. +3]           (used by the o-tile waves)
+  float4 wp[4];    // FA(Wp) block (ti, w):    Wp[16ti + r][16w + 4g .. +3]
+  float4 kg[4];    // FA(Kg^T) block (w, u):   Kg^T[16w + r][16u + 4g .. +3]
+  float4 uu;       // FA(U^T) block (slice, tp), lane lp (the v_new reduction pair)
   float4 gm;       // gamma[16w + 4g .. +3]
-  float4 uu;       // U^T[c0 + j_p][16t_p + 4g_p .. +3]       (v_new reduction pair)
 };
 
-template <int D, int MODE, bool RES>
+template <int D, int MODE>
 __global__ __launch_bounds__(D / 16 * WAVE) void scan_fwd_kernel(ScanFwdArgs a) {
-  constexpr int NW = D / 16, NT = NW * WAVE, NVB = D / 16, NP = 512 / NT;
-  __shared__ float4 sPv[NW * 4 * WAVE];
-  __shared__ float4 sPo[NW * 4 * WAVE];
-  __shared__ float sVT[16 * LVT];
-  __shared__ float4 sO1[4 * WAVE];
-  const Cfg& cf = a.cfg;
-  const float clip = cf.clip, scale = cf.scale;
+  constexpr int NW = D / 16, NT = NW * WAVE, NVB = D / 16;
+  __shared__ float4 sPv[NW * 4 * WAVE];    // partial (Wp h) tiles, [wave][ti][lane]
+  __shared__ float4 sVB[4 * WAVE];         // v_new tiles in B-operand layout, [u][lane]
+  const float clip = a.cfg.clip;
   const int nc = a.nc;
   const int lin = xcd_remap(gridDim.x);
   const int vb = lin % NVB, bh = lin / NVB, c0 = 16 * vb;
   const int tid = threadIdx.x, l = lane_id(), r = l & 15, g = l >> 4, w = wave_id();
-  const bool o_role = NW == 8 ? (w >= 4) : true;
-  const int to = NW == 8 ? (w >= 4 ? w - 4 : 0) : w;
-  // the reduction pair of this thread: output tile tp, lane lp of its MFMA layout
-  const int tp = (tid & 255) >> 6, lp = tid & 63, gp = lp >> 4, jp = lp & 15;
+  // the reduction pair of this thread (threads < 256): output tile tp, lane lp
+  const int tp = (tid & 255) >> 6, lp = tid & 63;
 
   f4 h;
 #pragma unroll
   for (int e = 0; e < 4; ++e)
     h[e] = a.h0 ? a.h0[(size_t)bh * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r] : 0.f;
 
-  auto load = [&](FwdOps<D>& op, int c) {
+  auto load = [&](FwdOps& op, int c) {
     const size_t ch = (size_t)bh * nc + (c < nc ? c : nc - 1), tb = ch * T * D;
-    const float* pw = a.wp + tb + (size_t)r * D + 16 * w + 4 * g;
-    const float* pq = a.qg + tb + (size_t)r * D + 16 * w + 4 * g;
-    const float* pk = a.kgT + tb + (size_t)(16 * w + r) * T + 4 * g;
-    const float* pa = a.aqk + ch * T * T + (size_t)(16 * to + r) * T + 4 * g;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      op.wp[i] = ld4(pw + 16 * i * D);
-      op.qg[i] = ld4(pq + 16 * i * D);
-      op.kg[i] = ld4(pk + 16 * i);
-      op.aq[i] = ld4(pa + 16 * i);
+      op.wp[i] = ld4(a.wp_f + tb + frag_blk(i, w, D) + 4 * l);
+      op.kg[i] = ld4(a.kgT_f + tb + frag_blk(w, i, T) + 4 * l);
     }
+    op.uu = ld4(a.uT_f + tb + frag_blk(vb, tp, T) + 4 * lp);
     op.gm = ld4(a.gl + ch * D + 16 * w + 4 * g);
-    op.uu = ld4(a.uT + tb + (size_t)(c0 + jp) * T + 16 * tp + 4 * gp);
   };
 
-  auto step = [&](const FwdOps<D>& op, int c) {
+  auto step = [&](const FwdOps& op, int c) {
     const size_t ch = (size_t)bh * nc + c, tb = ch * T * D;
-    if constexpr (RES) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) a.h_pre[ch * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r] = h[e];
-    }
-    // partial Wp h and Qg h over this wave's 16 key rows
+    st4(a.h_pre_f + ch * D * D + frag_blk(vb, w, D) + 4 * l, f4_to_float4(h));
+    // partial Wp h over this wave's 16 key rows
     const float4 hb = f4_to_float4(h);
-    f4 pv[4], po[4];
+    f4 pv[4];
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) {
       pv[ti] = f4{0.f, 0.f, 0.f, 0.f};
-      po[ti] = f4{0.f, 0.f, 0.f, 0.f};
       mma16<MODE>(pv[ti], op.wp[ti], hb);
-      mma16<MODE>(po[ti], op.qg[ti], hb);
     }
     drain(pv[0], pv[1], pv[2], pv[3]);
-    drain(po[0], po[1], po[2], po[3]);
 #pragma unroll
-    for (int ti = 0; ti < 4; ++ti) {
-      sPv[(w * 4 + ti) * WAVE + l] = f4_to_float4(pv[ti]);
-      sPo[(w * 4 + ti) * WAVE + l] = f4_to_float4(po[ti]);
+    for (int ti = 0; ti < 4; ++ti) sPv[(w * 4 + ti) * WAVE + l] = f4_to_float4(pv[ti]);
+    __syncthreads();
+    // fixed-order reduction over waves: v_new = U - sum
+    if (tid < 4 * WAVE) {
+      float4 s = sPv[tid];
+#pragma unroll
+      for (int w2 = 1; w2 < NW; ++w2) s = add4(s, sPv[w2 * 4 * WAVE + tid]);
+      const float4 vn = sub4(op.uu, s);
+      sVB[tid] = vn;
+      st4(a.v_new_f + tb + frag_blk(vb, tp, T) + 4 * lp, vn);
     }
     __syncthreads();
-    // fixed-order reduction over waves: v_new = U - sum, O1 = sum
-#pragma unroll
-    for (int q = 0; q < NP; ++q) {
-      const int p = tid + q * NT, mat = p >> 8, pi = p & 255;
-      const float4* src = mat ? sPo : sPv;
-      float4 s = src[pi];
-#pragma unroll
-      for (int w2 = 1; w2 < NW; ++w2) {
-        const float4 x = src[w2 * 4 * WAVE + pi];
-        s.x += x.x; s.y += x.y; s.z += x.z; s.w += x.w;
-      }
-      if (mat == 0) {
-        const float4 vn = make_float4(op.uu.x - s.x, op.uu.y - s.y, op.uu.z - s.z, op.uu.w - s.w);
-        st4(&sVT[jp * LVT + 16 * tp + 4 * gp], vn);
-        if constexpr (RES) {
-          float* pv2 = a.v_new + tb + (size_t)(16 * tp + 4 * gp) * D + c0 + jp;
-          pv2[0] = vn.x; pv2[D] = vn.y; pv2[2 * D] = vn.z; pv2[3 * D] = vn.w;
-        }
-      } else {
-        sO1[pi] = s;
-      }
-    }
-    __syncthreads();
-    float4 vt[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) vt[u] = ld4(&sVT[r * LVT + 16 * u + 4 * g]);
     f4 hn = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < 4; ++u) mma16<MODE>(hn, op.kg[u], vt[u]);
-    if (o_role) {
-      // straight-line over all 4 blocks: the blocks above the diagonal of Aqk are exact zeros
-      f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int u = 0; u < 4; ++u) mma16<MODE>(acc, op.aq[u], vt[u]);
-      drain(acc);
-      const float4 o1 = sO1[to * WAVE + l];
-      const float ov[4] = {o1.x, o1.y, o1.z, o1.w};
-      float* po2 = a.o + tb + (size_t)(16 * to + 4 * g) * D + c0 + r;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) po2[e * D] = sanitize(scale * ov[e] + acc[e], clip);
-    }
+    for (int u = 0; u < 4; ++u) mma16<MODE>(hn, op.kg[u], sVB[u * WAVE + l]);
     drain(hn);
     const float gmv[4] = {op.gm.x, op.gm.y, op.gm.z, op.gm.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) h[e] = sanitize(h[e] * exp_nonpos(gmv[e]) + hn[e], clip);
   };
 
-  FwdOps<D> A, B;
+  FwdOps A, B;
   load(A, 0);
   int c = 0;
   for (; c + 1 < nc; c += 2) {
@@ -205,18 +156,14 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
   auto chunk = [&](int s) { return (size_t)bh * nc + (s < nc ? nc - 1 - s : 0); };
   auto load = [&](BwdOps<D>& op, int s) {
     const size_t ch = chunk(s), tb = ch * T * D;
-    const float* pk = a.kg + tb + (size_t)r * D + 16 * w + 4 * g;
-    const float* pa = a.aqkT + ch * T * T + (size_t)(16 * ta + r) * T + 4 * g;
-    const float* pq = a.qgT + tb + (size_t)(16 * w + r) * T + 4 * g;
-    const float* pw = a.wpT + tb + (size_t)(16 * w + r) * T + 4 * g;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      op.kg[i] = ld4(pk + 16 * i * D);
-      op.qgT[i] = ld4(pq + 16 * i);
-      op.wpT[i] = ld4(pw + 16 * i);
+      op.kg[i] = ld4(a.kg_f + tb + frag_blk(i, w, D) + 4 * l);
+      op.qgT[i] = ld4(a.qgT_f + tb + frag_blk(w, i, T) + 4 * l);
+      op.wpT[i] = ld4(a.wpT_f + tb + frag_blk(w, i, T) + 4 * l);
     }
 #pragma unroll
-    for (int q = 0; q < PA; ++q) op.aqT[q] = ld4(pa + 16 * (ua + q));
+    for (int q = 0; q < PA; ++q) op.aqT[q] = ld4(a.aqkT_f + ch * T * T + frag_blk(ta, ua + q, T) + 4 * l);
     op.gm = ld4(a.gl + ch * D + 16 * w + 4 * g);
   };
   auto load_do = [&](int s) { return ld4(a.dout + chunk(s) * T * D + (size_t)srow * D + c0 + scol); };
@@ -234,8 +181,7 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
     const size_t ch = chunk(s), tb = ch * T * D;
     const float4 dnext = load_do(s + 1);           // dO of the next step, staged below
     // dh entering this chunk's step (mega.py:35)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) a.dh_next[ch * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r] = dh[e];
+    st4(a.dh_next_f + ch * D * D + frag_blk(vb, w, D) + 4 * l, f4_to_float4(dh));
     float4 dob[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) dob[u] = ld4(&sDOT[buf][r * LVT + 16 * u + 4 * g]);
@@ -279,8 +225,7 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
       const float4 dv = make_float4(sanitize(sm.x, clip), sanitize(sm.y, clip), sanitize(sm.z, clip),
                                     sanitize(sm.w, clip));
       st4(&sDVT[jp * LVT + 16 * tp + 4 * gp], dv);
-      float* pv = a.dv_new + tb + (size_t)(16 * tp + 4 * gp) * D + c0 + jp;
-      pv[0] = dv.x; pv[D] = dv.y; pv[2 * D] = dv.z; pv[3 * D] = dv.w;
+      st4(a.dv_new_f + tb + frag_blk(vb, tp, T) + 4 * lp, dv);
     }
     stage_do(buf ^ 1, dnext);
     __syncthreads();
@@ -310,16 +255,10 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
 }
 
 hipError_t launch_scan_fwd(int D, const ScanFwdArgs& a, hipStream_t s) {
-  const bool res = a.h_pre != nullptr;
   dispatch_mode(a.cfg.dot_mode, [&](auto m) {
     constexpr int M = decltype(m)::value;
-    if (D == 128) {
-      if (res) hipLaunchKernelGGL((scan_fwd_kernel<128, M, true>), dim3(a.n_bh * 8), dim3(512), 0, s, a);
-      else hipLaunchKernelGGL((scan_fwd_kernel<128, M, false>), dim3(a.n_bh * 8), dim3(512), 0, s, a);
-    } else {
-      if (res) hipLaunchKernelGGL((scan_fwd_kernel<64, M, true>), dim3(a.n_bh * 4), dim3(256), 0, s, a);
-      else hipLaunchKernelGGL((scan_fwd_kernel<64, M, false>), dim3(a.n_bh * 4), dim3(256), 0, s, a);
-    }
+    if (D == 128) hipLaunchKernelGGL((scan_fwd_kernel<128, M>), dim3(a.n_bh * 8), dim3(512), 0, s, a);
+    else hipLaunchKernelGGL((scan_fwd_kernel<64, M>), dim3(a.n_bh * 4), dim3(256), 0, s, a);
     return 0;
   });
   return hipGetLastError();

@@ -33,7 +33,8 @@ B_, H_, L_, D_, T_ = 4, 6, 2048, 128, 64
 def kernel_flops_per_token(T=T_, D=D_):
     return {
         "wy_fwd": 8 * T * D,                      # Aqk, Akk, Wp, U
-        "scan_fwd": 2 * T * D + 6 * D * D,        # Aqk v_new; Wp h, Qg h, Kg^T v_new
+        "scan_fwd": 4 * D * D,                    # Wp h, Kg^T v_new
+        "out_fwd": 2 * T * D + 2 * D * D,         # Aqk v_new, Qg h_pre
         "scan_bwd": 2 * T * D + 6 * D * D,        # Aqk^T dO; Kg dh, Qg^T dO, Wp^T dv_new
         "bwd_state": 6 * D * D,                   # dQg, dWp, dKg
         "bwd_wy": 18 * T * D + 4 * T * T,         # dAqk, dA, dkb, dwv, B4; dA A^T, A^T tmp

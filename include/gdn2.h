@@ -52,16 +52,19 @@ typedef struct gdn2_desc {
 } gdn2_desc;
 
 /* Residual buffer written by gdn2_fwd and read by gdn2_bwd: sub-buffers at the offsets
- * reported by gdn2_residual_layout (bytes, 256-aligned).  Shapes (float32), per chunk:
- *   AQKT  (B,H,nc,bt,bt)  gated q.k scores, transposed: AQKT[j][i] = Aqk[i][j]  (pipeline.py:25)
- *   A     (B,H,nc,bt,bt)  the WY inverse (I + (1-eps) Akk)^-1                  (pipeline.py:25)
- *   HPRE  (B,H,nc,D,D)    state entering each chunk                            (cd_slim.py:22)
- *   VNEW  (B,H,nc,bt,D)   v_new of each chunk                                  (cd_slim.py:23)
- *   WPT   (B,H,nc,D,bt)   W = A (b k e^gc), transposed                         (cd_slim.py:17)
- *   KG    (B,H,nc,bt,D)   gated k                                              (cd_slim.py:20)
- *   QGT   (B,H,nc,D,bt)   gated q, transposed                                  (cd_slim.py:21)
- *   GL    (B,H,nc,D)      gc of the chunk's last row                           (cd_slim.py:19)
- * Transposed tiles are what the reverse state scan reads as contiguous MFMA operands. */
+ * reported by gdn2_residual_layout (bytes, 256-aligned), float32, per chunk:
+ *   AQKT  (B,H,nc, bt*bt)  gated q.k scores, transposed, FRAG(Aqk^T)            (pipeline.py:25)
+ *   A     (B,H,nc,bt,bt)   the WY inverse (I + (1-eps) Akk)^-1, row-major        (pipeline.py:25)
+ *   HPRE  (B,H,nc, D*D)    state entering each chunk, FRAG(h_pre^T)              (cd_slim.py:22)
+ *   VNEW  (B,H,nc, D*bt)   v_new of each chunk, FRAG(v_new^T)                    (cd_slim.py:23)
+ *   WPT   (B,H,nc, D*bt)   W = A (b k e^gc), FRAG(W^T)                           (cd_slim.py:17)
+ *   KG    (B,H,nc, bt*D)   gated k, FRAG(Kg)                                     (cd_slim.py:20)
+ *   QGT   (B,H,nc, D*bt)   gated q, FRAG(Qg^T)                                   (cd_slim.py:21)
+ *   GL    (B,H,nc,D)       gc of the chunk's last row                            (cd_slim.py:19)
+ * FRAG(M) of an R x C matrix M is the MFMA fragment order the kernels load with one
+ * coalesced float4 per lane: 16x16 blocks in row-major block order (C/16 blocks per block
+ * row, 256 floats each); inside a block, floats [4 l, 4 l + 4) with l = r + 16 c hold
+ * M[16 bi + r][16 bj + 4 c + e], e = 0..3 (r = 0..15, c = 0..3). */
 enum { GDN2_RES_AQKT = 0, GDN2_RES_A, GDN2_RES_HPRE, GDN2_RES_VNEW, GDN2_RES_WPT, GDN2_RES_KG,
        GDN2_RES_QGT, GDN2_RES_GL, GDN2_RES_COUNT };
 
@@ -88,9 +91,9 @@ int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v,
              const float* d_hf, float* dq, float* dk, float* dv, float* dw, float* db, float* dg,
              float* dh0, void* workspace, void* stream);
 
-/* Chunk-parallel forward stages only.  Any output may be NULL except u (scratch for W/U),
- * aqk, wp, kg, qg, gl.  akk is the masked, sanitized Akk before the (1 - wy_eps) factor;
- * A is the sanitized inverse.  Shapes as in the residual layout. */
+/* Chunk-parallel forward stages only, all outputs row-major: aqk, akk, A (B,H,nc,bt,bt);
+ * wp, u, kg, qg (B,H,nc,bt,D); gl (B,H,nc,D).  akk and A may be NULL.  akk is the masked,
+ * sanitized Akk before the (1 - wy_eps) factor; A is the sanitized inverse. */
 int gdn2_wy_stage(const gdn2_desc* d, const float* q, const float* k, const float* v,
                   const float* w, const float* b, const float* g, float* aqk, float* akk,
                   float* A, float* wp, float* u, float* kg, float* qg, float* gl, void* stream);
@@ -104,8 +107,8 @@ int gdn2_debug_gemm(int mode, const float* A, const float* B, float* C, int M, i
  * gdn2_prof_begin(n) starts recording for up to n launches (process-wide, not re-entrant);
  * gdn2_prof_end synchronises on the recorded events and returns, per kernel id, the summed
  * duration in milliseconds and the launch count, then stops recording.
- * Kernel ids: 0 wy_fwd, 1 scan_fwd, 2 scan_bwd, 3 bwd_state, 4 bwd_wy. */
-#define GDN2_NUM_KERNELS 5
+ * Kernel ids: 0 wy_fwd, 1 scan_fwd, 2 scan_bwd, 3 bwd_state, 4 bwd_wy, 5 out_fwd. */
+#define GDN2_NUM_KERNELS 6
 int gdn2_prof_begin(int max_launches);
 int gdn2_prof_end(double ms_sum[GDN2_NUM_KERNELS], int counts[GDN2_NUM_KERNELS]);
 

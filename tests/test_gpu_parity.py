@@ -187,13 +187,11 @@ def test_forward_residuals_config1(cfg1):
     _lib.check(_lib.lib().gdn2_fwd(ctypes.byref(desc), *map(_lib.ptr, xs), _lib.ptr(h0), _lib.ptr(o), _lib.ptr(hf),
                                    _lib.ptr(res), _lib.ptr(ws), _lib.stream_handle()), "gdn2_fwd")
     torch.cuda.synchronize()
-    shapes = dict(aqkT=(B, H, nc, 64, 64), A=(B, H, nc, 64, 64), h_pre=(B, H, nc, D, D), v_new=(B, H, nc, 64, D),
-                  wpT=(B, H, nc, D, 64), kg=(B, H, nc, 64, D), qgT=(B, H, nc, D, 64), gl=(B, H, nc, D))
     got = {}
-    for n, off in zip(_lib.RES_NAMES, offs):
-        cnt = int(np.prod(shapes[n]))
-        t = res[off:off + 4 * cnt].view(torch.float32).reshape(shapes[n]).cpu()
-        got[n.rstrip("T")] = t.transpose(-1, -2) if n.endswith("T") else t
+    ends = list(offs[1:]) + [tot]
+    for n, off, end in zip(_lib.RES_NAMES, offs, ends):
+        flat = res[off:end].view(torch.float32).cpu()
+        got[n.rstrip("T")] = _lib.decode_residual(n, flat, B, H, nc, 64, D)
     t = [torch.from_numpy(a).double() for a in arrs]
     oc = O.OracleCfg.from_cfg(cfg)
     st = O.wy_stage_ref(*t, scale, oc)

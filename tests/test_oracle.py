@@ -19,8 +19,16 @@ import torch
 
 from oracle import gdn2_oracle as O
 
-torch.set_default_dtype(torch.float64)
 GOLD = Path(__file__).resolve().parent / "golden"
+
+
+@pytest.fixture(autouse=True)
+def _float64_default():
+    """float64 default dtype for these tests only (collection of other modules is unaffected)."""
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)
+    yield
+    torch.set_default_dtype(prev)
 
 
 def t64(x):

@@ -82,8 +82,9 @@ def test_residual_layout_and_workspaces():
         assert nxt - o >= s
     L = _lib.lib()
     d = _desc()
-    # [U^T | Aqk | Wp | Qg | Kg^T | gl]
-    assert L.gdn2_fwd_workspace_bytes(ctypes.byref(d), 1) == N * (4 * 64 * 128 + 64 * 64 + 128) * 4
+    # [Wp | U^T | Kg^T | Qg | Aqk], without a residual also [gl | h_pre | v_new]
+    assert L.gdn2_fwd_workspace_bytes(ctypes.byref(d), 1) == N * (4 * 64 * 128 + 64 * 64) * 4
+    assert L.gdn2_fwd_workspace_bytes(ctypes.byref(d), 0) == N * (5 * 64 * 128 + 64 * 64 + 128 + 128 * 128) * 4
     assert L.gdn2_bwd_workspace_bytes(ctypes.byref(d)) >= N * (4 * 64 * 128 + 128 * 128 + 128) * 4
 
 
@@ -130,6 +131,22 @@ def test_synthetic_inputs_recipe():
     rng = np.random.Generator(np.random.PCG64(0))
     draws = [rng.standard_normal((1, 2, 128, 64)) for _ in range(3)]   # order q, k, v
     assert np.array_equal(v, draws[2].astype(np.float32))
+
+
+def test_fragment_layout_roundtrip_and_definition():
+    from atomic_gdn2.layout import from_frag, to_frag
+    from atomic_gdn2 import _lib
+    m = torch.randn(2, 3, 64, 128)
+    f = to_frag(m)
+    assert torch.equal(from_frag(f, 64, 128), m)
+    off = lambda i, j, C: ((i // 16) * (C // 16) + j // 16) * 256 + 4 * ((i % 16) + 16 * ((j % 16) // 4)) + j % 4
+    for i, j in [(0, 0), (5, 7), (17, 33), (63, 127), (40, 90)]:
+        assert f[1, 2, off(i, j, 128)] == m[1, 2, i, j]
+    # residual decoding: a transposed fragment sub-buffer comes back as the named quantity
+    B, H, nc, T, D = 1, 2, 3, 64, 128
+    wp = torch.randn(B, H, nc, T, D)
+    flat = to_frag(wp.transpose(-1, -2).contiguous()).reshape(-1)
+    assert torch.equal(_lib.decode_residual("wpT", flat, B, H, nc, T, D), wp)
 
 
 def test_golden_fixture_inputs_are_reproduced():
