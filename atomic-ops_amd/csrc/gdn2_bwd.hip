@@ -83,14 +83,31 @@ __global__ __launch_bounds__(512) void bwd_state_kernel(BwdStateArgs a) {
 }
 
 // ------------------------------------------------------------------------------------
+// bwd_wy: one workgroup (8 waves) per chunk.
+//
+// Output ownership: wave w owns column strip s = w % (D/16) (columns 16 s .. 16 s + 15) and
+// NTW row tiles of it.  Lane l = n + 16 g works on column 16 s + n and rows 16 t + 4 g + e
+// (e = 0..3) of every row tile t: the MFMA accumulator layout, which is also the B-operand
+// layout, so the per-element factors of B4 (legs, q/k/b) computed once per lane feed both
+// the MFMA operands and the element-wise updates.
+//
+// Phases (LDS: gc | X1 | X2 | A | dAqk | dA/dAkk | column partial sums):
+//   P1 dAqk = (dO v_new^T) * causal                         X1 = v_new            (mega.py:32)
+//   P2 dA = san(dWp kb^T + dv_new (w v)^T)                   X1 = kb, X2 = dv_new  (mega.py:41)
+//   P3 tmp = san(dA A^T)                                      X1 = tmp              (mega.py:43)
+//   P4 dAkk = san(-(1-eps) A^T tmp) * strict                                       (mega.py:44)
+//   B4 VJP of the two-level scores, piece by piece (owned tiles, registers)   (b4.py:45-97)
+//   per owned tile: dkb = A^T dWp, dwv = A^T dv_new (mega.py:42), the gate gradients
+//   dq3 / dk3 / db3 / dgc3 and the combine with B4                           (mega.py:45-59)
+//   B5 dg = reverse cumsum of dgc3 + dgc4                                            (mega.py:53)
+// ------------------------------------------------------------------------------------
 template <int D>
 struct BwdWyLayout {
   static constexpr int LD = D + 4, LT = T + 4;
-  static constexpr int OFF_G = 0, OFF_X = T * LD, OFF_Y = 2 * T * LD;
-  static constexpr int OFF_DAQ = 3 * T * LD, OFF_DA = OFF_DAQ + T * LT, OFF_A = OFF_DA + T * LT;
-  static constexpr int OFF_COL = OFF_A + T * LT;
-  static constexpr int TOTAL = OFF_COL + D;
-  static_assert(2 * T * LD >= 3 * 32 * LD, "B4 staging must fit in X+Y");
+  static constexpr int OFF_G = 0, OFF_X1 = T * LD, OFF_X2 = 2 * T * LD;
+  static constexpr int OFF_A = 3 * T * LD, OFF_DAQ = OFF_A + T * LT, OFF_DA = OFF_DAQ + T * LT;
+  static constexpr int OFF_COL = OFF_DA + T * LT;
+  static constexpr int TOTAL = OFF_COL + 8 * 16;
 };
 
 // Tiles of a T x D output owned by wave w: column strip w % (D/16); row tiles
@@ -102,304 +119,372 @@ struct Strip {
   __device__ static int rtile(int w, int m) { return w / NS + m * STEP; }
 };
 
+// x[t] for a runtime t in [0, 4) without dynamic register indexing
+__device__ __forceinline__ float4 pick4(const float4 (&x)[4], int t) {
+  float4 o = x[0];
+#pragma unroll
+  for (int u = 1; u < 4; ++u)
+    if (t == u) o = x[u];
+  return o;
+}
+
 template <int D, int B3>
 __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   using Lay = BwdWyLayout<D>;
   using St = Strip<D>;
-  constexpr int LD = Lay::LD, LT = Lay::LT, NT = 512, NW = 8, NTW = St::NTW;
-  __shared__ float smem[Lay::TOTAL];
+  constexpr int LD = Lay::LD, LT = Lay::LT, NT = 512, NW = 8, NTW = St::NTW, NKB = D / 16;
+  __shared__ __attribute__((aligned(16))) float smem[Lay::TOTAL];
   float* sG = smem + Lay::OFF_G;
-  float* sX = smem + Lay::OFF_X;
-  float* sY = smem + Lay::OFF_Y;
+  float* sX1 = smem + Lay::OFF_X1;
+  float* sX2 = smem + Lay::OFF_X2;
+  float* sA = smem + Lay::OFF_A;
   float* sDAq = smem + Lay::OFF_DAQ;
   float* sDA = smem + Lay::OFF_DA;
-  float* sA = smem + Lay::OFF_A;
-  float* sCol = smem + Lay::OFF_COL;
+  float* sColP = smem + Lay::OFF_COL;
   const Cfg& cf = a.cfg;
   const float clip = cf.clip, scale = cf.scale;
-  const int chunk = blockIdx.x, tid = threadIdx.x, wv = wave_id();
+  const int chunk = blockIdx.x, tid = threadIdx.x, wv = wave_id(), l = lane_id(), r = l & 15, g = l >> 4;
   const size_t tb = (size_t)chunk * T * D, sb = (size_t)chunk * T * T;
   const float* __restrict__ q = a.q + tb;
   const float* __restrict__ k = a.k + tb;
   const float* __restrict__ b = a.b + tb;
   const float* __restrict__ w = a.w + tb;
   const float* __restrict__ v = a.v + tb;
-  const int strip = St::strip(wv);
-  const int dcol = strip * 16 + tile_col();
+  const float* __restrict__ dout = a.dout + tb;
+  const float* __restrict__ dwp = a.dwp + tb;
+  const int strip = St::strip(wv), dcol = 16 * strip + r;
+  auto owned = [&](int t) { return t >= St::rtile(wv, 0) && (t - St::rtile(wv, 0)) % St::STEP == 0; };
 
-  chunk_cumsum<D, LD, NT>(a.g + tb, sG);
+  // x[16 t + 4 g + e][dcol], e = 0..3: this lane's column at the rows of row tile t
+  auto col4 = [&](const float* __restrict__ x, int t) {
+    const float* p = x + (16 * t + 4 * g) * D + dcol;
+    return make_float4(p[0], p[D], p[2 * D], p[3 * D]);
+  };
 
-  // dAqk = (dO v_new^T) * causal                                     (mega.py:32)
-  load_rows<LD>(sX, a.dout + tb, T, D, tid, NT);
-  load_fragT<LD>(sY, a.v_new_f + tb, D, T, 0, T, tid, NT);
-  load_rows<LT>(sA, a.A + sb, T, T, tid, NT);
-  __syncthreads();
+  load_fragT<LD>(sX1, a.v_new_f + tb, D, T, 0, T, tid, NT);
+  chunk_cumsum<D, LD, NT>(a.g + tb, sG);          // ends with a barrier: sG, X1 ready
+
+  // P1: dAqk = (dO v_new^T) * causal
   for (int t = wv; t < 16; t += NW) {
-    const int ti = t / 4, tj = t % 4;
+    const int ti = t >> 2, tj = t & 3;
+    const float* ar = dout + (16 * ti + r) * D + 4 * g;
+    const float* br = sX1 + (16 * tj + r) * LD + 4 * g;
     f4 acc = {0.f, 0.f, 0.f, 0.f};
-    mma_tile<B3>(acc, rm(sX, LD).shift(ti * 16, 0), tr(sY, LD).shift(0, tj * 16), D);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = ti * 16 + tile_row(r), j = tj * 16 + tile_col();
-      sDAq[i * LT + j] = j <= i ? acc[r] : 0.f;
+    for (int kb = 0; kb < NKB; ++kb) mma16<B3>(acc, ld4(ar + 16 * kb), ld4(br + 16 * kb));
+    drain(acc);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 16 * ti + 4 * g + e, j = 16 * tj + r;
+      sDAq[i * LT + j] = j <= i ? acc[e] : 0.f;
     }
   }
   __syncthreads();
 
-  // dA = san(dWp kb^T + dv_new (w v)^T)                               (mega.py:41)
-  f4 accA[2];
-  accA[0] = f4{0.f, 0.f, 0.f, 0.f};
-  accA[1] = f4{0.f, 0.f, 0.f, 0.f};
-  load_rows<LD>(sX, a.dwp + tb, T, D, tid, NT);
-  for (int e = tid; e < T * D; e += NT) {
-    const int i = e / D, d = e % D;
-    sY[i * LD + d] = (b[e] * k[e]) * exp_nonpos(sG[i * LD + d]);
+  // P2 operands: X1 = kb = b k e^{min(gc,0)}, X2 = dv_new (kept for P5), sA = A
+  load_fragT<LD>(sX2, a.dv_new_f + tb, D, T, 0, T, tid, NT);
+  for (int f = tid; f < T * D / 4; f += NT) {
+    const int i = f / (D / 4), d = 4 * (f % (D / 4));
+    st4(sX1 + i * LD + d, mul4(mul4(ld4(b + i * D + d), ld4(k + i * D + d)), expnp4(ld4(sG + i * LD + d))));
   }
-  __syncthreads();
-#pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    const int t = wv + 8 * m, ti = t / 4, tj = t % 4;
-    mma_tile<B3>(accA[m], rm(sX, LD).shift(ti * 16, 0), tr(sY, LD).shift(0, tj * 16), D);
-  }
-  __syncthreads();
-  load_fragT<LD>(sX, a.dv_new_f + tb, D, T, 0, T, tid, NT);
-  for (int e = tid; e < T * D; e += NT) {
-    const int i = e / D, d = e % D;
-    sY[i * LD + d] = w[e] * v[e];
-  }
-  __syncthreads();
-#pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    const int t = wv + 8 * m, ti = t / 4, tj = t % 4;
-    f4 acc2 = {0.f, 0.f, 0.f, 0.f};
-    mma_tile<B3>(acc2, rm(sX, LD).shift(ti * 16, 0), tr(sY, LD).shift(0, tj * 16), D);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = ti * 16 + tile_row(r), j = tj * 16 + tile_col();
-      sDA[i * LT + j] = sanitize(accA[m][r] + acc2[r], clip);
-    }
-  }
+  for (int f = tid; f < T * T / 4; f += NT) st4(sA + (f >> 4) * LT + 4 * (f & 15), ld4(a.A + sb + 4 * f));
   __syncthreads();
 
-  // tmp = san(dA A^T) into X; dAkk = san(-(1-eps) A^T tmp * strict) into sDA  (mega.py:43-44)
-  float* sTmp = sX;
+  // P2: dA = san(dWp kb^T + dv_new (w v)^T)
   for (int t = wv; t < 16; t += NW) {
-    const int ti = t / 4, tj = t % 4;
-    f4 acc = {0.f, 0.f, 0.f, 0.f};
-    mma_tile<B3>(acc, rm(sDA, LT).shift(ti * 16, 0), tr(sA, LT).shift(0, tj * 16), T);
+    const int ti = t >> 2, tj = t & 3;
+    const float* a1 = dwp + (16 * ti + r) * D + 4 * g;
+    const float* b1 = sX1 + (16 * tj + r) * LD + 4 * g;
+    const float* a2 = sX2 + (16 * ti + r) * LD + 4 * g;
+    const float* wr = w + (16 * tj + r) * D + 4 * g;
+    const float* vr = v + (16 * tj + r) * D + 4 * g;
+    f4 acc1 = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = ti * 16 + tile_row(r), j = tj * 16 + tile_col();
-      sTmp[i * LT + j] = sanitize(acc[r], clip);
+    for (int kb = 0; kb < NKB; ++kb) {
+      mma16<B3>(acc1, ld4(a1 + 16 * kb), ld4(b1 + 16 * kb));
+      mma16<B3>(acc2, ld4(a2 + 16 * kb), mul4(ld4(wr + 16 * kb), ld4(vr + 16 * kb)));
     }
+    drain(acc1, acc2);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sDA[(16 * ti + 4 * g + e) * LT + 16 * tj + r] = sanitize(acc1[e] + acc2[e], clip);
+  }
+
+  __syncthreads();
+
+  // P3: tmp = san(dA A^T) into X1 (as T x LT)
+  float* sTmp = sX1;
+  for (int t = wv; t < 16; t += NW) {
+    const int ti = t >> 2, tj = t & 3;
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+      mma16<B3>(acc, ld4(sDA + (16 * ti + r) * LT + 16 * kb + 4 * g), ld4(sA + (16 * tj + r) * LT + 16 * kb + 4 * g));
+    drain(acc);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sTmp[(16 * ti + 4 * g + e) * LT + 16 * tj + r] = sanitize(acc[e], clip);
   }
   __syncthreads();
-  {
-    f4 accK[2];
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const int t = wv + 8 * m, ti = t / 4, tj = t % 4;
-      accK[m] = f4{0.f, 0.f, 0.f, 0.f};
-      mma_tile<B3>(accK[m], tr(sA, LT).shift(ti * 16, 0), rm(sTmp, LT).shift(0, tj * 16), T);
-    }
-    __syncthreads();   // all reads of sDA (tmp GEMM) and sTmp done before overwriting
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const int t = wv + 8 * m, ti = t / 4, tj = t % 4;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = ti * 16 + tile_row(r), j = tj * 16 + tile_col();
-        sDA[i * LT + j] = j < i ? sanitize(-accK[m][r] * cf.ome, clip) : 0.f;
+
+  // P4: dAkk = san(-(1-eps) A^T tmp) * strict into sDA; tiles above the diagonal are zero
+  for (int t = wv; t < 16; t += NW) {
+    const int ti = t >> 2, tj = t & 3;
+    float ov[4] = {0.f, 0.f, 0.f, 0.f};
+    if (tj <= ti) {
+      f4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int kb = ti; kb < 4; ++kb) {
+        const float* ac = sA + (16 * kb + 4 * g) * LT + 16 * ti + r;
+        const float* tc = sTmp + (16 * kb + 4 * g) * LT + 16 * tj + r;
+        mma16<B3>(acc, make_float4(ac[0], ac[LT], ac[2 * LT], ac[3 * LT]),
+                  make_float4(tc[0], tc[LT], tc[2 * LT], tc[3 * LT]));
       }
+      drain(acc);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        ov[e] = (16 * tj + r < 16 * ti + 4 * g + e) ? sanitize(-acc[e] * cf.ome, clip) : 0.f;
     }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sDA[(16 * ti + 4 * g + e) * LT + 16 * tj + r] = ov[e];
   }
-  // last-row decay gradient (mega.py:50): sum_i dkg*kg*mkg + e^gamma * sum_v(dh_next*h_pre) * mdec
-  if (tid < D) {
-    const int d = tid;
-    const float gl = sG[(T - 1) * LD + d];
-    float s = 0.f;
-    for (int i = 0; i < T; ++i) {
-      const float gi = sG[i * LD + d];
-      const float kg = sanitize(k[i * D + d] * exp_nonpos(gl - gi), clip);
-      const float mkg = (gl - gi) < 0.f ? 1.f : 0.f;
-      s += (a.dkg[tb + i * D + d] * kg) * mkg;
-    }
-    const float dec = exp_nonpos(gl), mdec = gl < 0.f ? 1.f : 0.f;
-    sCol[d] = s + dec * a.dlast[(size_t)chunk * D + d] * mdec;
-  }
+  __syncthreads();
 
-  // B4: VJP of the two-level scores, piece by piece (bwd/b4.py:45-97)
-  f4 bq[NTW], bbk[NTW], bk[NTW], bgc[NTW];
+  // B4: VJP of the two-level scores on the owned tiles (b4.py:45-97)
+  f4 dq4[NTW], dbk4[NTW], dk4[NTW], dgc4[NTW];
 #pragma unroll
   for (int m = 0; m < NTW; ++m) {
-    bq[m] = f4{0.f, 0.f, 0.f, 0.f};
-    bbk[m] = bq[m];
-    bk[m] = bq[m];
-    bgc[m] = bq[m];
+    dq4[m] = f4{0.f, 0.f, 0.f, 0.f};
+    dbk4[m] = dq4[m];
+    dk4[m] = dq4[m];
+    dgc4[m] = dq4[m];
   }
-  float* sQt = sX;
-  float* sBt = sX + 32 * LD;
-  float* sKt = sX + 64 * LD;
+  const bool lean = cf.diag == DIAG_LEAN;
   for (int pi = 0; pi < cf.pieces.n; ++pi) {
     const Piece pc = cf.pieces.p[pi];
-    const int P = pc.P;
-    const bool lean = (pc.kind == 1 && cf.diag == DIAG_LEAN);
-    __syncthreads();
-    for (int e = tid; e < P * D; e += NT) {
-      const int i = e / D, d = e % D;
-      const int row = pc.row0 + i, col = pc.col0 + i;
-      const float ra = lean ? 1.f : piece_row_leg(pc, sG, LD, row, d);
-      const float cb = lean ? 1.f : piece_col_leg(pc, sG, LD, col, d);
-      sQt[i * LD + d] = q[row * D + d] * ra;
-      sBt[i * LD + d] = (b[row * D + d] * k[row * D + d]) * ra;
-      sKt[i * LD + d] = k[col * D + d] * cb;
+    const int nb = pc.P / 16, tr0 = pc.row0 / 16, tc0 = pc.col0 / 16;
+    if (pc.kind == 1 && lean) continue;
+    // legs at this lane's positions; qt = q ra, bkt = (b k) ra over the piece rows,
+    // kt = k cb over the piece columns (k blocks of 16)
+    float4 ra[2], cbl[2], qt[2], bkt[2], kt[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const int ti = tr0 + (kb < nb ? kb : 0), tj = tc0 + (kb < nb ? kb : 0);
+      float rv[4], cv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        rv[e] = piece_row_leg(pc, sG, LD, 16 * ti + 4 * g + e, dcol);
+        cv[e] = piece_col_leg(pc, sG, LD, 16 * tj + 4 * g + e, dcol);
+      }
+      ra[kb] = make_float4(rv[0], rv[1], rv[2], rv[3]);
+      cbl[kb] = make_float4(cv[0], cv[1], cv[2], cv[3]);
+      qt[kb] = mul4(col4(q, ti), ra[kb]);
+      bkt[kb] = mul4(mul4(col4(b, ti), col4(k, ti)), ra[kb]);
+      kt[kb] = mul4(col4(k, tj), cbl[kb]);
     }
-    __syncthreads();
-#pragma unroll
-    for (int m = 0; m < NTW; ++m) {
-      const int rt = St::rtile(wv, m);
-      const int r0 = 16 * rt;
-      if (!lean) {
-        if (r0 >= pc.row0 && r0 < pc.row0 + P) {     // rows of the piece: dq, dbk
-          const int lr = r0 - pc.row0;
-          f4 dqt = {0.f, 0.f, 0.f, 0.f}, dbt = {0.f, 0.f, 0.f, 0.f};
-          mma_tile<DOT_HIGHEST>(dqt, rm(sDAq, LT).shift(r0, pc.col0), rm(sKt, LD).shift(0, strip * 16), P);
-          mma_tile<DOT_HIGHEST>(dbt, rm(sDA, LT).shift(r0, pc.col0), rm(sKt, LD).shift(0, strip * 16), P);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int i = r0 + tile_row(r), il = lr + tile_row(r), d = dcol;
-            const float ra = piece_row_leg(pc, sG, LD, i, d);
-            const float x = scale * dqt[r];
-            bq[m][r] += x * ra;
-            bbk[m][r] += dbt[r] * ra;
-            bgc[m][r] += x * sQt[il * LD + d] + dbt[r] * sBt[il * LD + d];
-          }
-        }
-        if (r0 >= pc.col0 && r0 < pc.col0 + P) {     // columns of the piece: dk
-          const int lc = r0 - pc.col0;
-          f4 k1 = {0.f, 0.f, 0.f, 0.f}, k2 = {0.f, 0.f, 0.f, 0.f};
-          mma_tile<DOT_HIGHEST>(k1, tr(sDAq + pc.row0 * LT, LT).shift(r0, 0), rm(sQt, LD).shift(0, strip * 16), P);
-          mma_tile<DOT_HIGHEST>(k2, tr(sDA + pc.row0 * LT, LT).shift(r0, 0), rm(sBt, LD).shift(0, strip * 16), P);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int j = r0 + tile_row(r), jl = lc + tile_row(r), d = dcol;
-            const float cb = piece_col_leg(pc, sG, LD, j, d);
-            const float x = scale * k1[r] + k2[r];
-            bk[m][r] += x * cb;
-            bgc[m][r] -= x * sKt[jl * LD + d];
-          }
-        }
+    // rows of the piece: dq, dbk, dgc
+    for (int rb = 0; rb < nb; ++rb) {
+      const int ti = tr0 + rb;
+      if (!owned(ti)) continue;
+      f4 dqt = {0.f, 0.f, 0.f, 0.f}, dbt = {0.f, 0.f, 0.f, 0.f};
+      const float* pq = sDAq + (16 * ti + r) * LT + pc.col0 + 4 * g;
+      const float* pk = sDA + (16 * ti + r) * LT + pc.col0 + 4 * g;
+      if (nb == 2) {          // whole chains per branch, each ending in drain()
+        mma16<DOT_HIGHEST>(dqt, ld4(pq), kt[0]);
+        mma16<DOT_HIGHEST>(dbt, ld4(pk), kt[0]);
+        mma16<DOT_HIGHEST>(dqt, ld4(pq + 16), kt[1]);
+        mma16<DOT_HIGHEST>(dbt, ld4(pk + 16), kt[1]);
+        drain(dqt, dbt);
       } else {
-        // lean diagonal (b4.py:20-30): exact E = exp(clip(gc_i - gc_j, +-diff_clip))
-        const float dc = cf.diff_clip;
-        if (r0 >= pc.row0 && r0 < pc.row0 + P) {
+        mma16<DOT_HIGHEST>(dqt, ld4(pq), kt[0]);
+        mma16<DOT_HIGHEST>(dbt, ld4(pk), kt[0]);
+        drain(dqt, dbt);
+      }
+      const float4 rr = rb ? ra[1] : ra[0], qq = rb ? qt[1] : qt[0], bb = rb ? bkt[1] : bkt[0];
+      const float rv[4] = {rr.x, rr.y, rr.z, rr.w}, qtv[4] = {qq.x, qq.y, qq.z, qq.w};
+      const float btv[4] = {bb.x, bb.y, bb.z, bb.w};
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int i = r0 + tile_row(r), il = i - pc.row0, d = dcol;
-            float sq = 0.f, sbk = 0.f;
-            for (int jl = 0; jl < P; ++jl) {
-              const int j = pc.col0 + jl;
-              const float E = expf(fminf(fmaxf(sG[i * LD + d] - sG[j * LD + d], -dc), dc));
-              const float ek = E * sKt[jl * LD + d];
-              sq += sDAq[i * LT + j] * ek;
-              sbk += sDA[i * LT + j] * ek;
-            }
-            const float x = scale * sq;
-            bq[m][r] += x;
-            bbk[m][r] += sbk;
-            bgc[m][r] += sQt[il * LD + d] * x + sBt[il * LD + d] * sbk;
-          }
+      for (int m = 0; m < NTW; ++m) {
+        if (St::rtile(wv, m) != ti) continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x = scale * dqt[e];
+          dq4[m][e] += x * rv[e];
+          dbk4[m][e] += dbt[e] * rv[e];
+          dgc4[m][e] += x * qtv[e] + dbt[e] * btv[e];
         }
-        if (r0 >= pc.col0 && r0 < pc.col0 + P) {
+      }
+    }
+    // columns of the piece: dk, dgc
+    for (int cb = 0; cb < nb; ++cb) {
+      const int tj = tc0 + cb;
+      if (!owned(tj)) continue;
+      f4 k1 = {0.f, 0.f, 0.f, 0.f}, k2 = {0.f, 0.f, 0.f, 0.f};
+      auto colop = [&](const float* base, int kb) {
+        const float* p = base + (pc.row0 + 16 * kb + 4 * g) * LT + 16 * tj + r;
+        return make_float4(p[0], p[LT], p[2 * LT], p[3 * LT]);
+      };
+      if (nb == 2) {
+        mma16<DOT_HIGHEST>(k1, colop(sDAq, 0), qt[0]);
+        mma16<DOT_HIGHEST>(k2, colop(sDA, 0), bkt[0]);
+        mma16<DOT_HIGHEST>(k1, colop(sDAq, 1), qt[1]);
+        mma16<DOT_HIGHEST>(k2, colop(sDA, 1), bkt[1]);
+        drain(k1, k2);
+      } else {
+        mma16<DOT_HIGHEST>(k1, colop(sDAq, 0), qt[0]);
+        mma16<DOT_HIGHEST>(k2, colop(sDA, 0), bkt[0]);
+        drain(k1, k2);
+      }
+      const float4 cc = cb ? cbl[1] : cbl[0], kk = cb ? kt[1] : kt[0];
+      const float cv[4] = {cc.x, cc.y, cc.z, cc.w}, ktv[4] = {kk.x, kk.y, kk.z, kk.w};
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int j = r0 + tile_row(r), jl = j - pc.col0, d = dcol;
-            float s = 0.f;
-            for (int il = 0; il < P; ++il) {
-              const int i = pc.row0 + il;
-              const float E = expf(fminf(fmaxf(sG[i * LD + d] - sG[j * LD + d], -dc), dc));
-              const float M = sDAq[i * LT + j] * (scale * sQt[il * LD + d]) + sDA[i * LT + j] * sBt[il * LD + d];
-              s += M * E;
+      for (int m = 0; m < NTW; ++m) {
+        if (St::rtile(wv, m) != tj) continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x = scale * k1[e] + k2[e];
+          dk4[m][e] += x * cv[e];
+          dgc4[m][e] -= x * ktv[e];
+        }
+      }
+    }
+  }
+
+  // lean diagonal blocks (b4.py:20-30): exact E = exp(clip(gc_i - gc_j, +-diff_clip)) per element
+  if (lean) {
+    for (int pi = 0; pi < cf.pieces.n; ++pi) {
+      const Piece pc = cf.pieces.p[pi];
+      if (pc.kind != 1) continue;
+      const float dc = cf.diff_clip;
+#pragma unroll
+      for (int m = 0; m < NTW; ++m) {
+        const int rt = St::rtile(wv, m);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int x = 16 * rt + 4 * g + e;      // row (as i) or column (as j) of the piece
+          const float gx = sG[x * LD + dcol];
+          if (x >= pc.row0 && x < pc.row0 + pc.P) {
+            float sq = 0.f, sbk = 0.f;
+            for (int jl = 0; jl < pc.P; ++jl) {
+              const int j = pc.col0 + jl;
+              const float E = expf(fminf(fmaxf(gx - sG[j * LD + dcol], -dc), dc));
+              const float ek = E * k[j * D + dcol];
+              sq += sDAq[x * LT + j] * ek;
+              sbk += sDA[x * LT + j] * ek;
             }
-            bk[m][r] += s;
-            bgc[m][r] -= sKt[jl * LD + d] * s;
+            const float xs = scale * sq, qx = q[x * D + dcol], bkx = b[x * D + dcol] * k[x * D + dcol];
+            dq4[m][e] += xs;
+            dbk4[m][e] += sbk;
+            dgc4[m][e] += qx * xs + bkx * sbk;
+          }
+          if (x >= pc.col0 && x < pc.col0 + pc.P) {
+            float s2 = 0.f;
+            for (int il = 0; il < pc.P; ++il) {
+              const int i = pc.row0 + il;
+              const float E = expf(fminf(fmaxf(sG[i * LD + dcol] - gx, -dc), dc));
+              const float M = sDAq[i * LT + x] * (scale * q[i * D + dcol]) + sDA[i * LT + x] * (b[i * D + dcol] * k[i * D + dcol]);
+              s2 += M * E;
+            }
+            dk4[m][e] += s2;
+            dgc4[m][e] -= k[x * D + dcol] * s2;
           }
         }
       }
     }
   }
-  __syncthreads();
 
-  // dkb = A^T dWp, dwv = A^T dv_new (mega.py:42), the gate gradients dq3/dk3/db3/dgc3
-  // (mega.py:45-51), and the combine with B4 (mega.py:52-59), tile by tile.
-  load_rows<LD>(sX, a.dwp + tb, T, D, tid, NT);
-  load_fragT<LD>(sY, a.dv_new_f + tb, D, T, 0, T, tid, NT);
+  // last-row decay gradient (mega.py:50): sum_i dkg kg [gl - gc < 0] + e^gamma sum_v(dh_next h_pre) [gl < 0]
+  const float gl = sG[(T - 1) * LD + dcol];
+  {
+    float part = 0.f;
+#pragma unroll
+    for (int m = 0; m < NTW; ++m) {
+      const int rt = St::rtile(wv, m), i0 = 16 * rt + 4 * g;
+      const float4 k4 = col4(k, rt);
+      const float ka[4] = {k4.x, k4.y, k4.z, k4.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float gi = sG[(i0 + e) * LD + dcol];
+        const float kgv = sanitize(ka[e] * exp_nonpos(gl - gi), clip);
+        const float mkg = (gl - gi) < 0.f ? 1.f : 0.f;
+        part += (a.dkg[tb + (i0 + e) * D + dcol] * kgv) * mkg;
+      }
+    }
+    part += __shfl_xor(part, 16);
+    part += __shfl_xor(part, 32);
+    if (g == 0) sColP[wv * 16 + r] = part;
+  }
   __syncthreads();
-  f4 dgcT[NTW];
+  float colsum = 0.f;
+  for (int w2 = strip; w2 < NW; w2 += St::NS) colsum += sColP[w2 * 16 + r];
+  {
+    const float dec = exp_nonpos(gl), mdec = gl < 0.f ? 1.f : 0.f;
+    colsum += dec * a.dlast[(size_t)chunk * D + dcol] * mdec;
+  }
+
+  // per owned tile: dkb = A^T dWp, dwv = A^T dv_new (mega.py:42; A^T is upper triangular, so
+  // row tile rt only sees k blocks >= rt), then the gate gradients (mega.py:45-51) and the
+  // combine with B4 (mega.py:52-59); dgc -> X1 for B5
+  float* sDgc = sX1;
 #pragma unroll
   for (int m = 0; m < NTW; ++m) {
-    const int rt = St::rtile(wv, m);
+    const int rt = St::rtile(wv, m), i0 = 16 * rt + 4 * g;
     f4 dkb = {0.f, 0.f, 0.f, 0.f}, dwv = {0.f, 0.f, 0.f, 0.f};
-    // A^T is upper triangular: rows of tile rt only see k >= 16*rt
-    const int k0 = 16 * rt;
-    mma_tile<B3>(dkb, tr(sA, LT).shift(16 * rt, k0), rm(sX, LD).shift(k0, strip * 16), T - k0);
-    mma_tile<B3>(dwv, tr(sA, LT).shift(16 * rt, k0), rm(sY, LD).shift(k0, strip * 16), T - k0);
+    for (int kb = rt; kb < 4; ++kb) {
+      const float* ac = sA + (16 * kb + 4 * g) * LT + 16 * rt + r;
+      const float4 av = make_float4(ac[0], ac[LT], ac[2 * LT], ac[3 * LT]);
+      const float* pv = sX2 + (16 * kb + 4 * g) * LD + dcol;
+      mma16<B3>(dkb, av, col4(dwp, kb));
+      mma16<B3>(dwv, av, make_float4(pv[0], pv[LD], pv[2 * LD], pv[3 * LD]));
+    }
+    drain(dkb, dwv);
+    const float4 q4 = col4(q, rt), k4 = col4(k, rt), b4 = col4(b, rt);
+    const float qa[4] = {q4.x, q4.y, q4.z, q4.w}, ka[4] = {k4.x, k4.y, k4.z, k4.w}, ba[4] = {b4.x, b4.y, b4.z, b4.w};
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = 16 * rt + tile_row(r), d = dcol, e = i * D + d;
-      const float ve = v[e], we = w[e], be = b[e], ke = k[e];
-      a.dw[tb + e] = sanitize(dwv[r] * ve, clip);     // mega.py:57
-      a.dv[tb + e] = sanitize(dwv[r] * we, clip);     // mega.py:58
-      const float gi = sG[i * LD + d], gl = sG[(T - 1) * LD + d];
+    for (int e = 0; e < 4; ++e) {
+      const int i = i0 + e, x = i * D + dcol;
+      const float ve = v[x], we = w[x], be = ba[e], ke = ka[e], qe = qa[e];
+      a.dw[tb + x] = sanitize(dwv[e] * ve, clip);     // mega.py:57
+      a.dv[tb + x] = sanitize(dwv[e] * we, clip);     // mega.py:58
+      const float gi = sG[i * LD + dcol];
       const float egc = exp_nonpos(gi), ekg = exp_nonpos(gl - gi);
       const float mgc = gi < 0.f ? 1.f : 0.f, mkg = (gl - gi) < 0.f ? 1.f : 0.f;
-      const float kb = (be * ke) * egc;
-      const float kg = sanitize(ke * ekg, clip), qg = sanitize(q[e] * egc, clip);
-      const float dqg = a.dqg[tb + e], dkg = a.dkg[tb + e];
+      const float kbv = (be * ke) * egc;
+      const float kg = sanitize(ke * ekg, clip), qg = sanitize(qe * egc, clip);
+      const float dqg = a.dqg[tb + x], dkg = a.dkg[tb + x];
       const float dx = dkg * kg;
       const float dq3 = dqg * egc;
-      const float dk3 = (dkb[r] * egc) * be + dkg * ekg;
-      const float db3 = (dkb[r] * egc) * ke;
-      float dgc3 = ((dkb[r] * kb) * mgc + (dqg * qg) * mgc) - dx * mkg;
-      dgc3 = sanitize(dgc3 + (i == T - 1 ? sCol[d] : 0.f), clip);
-      const float dqv = sanitize(bq[m][r], clip);
-      const float dbkv = sanitize(bbk[m][r], clip);
-      const float dk4 = sanitize(bk[m][r] + dbkv * be, clip);
-      const float db4 = sanitize(dbkv * ke, clip);
-      const float dgc4 = sanitize(bgc[m][r], clip);
-      a.dq[tb + e] = sanitize(dq3 + dqv, clip);
-      a.dk[tb + e] = sanitize(dk3 + dk4, clip);
-      a.db[tb + e] = sanitize(db3 + db4, clip);
-      dgcT[m][r] = dgc3 + dgc4;
+      const float dk3 = (dkb[e] * egc) * be + dkg * ekg;
+      const float db3 = (dkb[e] * egc) * ke;
+      float dgc3 = ((dkb[e] * kbv) * mgc + (dqg * qg) * mgc) - dx * mkg;
+      dgc3 = sanitize(dgc3 + (i == T - 1 ? colsum : 0.f), clip);
+      const float dqv = sanitize(dq4[m][e], clip);
+      const float dbkv = sanitize(dbk4[m][e], clip);
+      const float dk4v = sanitize(dk4[m][e] + dbkv * be, clip);
+      const float db4v = sanitize(dbkv * ke, clip);
+      const float dgc4v = sanitize(dgc4[m][e], clip);
+      a.dq[tb + x] = sanitize(dq3 + dqv, clip);
+      a.dk[tb + x] = sanitize(dk3 + dk4v, clip);
+      a.db[tb + x] = sanitize(db3 + db4v, clip);
+      sDgc[i * LD + dcol] = dgc3 + dgc4v;
     }
   }
   __syncthreads();
-  // B5: dg = reverse cumsum over the chunk rows of dgc3 + dgc4 (mega.py:53)
-  float* sDgc = sX;
-#pragma unroll
-  for (int m = 0; m < NTW; ++m) {
-    const int rt = St::rtile(wv, m);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) sDgc[(16 * rt + tile_row(r)) * LD + dcol] = dgcT[m][r];
-  }
-  __syncthreads();
+
+  // B5: dg = reverse cumsum over the chunk rows of dgc3 + dgc4 (mega.py:53).  Thread t owns
+  // float4 column t % (D/4) over a run of RUN rows; runs below are added in order.
   {
-    // reverse cumsum: column d split in NSEG runs of RUN rows
-    constexpr int NSEG = NT / D, RUN = T / NSEG;
-    const int d = tid % D, s = tid / D;
-    float acc = 0.f;
-    for (int i = RUN - 1; i >= 0; --i) {
-      const int row = s * RUN + i;
-      acc += sDgc[row * LD + d];
-      sY[row * LD + d] = acc;
-    }
+    constexpr int NQ = D / 4, NSEG = NT / NQ, RUN = T / NSEG;
+    const int d = 4 * (tid % NQ), sg = tid / NQ;
+    float4 x[RUN];
+#pragma unroll
+    for (int i = 0; i < RUN; ++i) x[i] = ld4(sDgc + (sg * RUN + i) * LD + d);
+#pragma unroll
+    for (int i = RUN - 2; i >= 0; --i) x[i] = add4(x[i + 1], x[i]);
+    float* sTot = sDA;                             // dAkk is no longer needed
+    st4(sTot + sg * LD + d, x[0]);                 // run totals
     __syncthreads();
-    float off = 0.f;
-    for (int s2 = NSEG - 1; s2 > s; --s2) off += sY[(s2 * RUN) * LD + d];
-    for (int i = 0; i < RUN; ++i) {
-      const int row = s * RUN + i;
-      a.dg[tb + row * D + d] = sanitize(sY[row * LD + d] + off, clip);
-    }
+    float4 off = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s2 = NSEG - 1; s2 > sg; --s2) off = add4(off, ld4(sTot + s2 * LD + d));
+#pragma unroll
+    for (int i = 0; i < RUN; ++i) st4(a.dg + tb + (sg * RUN + i) * D + d, san4(add4(x[i], off), clip));
   }
 }
 
