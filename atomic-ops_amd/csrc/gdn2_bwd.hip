@@ -92,8 +92,8 @@ __global__ __launch_bounds__(512) void bwd_state_kernel(BwdStateArgs a) {
 // the MFMA operands and the element-wise updates.
 //
 // Phases (LDS: gc | X1 | X2 | A | dAqk | dA/dAkk | column partial sums):
-//   P1 dAqk = (dO v_new^T) * causal                         X1 = v_new            (mega.py:32)
-//   P2 dA = san(dWp kb^T + dv_new (w v)^T)                   X1 = kb, X2 = dv_new  (mega.py:41)
+//   P1 dAqk = (dO v_new^T) * causal                 X1 = v_new, X2 = dO              (mega.py:32)
+//   P2 dA = san(dWp kb^T + dv_new (w v)^T)           X1 = kb / w v, X2 = dWp / dv_new (mega.py:41)
 //   P3 tmp = san(dA A^T)                                      X1 = tmp              (mega.py:43)
 //   P4 dAkk = san(-(1-eps) A^T tmp) * strict                                       (mega.py:44)
 //   B4 VJP of the two-level scores, piece by piece (owned tiles, registers)   (b4.py:45-97)
@@ -119,13 +119,14 @@ struct Strip {
   __device__ static int rtile(int w, int m) { return w / NS + m * STEP; }
 };
 
-// x[t] for a runtime t in [0, 4) without dynamic register indexing
+// x[t] for a runtime t in [0, 4) as selects over constant indices (no dynamic register
+// indexing, which would move the array to scratch memory)
+__device__ __forceinline__ float sel4(float a0, float a1, float a2, float a3, int t) {
+  return t == 0 ? a0 : (t == 1 ? a1 : (t == 2 ? a2 : a3));
+}
 __device__ __forceinline__ float4 pick4(const float4 (&x)[4], int t) {
-  float4 o = x[0];
-#pragma unroll
-  for (int u = 1; u < 4; ++u)
-    if (t == u) o = x[u];
-  return o;
+  return make_float4(sel4(x[0].x, x[1].x, x[2].x, x[3].x, t), sel4(x[0].y, x[1].y, x[2].y, x[3].y, t),
+                     sel4(x[0].z, x[1].z, x[2].z, x[3].z, t), sel4(x[0].w, x[1].w, x[2].w, x[3].w, t));
 }
 
 template <int D, int B3>
@@ -161,13 +162,24 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     return make_float4(p[0], p[D], p[2 * D], p[3 * D]);
   };
 
+  // T x D row-major global tile -> LDS (row stride LD), coalesced float4
+  auto copy_rows = [&](float* dst, const float* __restrict__ src) {
+    for (int f = tid; f < T * D / 4; f += NT) {
+      const int i = f / (D / 4), d = 4 * (f % (D / 4));
+      st4(dst + i * LD + d, ld4(src + i * D + d));
+    }
+  };
+
+  // X1 = v_new, X2 = dO, sA = A, sG = gc
   load_fragT<LD>(sX1, a.v_new_f + tb, D, T, 0, T, tid, NT);
-  chunk_cumsum<D, LD, NT>(a.g + tb, sG);          // ends with a barrier: sG, X1 ready
+  copy_rows(sX2, dout);
+  for (int f = tid; f < T * T / 4; f += NT) st4(sA + (f >> 4) * LT + 4 * (f & 15), ld4(a.A + sb + 4 * f));
+  chunk_cumsum<D, LD, NT>(a.g + tb, sG);          // ends with a barrier
 
   // P1: dAqk = (dO v_new^T) * causal
   for (int t = wv; t < 16; t += NW) {
     const int ti = t >> 2, tj = t & 3;
-    const float* ar = dout + (16 * ti + r) * D + 4 * g;
+    const float* ar = sX2 + (16 * ti + r) * LD + 4 * g;
     const float* br = sX1 + (16 * tj + r) * LD + 4 * g;
     f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -181,34 +193,45 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   }
   __syncthreads();
 
-  // P2 operands: X1 = kb = b k e^{min(gc,0)}, X2 = dv_new (kept for P5), sA = A
-  load_fragT<LD>(sX2, a.dv_new_f + tb, D, T, 0, T, tid, NT);
+  // P2: dA = san(dWp kb^T + dv_new (w v)^T), the two products with operands staged in turn:
+  //     X1 = kb = b k e^{min(gc,0)}, X2 = dWp; then X1 = w v, X2 = dv_new (kept for dwv)
   for (int f = tid; f < T * D / 4; f += NT) {
     const int i = f / (D / 4), d = 4 * (f % (D / 4));
     st4(sX1 + i * LD + d, mul4(mul4(ld4(b + i * D + d), ld4(k + i * D + d)), expnp4(ld4(sG + i * LD + d))));
   }
-  for (int f = tid; f < T * T / 4; f += NT) st4(sA + (f >> 4) * LT + 4 * (f & 15), ld4(a.A + sb + 4 * f));
+  copy_rows(sX2, dwp);
   __syncthreads();
-
-  // P2: dA = san(dWp kb^T + dv_new (w v)^T)
-  for (int t = wv; t < 16; t += NW) {
-    const int ti = t >> 2, tj = t & 3;
-    const float* a1 = dwp + (16 * ti + r) * D + 4 * g;
-    const float* b1 = sX1 + (16 * tj + r) * LD + 4 * g;
-    const float* a2 = sX2 + (16 * ti + r) * LD + 4 * g;
-    const float* wr = w + (16 * tj + r) * D + 4 * g;
-    const float* vr = v + (16 * tj + r) * D + 4 * g;
-    f4 acc1 = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
+  f4 accA[2];
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
-      mma16<B3>(acc1, ld4(a1 + 16 * kb), ld4(b1 + 16 * kb));
-      mma16<B3>(acc2, ld4(a2 + 16 * kb), mul4(ld4(wr + 16 * kb), ld4(vr + 16 * kb)));
-    }
-    drain(acc1, acc2);
+  for (int m2 = 0; m2 < 2; ++m2) {
+    const int t = wv + NW * m2, ti = t >> 2, tj = t & 3;
+    const float* ar = sX2 + (16 * ti + r) * LD + 4 * g;
+    const float* br = sX1 + (16 * tj + r) * LD + 4 * g;
+    accA[m2] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) sDA[(16 * ti + 4 * g + e) * LT + 16 * tj + r] = sanitize(acc1[e] + acc2[e], clip);
+    for (int kb = 0; kb < NKB; ++kb) mma16<B3>(accA[m2], ld4(ar + 16 * kb), ld4(br + 16 * kb));
+    drain(accA[m2]);
   }
-
+  __syncthreads();
+  for (int f = tid; f < T * D / 4; f += NT) {
+    const int i = f / (D / 4), d = 4 * (f % (D / 4));
+    st4(sX1 + i * LD + d, mul4(ld4(w + i * D + d), ld4(v + i * D + d)));
+  }
+  load_fragT<LD>(sX2, a.dv_new_f + tb, D, T, 0, T, tid, NT);
+  __syncthreads();
+#pragma unroll
+  for (int m2 = 0; m2 < 2; ++m2) {
+    const int t = wv + NW * m2, ti = t >> 2, tj = t & 3;
+    const float* ar = sX2 + (16 * ti + r) * LD + 4 * g;
+    const float* br = sX1 + (16 * tj + r) * LD + 4 * g;
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) mma16<B3>(acc, ld4(ar + 16 * kb), ld4(br + 16 * kb));
+    drain(acc);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      sDA[(16 * ti + 4 * g + e) * LT + 16 * tj + r] = sanitize(accA[m2][e] + acc[e], clip);
+  }
   __syncthreads();
 
   // P3: tmp = san(dA A^T) into X1 (as T x LT)
@@ -256,6 +279,14 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     dk4[m] = dq4[m];
     dgc4[m] = dq4[m];
   }
+  // q, k, b of this lane's column at the rows of all four row tiles (B4 and the gates)
+  float4 qv[4], kv[4], bv[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    qv[t] = col4(q, t);
+    kv[t] = col4(k, t);
+    bv[t] = col4(b, t);
+  }
   const bool lean = cf.diag == DIAG_LEAN;
   for (int pi = 0; pi < cf.pieces.n; ++pi) {
     const Piece pc = cf.pieces.p[pi];
@@ -275,9 +306,9 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
       }
       ra[kb] = make_float4(rv[0], rv[1], rv[2], rv[3]);
       cbl[kb] = make_float4(cv[0], cv[1], cv[2], cv[3]);
-      qt[kb] = mul4(col4(q, ti), ra[kb]);
-      bkt[kb] = mul4(mul4(col4(b, ti), col4(k, ti)), ra[kb]);
-      kt[kb] = mul4(col4(k, tj), cbl[kb]);
+      qt[kb] = mul4(pick4(qv, ti), ra[kb]);
+      bkt[kb] = mul4(mul4(pick4(bv, ti), pick4(kv, ti)), ra[kb]);
+      kt[kb] = mul4(pick4(kv, tj), cbl[kb]);
     }
     // rows of the piece: dq, dbk, dgc
     for (int rb = 0; rb < nb; ++rb) {
@@ -390,42 +421,24 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     }
   }
 
-  // last-row decay gradient (mega.py:50): sum_i dkg kg [gl - gc < 0] + e^gamma sum_v(dh_next h_pre) [gl < 0]
-  const float gl = sG[(T - 1) * LD + dcol];
-  {
-    float part = 0.f;
-#pragma unroll
-    for (int m = 0; m < NTW; ++m) {
-      const int rt = St::rtile(wv, m), i0 = 16 * rt + 4 * g;
-      const float4 k4 = col4(k, rt);
-      const float ka[4] = {k4.x, k4.y, k4.z, k4.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float gi = sG[(i0 + e) * LD + dcol];
-        const float kgv = sanitize(ka[e] * exp_nonpos(gl - gi), clip);
-        const float mkg = (gl - gi) < 0.f ? 1.f : 0.f;
-        part += (a.dkg[tb + (i0 + e) * D + dcol] * kgv) * mkg;
-      }
-    }
-    part += __shfl_xor(part, 16);
-    part += __shfl_xor(part, 32);
-    if (g == 0) sColP[wv * 16 + r] = part;
-  }
-  __syncthreads();
-  float colsum = 0.f;
-  for (int w2 = strip; w2 < NW; w2 += St::NS) colsum += sColP[w2 * 16 + r];
-  {
-    const float dec = exp_nonpos(gl), mdec = gl < 0.f ? 1.f : 0.f;
-    colsum += dec * a.dlast[(size_t)chunk * D + dcol] * mdec;
-  }
-
   // per owned tile: dkb = A^T dWp, dwv = A^T dv_new (mega.py:42; A^T is upper triangular, so
   // row tile rt only sees k blocks >= rt), then the gate gradients (mega.py:45-51) and the
-  // combine with B4 (mega.py:52-59); dgc -> X1 for B5
+  // combine with B4 (mega.py:52-59); dgc -> X1 for B5.  Row T-1 also needs the last-row decay
+  // term (mega.py:50), a sum over all rows: its dgc is finished after the loop.
+  const float* __restrict__ dqgp = a.dqg + tb;
+  const float* __restrict__ dkgp = a.dkg + tb;
+  float* __restrict__ o_dq = a.dq + tb;
+  float* __restrict__ o_dk = a.dk + tb;
+  float* __restrict__ o_db = a.db + tb;
+  float* __restrict__ o_dw = a.dw + tb;
+  float* __restrict__ o_dv = a.dv + tb;
   float* sDgc = sX1;
+  const float gl = sG[(T - 1) * LD + dcol];
+  float part = 0.f, fix3 = 0.f, fix4 = 0.f;
 #pragma unroll
   for (int m = 0; m < NTW; ++m) {
     const int rt = St::rtile(wv, m), i0 = 16 * rt + 4 * g;
+    const float4 w4 = col4(w, rt), v4 = col4(v, rt), dqg4 = col4(dqgp, rt), dkg4 = col4(dkgp, rt);
     f4 dkb = {0.f, 0.f, 0.f, 0.f}, dwv = {0.f, 0.f, 0.f, 0.f};
     for (int kb = rt; kb < 4; ++kb) {
       const float* ac = sA + (16 * kb + 4 * g) * LT + 16 * rt + r;
@@ -435,36 +448,56 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
       mma16<B3>(dwv, av, make_float4(pv[0], pv[LD], pv[2 * LD], pv[3 * LD]));
     }
     drain(dkb, dwv);
-    const float4 q4 = col4(q, rt), k4 = col4(k, rt), b4 = col4(b, rt);
+    const float4 q4 = pick4(qv, rt), k4 = pick4(kv, rt), b4 = pick4(bv, rt);
     const float qa[4] = {q4.x, q4.y, q4.z, q4.w}, ka[4] = {k4.x, k4.y, k4.z, k4.w}, ba[4] = {b4.x, b4.y, b4.z, b4.w};
+    const float wa[4] = {w4.x, w4.y, w4.z, w4.w}, va[4] = {v4.x, v4.y, v4.z, v4.w};
+    const float qga[4] = {dqg4.x, dqg4.y, dqg4.z, dqg4.w}, kga[4] = {dkg4.x, dkg4.y, dkg4.z, dkg4.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int i = i0 + e, x = i * D + dcol;
-      const float ve = v[x], we = w[x], be = ba[e], ke = ka[e], qe = qa[e];
-      a.dw[tb + x] = sanitize(dwv[e] * ve, clip);     // mega.py:57
-      a.dv[tb + x] = sanitize(dwv[e] * we, clip);     // mega.py:58
+      const float be = ba[e], ke = ka[e], qe = qa[e];
+      o_dw[x] = sanitize(dwv[e] * va[e], clip);     // mega.py:57
+      o_dv[x] = sanitize(dwv[e] * wa[e], clip);     // mega.py:58
       const float gi = sG[i * LD + dcol];
       const float egc = exp_nonpos(gi), ekg = exp_nonpos(gl - gi);
       const float mgc = gi < 0.f ? 1.f : 0.f, mkg = (gl - gi) < 0.f ? 1.f : 0.f;
       const float kbv = (be * ke) * egc;
       const float kg = sanitize(ke * ekg, clip), qg = sanitize(qe * egc, clip);
-      const float dqg = a.dqg[tb + x], dkg = a.dkg[tb + x];
+      const float dqg = qga[e], dkg = kga[e];
       const float dx = dkg * kg;
+      part += dx * mkg;
       const float dq3 = dqg * egc;
       const float dk3 = (dkb[e] * egc) * be + dkg * ekg;
       const float db3 = (dkb[e] * egc) * ke;
-      float dgc3 = ((dkb[e] * kbv) * mgc + (dqg * qg) * mgc) - dx * mkg;
-      dgc3 = sanitize(dgc3 + (i == T - 1 ? colsum : 0.f), clip);
+      const float dgc3 = ((dkb[e] * kbv) * mgc + (dqg * qg) * mgc) - dx * mkg;
       const float dqv = sanitize(dq4[m][e], clip);
       const float dbkv = sanitize(dbk4[m][e], clip);
       const float dk4v = sanitize(dk4[m][e] + dbkv * be, clip);
       const float db4v = sanitize(dbkv * ke, clip);
       const float dgc4v = sanitize(dgc4[m][e], clip);
-      a.dq[tb + x] = sanitize(dq3 + dqv, clip);
-      a.dk[tb + x] = sanitize(dk3 + dk4v, clip);
-      a.db[tb + x] = sanitize(db3 + db4v, clip);
-      sDgc[i * LD + dcol] = dgc3 + dgc4v;
+      o_dq[x] = sanitize(dq3 + dqv, clip);
+      o_dk[x] = sanitize(dk3 + dk4v, clip);
+      o_db[x] = sanitize(db3 + db4v, clip);
+      if (i == T - 1) {
+        fix3 = dgc3;
+        fix4 = dgc4v;
+      } else {
+        sDgc[i * LD + dcol] = sanitize(dgc3, clip) + dgc4v;
+      }
     }
+  }
+  // last-row decay gradient: sum over all rows of the column (lanes g, then the waves of the
+  // strip in order) + e^gamma sum_v(dh_next h_pre) [gl < 0]
+  part += __shfl_xor(part, 16);
+  part += __shfl_xor(part, 32);
+  if (g == 0) sColP[wv * 16 + r] = part;
+  __syncthreads();
+  if (owned(3) && g == 3) {
+    float colsum = 0.f;
+    for (int w2 = strip; w2 < NW; w2 += St::NS) colsum += sColP[w2 * 16 + r];
+    const float dec = exp_nonpos(gl), mdec = gl < 0.f ? 1.f : 0.f;
+    colsum += dec * a.dlast[(size_t)chunk * D + dcol] * mdec;
+    sDgc[(T - 1) * LD + dcol] = sanitize(fix3 + colsum, clip) + fix4;
   }
   __syncthreads();
 
