@@ -62,9 +62,10 @@ def make_blr_trainable(cfg, scale):
     class _Segment(torch.autograd.Function):
         @staticmethod
         def forward(ctx, q, k, v, w, b, g, h0):
-            dts = tuple(t.dtype for t in (q, k, v, w, b, g, h0))
+            # h0 None = zero initial state (the kernel takes a null pointer; no zero fill)
+            dts = tuple(t.dtype for t in (q, k, v, w, b, g)) + ((h0.dtype,) if h0 is not None else (torch.float32,))
             xs = [_f32(t) for t in (q, k, v, w, b, g)]
-            h0c = _f32(h0)
+            h0c = None if h0 is None else _f32(h0)
             B, H, L, D = xs[0].shape
             desc = _lib.make_desc(cfg, B, H, L, D, scale)
             dev = xs[0].device
@@ -106,7 +107,8 @@ def make_blr_trainable(cfg, scale):
                                        _lib.ptr(dv), _lib.ptr(dw), _lib.ptr(db), _lib.ptr(dg),
                                        _lib.ptr(dh0), _lib.ptr(ws), _lib.stream_handle(dev)), "gdn2_bwd")
             outs = (dq, dk, dv, dw, db, dg, dh0)
-            return tuple(_fin(x, dt, cfg) for x, dt in zip(outs, ctx.dts))
+            grads = tuple(_fin(x, dt, cfg) for x, dt in zip(outs, ctx.dts))
+            return grads if ctx.needs_input_grad[6] else grads[:6] + (None,)
 
     def call(q, k, v, w, b, g, h0=None):
         """q..g: (B,H,L,D), L % bt == 0. Returns (o (B,H,L,D) f32, h_final (B,H,D,D) f32)."""
@@ -115,8 +117,8 @@ def make_blr_trainable(cfg, scale):
         if L % cfg.bt:
             raise ValueError(f"L={L} must be divisible by bt={cfg.bt}")
         nc = L // cfg.bt
-        h = q.new_zeros((bsz, H, D, D), dtype=torch.float32) if h0 is None else h0
-        if h.shape != (bsz, H, D, D):
+        h = h0
+        if h is not None and h.shape != (bsz, H, D, D):
             raise ValueError(f"h0.shape={tuple(h.shape)} must be {(bsz, H, D, D)}")
         _check_device(q)
         outs = []

@@ -37,6 +37,10 @@ __device__ __forceinline__ float sanitize(float x, float c) {
 
 __device__ __forceinline__ float exp_nonpos(float x) { return expf(fminf(x, 0.f)); }
 
+// e^x as one hardware 2^y (v_exp_f32) of y = x log2(e): relative error ~1e-6 over the range
+// used (|x| < 88), for the many rescaling legs of the scores; element-wise gates keep expf.
+__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
+
 // ---- bfloat16 helpers: round-to-nearest-even, NaN kept quiet ------------------------
 __device__ __forceinline__ uint32_t bf16_bits(float x) {
   uint32_t u = __float_as_uint(x);

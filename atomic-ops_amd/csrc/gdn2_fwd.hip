@@ -30,20 +30,23 @@ struct WyLayout {
   static_assert(T * LT >= 8 * 16 * 20, "transpose scratch must fit in S");
 };
 
-// One 16x16 score tile of a piece: acc += sum_d (src[i][d] ra(i,d)) (k[j][d] cb(j,d)), where i
-// (j) is the A row (B column) of the calling lane.  Legs (fwd/scores.py:42-75):
+// One 16x16 tile position of a score piece, both matrices at once (they share the legs and
+// the B operand): accq += sum_d (q[i][d] ra) (k[j][d] cb), acck += sum_d (bk[i][d] ra) (k[j][d] cb),
+// where i (j) is the A row (B column) of the calling lane.  Legs (fwd/scores.py:42-75):
 //   KIND 0 (off-diagonal, anchor a): ra = e^{min(gc_i - gc_a, 0)}, cb = e^{min(gc_a - gc_j, 0)}
 //   KIND 1 (BTL diagonal block [s0, s1)): r = gc_s0, half = (gc_s0 - gc_{s1-1}) / 2,
 //          ra = e^{(gc_i - r) + half}, cb = e^{(r - gc_j) - half}
 template <int D, int LD, int DOT, int KIND>
-__device__ __forceinline__ void score_tile(f4& acc, const float* src, int sld, const float* __restrict__ kk,
-                                           const float* sG, const Piece& pc, int i, int j) {
+__device__ __forceinline__ void score_pair(f4& accq, f4& acck, const float* __restrict__ q, const float* sBK,
+                                           const float* __restrict__ kk, const float* sG, const Piece& pc, int i,
+                                           int j) {
   const int g = lane_id() >> 4;
   const float* gi = sG + i * LD;
   const float* gj = sG + j * LD;
   const float* ga = sG + (KIND == 0 ? pc.anchor : pc.s0) * LD;
   const float* gz = sG + (KIND == 0 ? pc.anchor : pc.s1 - 1) * LD;
-  const float* si = src + i * sld;
+  const float* qi = q + i * D;
+  const float* bi = sBK + i * LD;
   const float* kj = kk + j * D;
 #pragma unroll 2
   for (int kb = 0; kb < D / 16; ++kb) {
@@ -51,18 +54,22 @@ __device__ __forceinline__ void score_tile(f4& acc, const float* src, int sld, c
     const float4 vi = ld4(gi + d), vj = ld4(gj + d), va = ld4(ga + d);
     float4 ra, cb;
     if constexpr (KIND == 0) {
-      ra = expnp4(sub4(vi, va));
-      cb = expnp4(sub4(va, vj));
+      ra = make_float4(fast_exp(fminf(vi.x - va.x, 0.f)), fast_exp(fminf(vi.y - va.y, 0.f)),
+                       fast_exp(fminf(vi.z - va.z, 0.f)), fast_exp(fminf(vi.w - va.w, 0.f)));
+      cb = make_float4(fast_exp(fminf(va.x - vj.x, 0.f)), fast_exp(fminf(va.y - vj.y, 0.f)),
+                       fast_exp(fminf(va.z - vj.z, 0.f)), fast_exp(fminf(va.w - vj.w, 0.f)));
     } else {
       const float4 h = scale4(sub4(va, ld4(gz + d)), 0.5f);
-      ra = make_float4(expf((vi.x - va.x) + h.x), expf((vi.y - va.y) + h.y), expf((vi.z - va.z) + h.z),
-                       expf((vi.w - va.w) + h.w));
-      cb = make_float4(expf((va.x - vj.x) - h.x), expf((va.y - vj.y) - h.y), expf((va.z - vj.z) - h.z),
-                       expf((va.w - vj.w) - h.w));
+      ra = make_float4(fast_exp((vi.x - va.x) + h.x), fast_exp((vi.y - va.y) + h.y), fast_exp((vi.z - va.z) + h.z),
+                       fast_exp((vi.w - va.w) + h.w));
+      cb = make_float4(fast_exp((va.x - vj.x) - h.x), fast_exp((va.y - vj.y) - h.y), fast_exp((va.z - vj.z) - h.z),
+                       fast_exp((va.w - vj.w) - h.w));
     }
-    mma16<DOT>(acc, mul4(ld4(si + d), ra), mul4(ld4(kj + d), cb));
+    const float4 bv = mul4(ld4(kj + d), cb);
+    mma16<DOT>(accq, mul4(ld4(qi + d), ra), bv);
+    mma16<DOT>(acck, mul4(ld4(bi + d), ra), bv);
   }
-  drain(acc);
+  drain(accq, acck);
 }
 
 // Leaf inverses of the mb x mb diagonal blocks of (I + Se) by forward substitution
@@ -106,26 +113,40 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
   const float* __restrict__ v = a.v + tb;
   const int tid = threadIdx.x, wv = wave_id(), l = lane_id(), r = l & 15, g = l >> 4;
 
+  // row-fragment items of this thread (item f is lane f%64 of 16x16 block f/64, so fragment
+  // stores are contiguous); all raw inputs are loaded up front, before the cumsum's g
+  constexpr int NIT = T * D / 4 / NT;
+  float4 xk[NIT], xb[NIT], xw[NIT], xv[NIT], xq[NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int f = tid + it * NT, blk = f >> 6, ln = f & 63;
+    const int o = (16 * (blk / NKB) + (ln & 15)) * D + 16 * (blk % NKB) + 4 * (ln >> 4);
+    xk[it] = ld4(k + o);
+    xb[it] = ld4(b + o);
+    xw[it] = ld4(w + o);
+    xv[it] = ld4(v + o);
+    xq[it] = ld4(q + o);
+  }
+
   // 1. gc = cumsum(g) inside the chunk
   chunk_cumsum<D, LD, NT>(a.g + tb, sG);
 
   // 2a. row fragments (cd_slim.py:17-21): FA(Kg) with kg = san(k e^{min(gl-gc,0)}),
-  //     FA(Qg) with qg = san(q e^{min(gc,0)}); b*k and w*v into LDS.  Item f is lane f%64 of
-  //     block f/64, so the fragment stores are contiguous.
-  for (int f = tid; f < T * D / 4; f += NT) {
-    const int blk = f >> 6, ln = f & 63;
+  //     FA(Qg) with qg = san(q e^{min(gc,0)}); b*k and w*v into LDS.
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int f = tid + it * NT, blk = f >> 6, ln = f & 63;
     const int i = 16 * (blk / NKB) + (ln & 15), d = 16 * (blk % NKB) + 4 * (ln >> 4);
     const float4 gc = ld4(sG + i * LD + d);
-    const float4 kv = ld4(k + i * D + d);
-    st4(sBK + i * LD + d, mul4(ld4(b + i * D + d), kv));
-    st4(sY + i * LD + d, mul4(ld4(w + i * D + d), ld4(v + i * D + d)));
+    st4(sBK + i * LD + d, mul4(xb[it], xk[it]));
+    st4(sY + i * LD + d, mul4(xw[it], xv[it]));
     if (a.kg_f || a.kg) {
-      const float4 kg = san4(mul4(kv, expnp4(sub4(ld4(sG + (T - 1) * LD + d), gc))), clip);
+      const float4 kg = san4(mul4(xk[it], expnp4(sub4(ld4(sG + (T - 1) * LD + d), gc))), clip);
       if (a.kg_f) st4(a.kg_f + tb + 4 * f, kg);
       if (a.kg) st4(a.kg + tb + i * D + d, kg);
     }
     if (a.qg_f || a.qg) {
-      const float4 qg = san4(mul4(ld4(q + i * D + d), expnp4(gc)), clip);
+      const float4 qg = san4(mul4(xq[it], expnp4(gc)), clip);
       if (a.qg_f) st4(a.qg_f + tb + 4 * f, qg);
       if (a.qg) st4(a.qg + tb + i * D + d, qg);
     }
@@ -154,25 +175,22 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
 
   // 3. scores, all pieces at once (scores.py:42-75): Aqk = s (q ra)(k cb)^T, Akk = (bk ra)(k cb)^T
   {
-    const int np = cf.pieces.n, P = cf.pieces.p[0].P, nb = P / 16, tpm = nb * nb, tpp = 2 * tpm;
+    const int np = cf.pieces.n, P = cf.pieces.p[0].P, nb = P / 16, tpp = nb * nb;
     const bool lean = cf.diag == DIAG_LEAN;
     for (int t = wv; t < np * tpp; t += NW) {
       const Piece pc = cf.pieces.p[t / tpp];
       if (pc.kind == 1 && lean) continue;
-      const int rem = t % tpp, mat = rem / tpm, ti = (rem % tpm) / nb, tj = rem % nb;
+      const int rem = t % tpp, ti = rem / nb, tj = rem % nb;
       const int i = pc.row0 + 16 * ti + r, j = pc.col0 + 16 * tj + r;
-      f4 acc = {0.f, 0.f, 0.f, 0.f};
-      if (mat == 0) {
-        if (pc.kind == 0) score_tile<D, LD, DOT, 0>(acc, q, D, k, sG, pc, i, j);
-        else score_tile<D, LD, DOT, 1>(acc, q, D, k, sG, pc, i, j);
-      } else {
-        if (pc.kind == 0) score_tile<D, LD, DOT, 0>(acc, sBK, LD, k, sG, pc, i, j);
-        else score_tile<D, LD, DOT, 1>(acc, sBK, LD, k, sG, pc, i, j);
-      }
-      float* out = mat ? sK : sS;
-      const float mul = mat ? 1.f : cf.scale;
+      f4 accq = {0.f, 0.f, 0.f, 0.f}, acck = {0.f, 0.f, 0.f, 0.f};
+      if (pc.kind == 0) score_pair<D, LD, DOT, 0>(accq, acck, q, sBK, k, sG, pc, i, j);
+      else score_pair<D, LD, DOT, 1>(accq, acck, q, sBK, k, sG, pc, i, j);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) out[(pc.row0 + 16 * ti + 4 * g + e) * LT + pc.col0 + 16 * tj + r] = mul * acc[e];
+      for (int e = 0; e < 4; ++e) {
+        const int o = (pc.row0 + 16 * ti + 4 * g + e) * LT + pc.col0 + 16 * tj + r;
+        sS[o] = cf.scale * accq[e];
+        sK[o] = acck[e];
+      }
     }
     if (lean) {
       // lean diagonal (scores.py:34-39): exact exp(clip(gc_i - gc_j, +-diff_clip)) per element

@@ -94,20 +94,20 @@ hipError_t launch_bwd_wy(int D, const BwdWyArgs& a, hipStream_t s);
 hipError_t launch_gemm_probe(int mode, const float* A, const float* B, float* C, int M, int N,
                              int K, hipStream_t s);
 
-// Device-side leg factors of a score piece (used by the forward scores and by B4).
+// Device-side leg factors of a score piece (B4; the forward scores inline the same formulas).
 __device__ __forceinline__ float piece_row_leg(const Piece& pc, const float* sG, int LD, int i, int d) {
   const float gi = sG[i * LD + d];
-  if (pc.kind == 0) return exp_nonpos(gi - sG[pc.anchor * LD + d]);
+  if (pc.kind == 0) return fast_exp(fminf(gi - sG[pc.anchor * LD + d], 0.f));
   const float r = sG[pc.s0 * LD + d];
   const float half = 0.5f * (r - sG[(pc.s1 - 1) * LD + d]);
-  return expf((gi - r) + half);
+  return fast_exp((gi - r) + half);
 }
 __device__ __forceinline__ float piece_col_leg(const Piece& pc, const float* sG, int LD, int j, int d) {
   const float gj = sG[j * LD + d];
-  if (pc.kind == 0) return exp_nonpos(sG[pc.anchor * LD + d] - gj);
+  if (pc.kind == 0) return fast_exp(fminf(sG[pc.anchor * LD + d] - gj, 0.f));
   const float r = sG[pc.s0 * LD + d];
   const float half = 0.5f * (r - sG[(pc.s1 - 1) * LD + d]);
-  return expf((r - gj) - half);
+  return fast_exp((r - gj) - half);
 }
 
 }  // namespace gdn2
