@@ -24,7 +24,7 @@ RES_STORAGE = {"aqkT": ("T", "T", True, True), "A": ("T", "T", False, False),
                "h_pre": ("D", "D", True, True), "v_new": ("D", "T", True, True),
                "wpT": ("D", "T", True, True), "kg": ("T", "D", True, False),
                "qgT": ("D", "T", True, True), "gl": (None, "D", False, False)}
-KERNEL_NAMES = ("wy_fwd", "scan_fwd", "scan_bwd", "bwd_state", "bwd_wy", "out_fwd")
+KERNEL_NAMES = ("wy_fwd", "scan_fwd", "scan_bwd", "bwd_state", "bwd_wy", "out_fwd", "bwd_pre")
 STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported configuration", 3: "HIP error"}
 
 _c_int, _c_dbl, _c_size, _vp = ctypes.c_int32, ctypes.c_double, ctypes.c_size_t, ctypes.c_void_p

@@ -179,11 +179,11 @@ size_t gdn2_fwd_workspace_bytes(const gdn2_desc* d, int with_residual) {
   return n;
 }
 
-// backward workspace: [dv_new | dh_next | dqg | dwp | dkg | dlast]
+// backward workspace: [dv_new | dh_next | dqg | dwp | dkg | dlast | X | Y]
 size_t gdn2_bwd_workspace_bytes(const gdn2_desc* d) {
   if (validate(d)) return 0;
   const Dims x = dims(d);
-  return 4 * align_up(x.n_chunks * x.tD * 4) + align_up(x.n_chunks * x.DD * 4) +
+  return 5 * align_up(x.n_chunks * x.tD * 4) + 2 * align_up(x.n_chunks * x.DD * 4) +
          align_up(x.n_chunks * x.D * 4);
 }
 
@@ -274,10 +274,16 @@ int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v,
   float* dqg = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
   float* dwp = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
   float* dkg = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
-  float* dlast = at<float>(workspace, o2);
+  float* dlast = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.D * 4);
+  float* xo = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
+  float* yo = at<float>(workspace, o2);
 
-  gdn2::ScanBwdArgs sa{wpT, kg, qgT, gl, aqkT, d_o, d_hf, dvn, dhn, dh0, (int)x.nc, (int)x.n_bh, cfg};
-  hipError_t e = timed(2, s, [&] { return gdn2::launch_scan_bwd(d->D, sa, s); });
+  gdn2::BwdPreArgs pa{aqkT, qgT, d_o, xo, yo, (int)x.n_chunks, cfg};
+  hipError_t e = timed(6, s, [&] { return gdn2::launch_bwd_pre(d->D, pa, s); });
+  if (e != hipSuccess) return hip_fail(e, "bwd_pre launch");
+
+  gdn2::ScanBwdArgs sa{wpT, kg, gl, xo, yo, d_hf, dvn, dhn, dh0, (int)x.nc, (int)x.n_bh, cfg};
+  e = timed(2, s, [&] { return gdn2::launch_scan_bwd(d->D, sa, s); });
   if (e != hipSuccess) return hip_fail(e, "scan_bwd launch");
 
   gdn2::BwdStateArgs ba{d_o, dvn, vnew, hpre, dhn, dqg, dwp, dkg, dlast, (int)x.n_chunks, cfg};

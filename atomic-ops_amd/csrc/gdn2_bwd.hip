@@ -2,10 +2,13 @@
 // one reverse loop per (batch, head), bwd/mega.py:9-58; here the sequential part and the
 // chunk-parallel part are separate launches so that the chunk-parallel part fills the GPU).
 //
+//   bwd_pre_kernel   one workgroup per chunk: the reverse scan's dO terms Aqk^T dO and
+//                    Qg^T (s dO), which do not depend on the carried state     (mega.py:34-35)
 //   (the reverse state scan, dv_new and dh_next per chunk, is in gdn2_scan.hip)
 //   bwd_state_kernel one workgroup per chunk: the reductions over the value dimension
 //                      dQg = (s dO) h_pre^T, dWp = -dv_new h_pre^T, dKg = v_new dh_next^T
-//                    and the row sums sum_v dh_next * h_pre                 (mega.py:38-40,50)
+//                    (written as FA(dQg^T), FA(dWp^T), FA(dKg^T)) and the row sums
+//                    sum_v dh_next * h_pre                                    (mega.py:38-40,50)
 //   bwd_wy_kernel    one workgroup per chunk: dAqk, dA, dkb, dwv, the WY-inverse backward
 //                    dAkk = -(1-eps) strict(A^T (dA A^T)), the elementwise gate gradients,
 //                    B4 (VJP of the two-level scores) and B5 (reverse cumsum)
@@ -36,15 +39,15 @@ struct StateLayout {
 template <int D, int B3>
 __global__ __launch_bounds__(512) void bwd_state_kernel(BwdStateArgs a) {
   using Lay = StateLayout<D>;
-  constexpr int LD = Lay::LD, RB = Lay::RB, NT = 512, NW = 8;
-  __shared__ float smem[Lay::TOTAL];
+  constexpr int LD = Lay::LD, RB = Lay::RB, NT = 512, NW = 8, NKB = D / 16;
+  __shared__ __attribute__((aligned(16))) float smem[Lay::TOTAL];
   float* sdO = smem + Lay::OFF_DO;
   float* sDV = smem + Lay::OFF_DV;
   float* sVn = smem + Lay::OFF_VN;
   float* sHp = smem + Lay::OFF_HP;
   float* sDH = smem + Lay::OFF_DH;
   const Cfg& cf = a.cfg;
-  const int chunk = blockIdx.x, tid = threadIdx.x, wv = wave_id();
+  const int chunk = blockIdx.x, tid = threadIdx.x, wv = wave_id(), l = lane_id(), r = l & 15, g = l >> 4;
   const size_t tb = (size_t)chunk * T * D, hb = (size_t)chunk * D * D;
   load_rows<LD>(sdO, a.dout + tb, T, D, tid, NT);
   load_fragT<LD>(sDV, a.dv_new_f + tb, D, T, 0, T, tid, NT);
@@ -54,19 +57,20 @@ __global__ __launch_bounds__(512) void bwd_state_kernel(BwdStateArgs a) {
     load_fragT<LD>(sHp, a.h_pre_f + hb, D, D, rb * RB, RB, tid, NT);
     load_fragT<LD>(sDH, a.dh_next_f + hb, D, D, rb * RB, RB, tid, NT);
     __syncthreads();
-    // 3 outputs x 4 row tiles x 2 column tiles (this block of RB key rows)
-    for (int t = wv; t < 24; t += NW) {
-      const int mat = t / 8, ti = (t % 8) / 2, tj = t % 2;
+    // 3 outputs x 4 row tiles x (RB/16) key tiles of this block of key rows.  A operand: rows
+    // of s dO / -dv_new / v_new; B operand: key rows of h_pre / dh_next (value-contiguous).
+    // The accumulator of tile (ti, key tile kt) is block (kt, ti) of the output's FA(^T).
+    for (int t = wv; t < 3 * 4 * (RB / 16); t += NW) {
+      const int mat = t / (4 * (RB / 16)), ti = (t / (RB / 16)) % 4, tj = t % (RB / 16);
+      const float* pa = (mat == 0 ? sdO : mat == 1 ? sDV : sVn) + (16 * ti + r) * LD + 4 * g;
+      const float* pb = (mat == 2 ? sDH : sHp) + (16 * tj + r) * LD + 4 * g;
+      const float mul = mat == 0 ? cf.scale : (mat == 1 ? -1.f : 1.f);
       f4 acc = {0.f, 0.f, 0.f, 0.f};
-      const View A = mat == 0 ? rm(sdO, LD, cf.scale) : (mat == 1 ? rm(sDV, LD, -1.f) : rm(sVn, LD));
-      const View B = tr(mat == 2 ? sDH : sHp, LD);
-      mma_tile<B3>(acc, A.shift(ti * 16, 0), B.shift(0, tj * 16), D);
-      float* out = mat == 0 ? a.dqg : (mat == 1 ? a.dwp : a.dkg);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = ti * 16 + tile_row(r), d = rb * RB + tj * 16 + tile_col();
-        out[tb + i * D + d] = acc[r];
-      }
+      for (int kb = 0; kb < NKB; ++kb) mma16<B3>(acc, scale4(ld4(pa + 16 * kb), mul), ld4(pb + 16 * kb));
+      drain(acc);
+      float* out = mat == 0 ? a.dqg : (mat == 1 ? a.dwp : a.dkg);
+      st4(out + tb + frag_blk(rb * (RB / 16) + tj, ti, T) + 4 * l, f4_to_float4(acc));
     }
     // sum_v dh_next * h_pre for the RB key rows: 16 threads per row, then a fixed-order combine
     {
@@ -161,6 +165,8 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     const float* p = x + (16 * t + 4 * g) * D + dcol;
     return make_float4(p[0], p[D], p[2 * D], p[3 * D]);
   };
+  // the same for a T x D tensor stored as FA(x^T): one float4 of block (strip, t)
+  auto fcol4 = [&](const float* __restrict__ x, int t) { return ld4(x + frag_blk(strip, t, T) + 4 * l); };
 
   // T x D row-major global tile -> LDS (row stride LD), coalesced float4
   auto copy_rows = [&](float* dst, const float* __restrict__ src) {
@@ -199,7 +205,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     const int i = f / (D / 4), d = 4 * (f % (D / 4));
     st4(sX1 + i * LD + d, mul4(mul4(ld4(b + i * D + d), ld4(k + i * D + d)), expnp4(ld4(sG + i * LD + d))));
   }
-  copy_rows(sX2, dwp);
+  load_fragT<LD>(sX2, dwp, D, T, 0, T, tid, NT);
   __syncthreads();
   f4 accA[2];
 #pragma unroll
@@ -253,8 +259,10 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     const int ti = t >> 2, tj = t & 3;
     float ov[4] = {0.f, 0.f, 0.f, 0.f};
     if (tj <= ti) {
+      // full k range as one straight-line chain (the blocks kb < ti of A^T are exact zeros)
       f4 acc = {0.f, 0.f, 0.f, 0.f};
-      for (int kb = ti; kb < 4; ++kb) {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
         const float* ac = sA + (16 * kb + 4 * g) * LT + 16 * ti + r;
         const float* tc = sTmp + (16 * kb + 4 * g) * LT + 16 * tj + r;
         mma16<B3>(acc, make_float4(ac[0], ac[LT], ac[2 * LT], ac[3 * LT]),
@@ -438,13 +446,16 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
 #pragma unroll
   for (int m = 0; m < NTW; ++m) {
     const int rt = St::rtile(wv, m), i0 = 16 * rt + 4 * g;
-    const float4 w4 = col4(w, rt), v4 = col4(v, rt), dqg4 = col4(dqgp, rt), dkg4 = col4(dkgp, rt);
+    const float4 w4 = col4(w, rt), v4 = col4(v, rt), dqg4 = fcol4(dqgp, rt), dkg4 = fcol4(dkgp, rt);
     f4 dkb = {0.f, 0.f, 0.f, 0.f}, dwv = {0.f, 0.f, 0.f, 0.f};
-    for (int kb = rt; kb < 4; ++kb) {
+    // straight-line MFMA chain: skip the zero k blocks only where rt is a compile-time value
+    constexpr bool RT_STATIC = St::NS == NW;          // rt == m for every wave
+#pragma unroll
+    for (int kb = RT_STATIC ? m : 0; kb < 4; ++kb) {
       const float* ac = sA + (16 * kb + 4 * g) * LT + 16 * rt + r;
       const float4 av = make_float4(ac[0], ac[LT], ac[2 * LT], ac[3 * LT]);
       const float* pv = sX2 + (16 * kb + 4 * g) * LD + dcol;
-      mma16<B3>(dkb, av, col4(dwp, kb));
+      mma16<B3>(dkb, av, fcol4(dwp, kb));
       mma16<B3>(dwv, av, make_float4(pv[0], pv[LD], pv[2 * LD], pv[3 * LD]));
     }
     drain(dkb, dwv);
@@ -519,6 +530,78 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
 #pragma unroll
     for (int i = 0; i < RUN; ++i) st4(a.dg + tb + (sg * RUN + i) * D + d, san4(add4(x[i], off), clip));
   }
+}
+
+// ------------------------------------------------------------------------------------
+// bwd_pre: the reverse scan's dO terms for one chunk (mega.py:34-35), which do not depend on dh:
+//   X = Aqk^T dO (T x D),  Y = Qg^T (s dO) (D x D)
+// as MFMA tiles whose accumulators are exactly the fragment blocks the scan loads: tile
+// (tp, vb) of X is block (vb, tp) of FA(X^T), tile (kb, vb) of Y is block (vb, kb) of FA(Y^T).
+// A operands straight from FA(Aqk^T) / FA(Qg^T); the B operand (dO columns) from LDS.
+// ------------------------------------------------------------------------------------
+template <int D, int B3>
+__global__ __launch_bounds__(256) void bwd_pre_kernel(BwdPreArgs a) {
+  constexpr int LT = T + 4, NT = 256, NW = NT / WAVE, NVB = D / 16, NKB = D / 16, NYW = NKB / NW;
+  __shared__ __attribute__((aligned(16))) float sOT[D * LT];      // dO^T: [value][token]
+  const int chunk = blockIdx.x, tid = threadIdx.x, w = wave_id(), l = lane_id(), r = l & 15, g = l >> 4;
+  const size_t tb = (size_t)chunk * T * D, sb = (size_t)chunk * T * T, hb = (size_t)chunk * D * D;
+  const float* __restrict__ dout = a.dout + tb;
+  for (int f = tid; f < T * D / 4; f += NT) {
+    const int t = f / (D / 4), c = 4 * (f % (D / 4));
+    const float4 x = ld4(dout + t * D + c);
+    sOT[(c + 0) * LT + t] = x.x;
+    sOT[(c + 1) * LT + t] = x.y;
+    sOT[(c + 2) * LT + t] = x.z;
+    sOT[(c + 3) * LT + t] = x.w;
+  }
+  // A operands, loaded once per wave: X row block tp = w (all four k blocks: the blocks u < tp
+  // of Aqk^T are exact zeros), Y row blocks kb = w + NW m
+  float4 ax[4], ay[NYW][4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    ax[u] = ld4(a.aqkT_f + sb + frag_blk(w, u, T) + 4 * l);
+#pragma unroll
+    for (int m = 0; m < NYW; ++m) ay[m][u] = ld4(a.qgT_f + tb + frag_blk(w + NW * m, u, T) + 4 * l);
+  }
+  __syncthreads();
+  const float scale = a.cfg.scale;
+#pragma unroll 1
+  for (int vb = 0; vb < NVB; ++vb) {
+    // B operand: dO[16u + 4g + e][16 vb + r] = dO^T[16 vb + r][16u + 4g + e]; and s dO
+    float4 bo[4], bs[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      bo[u] = ld4(sOT + (16 * vb + r) * LT + 16 * u + 4 * g);
+      bs[u] = scale4(bo[u], scale);
+    }
+    f4 accx = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) mma16<B3>(accx, ax[u], bo[u]);
+    f4 accy[NYW];
+#pragma unroll
+    for (int m = 0; m < NYW; ++m) {
+      accy[m] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) mma16<B3>(accy[m], ay[m][u], bs[u]);
+    }
+    drain(accx);
+    st4(a.x_f + tb + frag_blk(vb, w, T) + 4 * l, f4_to_float4(accx));
+#pragma unroll
+    for (int m = 0; m < NYW; ++m) {
+      drain(accy[m]);
+      st4(a.y_f + hb + frag_blk(vb, w + NW * m, D) + 4 * l, f4_to_float4(accy[m]));
+    }
+  }
+}
+
+hipError_t launch_bwd_pre(int D, const BwdPreArgs& a, hipStream_t s) {
+  dispatch_mode(a.cfg.b3_mode, [&](auto m) {
+    constexpr int M = decltype(m)::value;
+    if (D == 128) hipLaunchKernelGGL((bwd_pre_kernel<128, M>), dim3(a.n_chunks), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((bwd_pre_kernel<64, M>), dim3(a.n_chunks), dim3(256), 0, s, a);
+    return 0;
+  });
+  return hipGetLastError();
 }
 
 hipError_t launch_bwd_state(int D, const BwdStateArgs& a, hipStream_t s) {

@@ -28,7 +28,9 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 typedef short s4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (WAVE - 1); }
-__device__ __forceinline__ int wave_id() { return threadIdx.x / WAVE; }
+// Wave index as a provably wave-uniform value (SGPR): branches on it stay scalar, so no
+// exec-mask merge (and no accumulator copy at such a merge) lands inside an MFMA chain.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE); }
 
 __device__ __forceinline__ float sanitize(float x, float c) {
   if (x != x) return 0.f;

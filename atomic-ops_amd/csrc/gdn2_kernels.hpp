@@ -58,15 +58,25 @@ struct OutFwdArgs {
   Cfg cfg;
 };
 
-// Reverse state scan: reads FA(Wp^T), FA(Kg), FA(Qg^T), FA(Aqk^T), gl, dO (row-major); writes
-// dv_new as FA(dv_new^T) (D x T), dh_next as FA(dh_next^T) (D x D), dh0 row-major.
+// The reverse scan's dO terms, chunk-parallel: X = Aqk^T dO as FA(X^T) (D x T) and
+// Y = s Qg^T dO as FA(Y^T) (D x D), from FA(Aqk^T), FA(Qg^T) and dO (row-major).
+struct BwdPreArgs {
+  const float *aqkT_f, *qgT_f, *dout;
+  float *x_f, *y_f;
+  int n_chunks;
+  Cfg cfg;
+};
+
+// Reverse state scan: reads FA(Wp^T), FA(Kg), gl, X, Y; writes dv_new as FA(dv_new^T)
+// (D x T), dh_next as FA(dh_next^T) (D x D), dh0 row-major.
 struct ScanBwdArgs {
-  const float *wpT_f, *kg_f, *qgT_f, *gl, *aqkT_f, *dout, *dhf;
+  const float *wpT_f, *kg_f, *gl, *x_f, *y_f, *dhf;
   float *dv_new_f, *dh_next_f, *dh0;
   int nc, n_bh;
   Cfg cfg;
 };
 
+// dqg / dwp / dkg are (T x D) per chunk, written as FA(dqg^T) / FA(dwp^T) / FA(dkg^T).
 struct BwdStateArgs {
   const float *dout, *dv_new_f, *v_new_f, *h_pre_f, *dh_next_f;
   float *dqg, *dwp, *dkg, *dlast;
@@ -85,6 +95,7 @@ struct BwdWyArgs {
 hipError_t launch_wy_fwd(int D, const WyFwdArgs& a, hipStream_t s);
 hipError_t launch_scan_fwd(int D, const ScanFwdArgs& a, hipStream_t s);
 hipError_t launch_out_fwd(int D, const OutFwdArgs& a, hipStream_t s);
+hipError_t launch_bwd_pre(int D, const BwdPreArgs& a, hipStream_t s);
 hipError_t launch_scan_bwd(int D, const ScanBwdArgs& a, hipStream_t s);
 hipError_t launch_bwd_state(int D, const BwdStateArgs& a, hipStream_t s);
 hipError_t launch_bwd_wy(int D, const BwdWyArgs& a, hipStream_t s);

@@ -35,7 +35,8 @@ def kernel_flops_per_token(T=T_, D=D_):
         "wy_fwd": 8 * T * D,                      # Aqk, Akk, Wp, U
         "scan_fwd": 4 * D * D,                    # Wp h, Kg^T v_new
         "out_fwd": 2 * T * D + 2 * D * D,         # Aqk v_new, Qg h_pre
-        "scan_bwd": 2 * T * D + 6 * D * D,        # Aqk^T dO; Kg dh, Qg^T dO, Wp^T dv_new
+        "bwd_pre": 2 * T * D + 2 * D * D,         # Aqk^T dO, Qg^T dO
+        "scan_bwd": 4 * D * D,                    # Kg dh, Wp^T dv_new
         "bwd_state": 6 * D * D,                   # dQg, dWp, dKg
         "bwd_wy": 18 * T * D + 4 * T * T,         # dAqk, dA, dkb, dwv, B4; dA A^T, A^T tmp
     }
