@@ -3,11 +3,12 @@
 Workload: (B,H,L,D) = (4,6,2048,128) fp32, chunk 64, wy_eps = 0,
 zero h0, synthetic seeded inputs (atomic_gdn2.synthetic); one step = forward + backward of
 sum(o^2) + sum(h_final^2) w.r.t. q, k, v, w, b, g, all dot modes 'highest' (fp32 MFMA).
+The timed loop runs K steps bracketed by device synchronisation, without profiling events.
 
 Prints ONE JSON line.  ``value`` is the canonical-FLOP throughput of the whole step in
 TFLOP/s (F_grad = B*H*L*(32*T*D + 18*D^2 + 4*T^2)); ``ms_per_step`` is the latency.
 ``roofline`` describes the dominant kernel, timed live with HIP events recorded on the launch
-stream by the library (gdn2_prof_begin / gdn2_prof_end).  ``cpu_baseline`` times the torch
+stream by the library (gdn2_prof_begin / gdn2_prof_end) in a second pass of K steps.  ``cpu_baseline`` times the torch
 float32 CPU restatement of the reference algorithm (oracle/gdn2_oracle.py) on a bounded
 sample of the same workload on the host cores.
 """
@@ -106,25 +107,29 @@ def main():
     fn = make_blr_trainable(cfg, scale)
 
     def step():
-        # loss = sum(o^2) + sum(h_final^2): its value by two dot reductions, and the gradient
-        # through the operator's VJP with the exact cotangents d loss/d o = 2 o, d loss/d hf = 2 hf
+        # gradient of loss = sum(o^2) + sum(h_final^2): forward, the loss's cotangents
+        # d loss/d o = 2 o and d loss/d h_final = 2 h_final, and the operator's VJP.  Like
+        # jax.grad of the same loss, the step returns the gradients only (the scalar loss value
+        # feeds nothing and is not formed).
         o, hf = fn(*xs)
-        loss = torch.dot(o.view(-1), o.view(-1)) + torch.dot(hf.view(-1), hf.view(-1))
-        grads = torch.autograd.grad((o, hf), xs, grad_outputs=(2.0 * o, 2.0 * hf))
-        return loss, grads
+        return torch.autograd.grad((o, hf), xs, grad_outputs=(2.0 * o, 2.0 * hf))
 
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
-    _lib.prof_begin(args.steps * len(_lib.KERNEL_NAMES) + 16)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    prof = _lib.prof_end()
     ms = dt * 1e3 / args.steps
+    # per-kernel durations: a separate pass with HIP events around every library launch
+    # (the events add gaps of their own, so the timed loop above runs without them)
+    _lib.prof_begin(args.steps * len(_lib.KERNEL_NAMES) + 16)
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    prof = _lib.prof_end()
 
     # forward-only (no residuals) throughput on the same inputs
     with torch.no_grad():
