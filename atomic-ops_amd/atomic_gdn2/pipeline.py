@@ -110,6 +110,30 @@ def make_blr_trainable(cfg, scale):
             grads = tuple(_fin(x, dt, cfg) for x, dt in zip(outs, ctx.dts))
             return grads if ctx.needs_input_grad[6] else grads[:6] + (None,)
 
+    def forward_only(xs, h0):
+        """No gradient needed: one kernel sequence over all L (no residual kept).  Equal bit for
+        bit to the segment loop, whose segments only bound the residual memory: the scan
+        carries the fp32 state across chunk boundaries exactly as through h0 / h_final.  bf16
+        inputs go to the kernels as they are (widened on load); other dtypes are cast to fp32."""
+        q = xs[0]
+        B, H, L, D = q.shape
+        dev = q.device
+        bf16 = all(t.dtype == torch.bfloat16 for t in xs)
+        xs = [t.contiguous() if bf16 else _f32(t) for t in xs]
+        h0c = None if h0 is None else _f32(h0)
+        desc = _lib.make_desc(cfg, B, H, L, D, scale)
+        o = torch.empty((B, H, L, D), dtype=torch.float32, device=dev)
+        hf = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
+        L_ = _lib.lib()
+        with torch.cuda.device(dev):
+            _lib.residual_layout(desc)                   # validates the descriptor
+            ws = torch.empty(L_.gdn2_fwd_workspace_bytes(ctypes.byref(desc), 0), dtype=torch.uint8, device=dev)
+            entry = L_.gdn2_fwd_bf16 if bf16 else L_.gdn2_fwd
+            _lib.check(entry(ctypes.byref(desc), *map(_lib.ptr, xs), _lib.ptr(h0c), _lib.ptr(o), _lib.ptr(hf),
+                             None, _lib.ptr(ws), _lib.stream_handle(dev)),
+                       "gdn2_fwd_bf16" if bf16 else "gdn2_fwd")
+        return o, hf
+
     def call(q, k, v, w, b, g, h0=None):
         """q..g: (B,H,L,D), L % bt == 0. Returns (o (B,H,L,D) f32, h_final (B,H,D,D) f32)."""
         _check_inputs((q, k, v, w, b, g), "qkvwbg")
@@ -121,6 +145,9 @@ def make_blr_trainable(cfg, scale):
         if h is not None and h.shape != (bsz, H, D, D):
             raise ValueError(f"h0.shape={tuple(h.shape)} must be {(bsz, H, D, D)}")
         _check_device(q)
+        xs = (q, k, v, w, b, g)
+        if not (torch.is_grad_enabled() and any(t.requires_grad for t in xs + ((h,) if h is not None else ()))):
+            return forward_only(xs, h)
         outs = []
         for s in range(0, nc, cfg.max_chunks_per_call):
             e = min(nc, s + cfg.max_chunks_per_call)

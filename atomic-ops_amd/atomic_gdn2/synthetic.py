@@ -41,3 +41,21 @@ def make_inputs(B: int, H: int, L: int, D: int, seed: int = 0, device="cuda", dt
     if dtype is not None:
         ts = tuple(t.to(dtype) for t in ts)
     return ts, scale
+
+
+def make_inputs_device(B: int, H: int, L: int, D: int, seed: int = 0, device="cuda", dtype=None):
+    """The same distributions drawn by torch's generator on ``device`` (for workloads too large
+    to draw on the host, e.g. the long-context forward): q, k, w L2-normalised rows, v ~ N(0,1),
+    b = sigmoid(N), g = -0.1 softplus(N); float32, cast to ``dtype`` if given."""
+    import torch
+    gen = torch.Generator(device=device).manual_seed(seed)
+    sh = (B, H, L, D)
+    q, k, v, w, b, g = (torch.randn(sh, generator=gen, device=device) for _ in range(6))
+    l2 = lambda x: x / torch.linalg.vector_norm(x, dim=-1, keepdim=True)
+    q, k, w = l2(q), l2(k), l2(w)
+    b = torch.sigmoid(b)
+    g = -0.1 * torch.nn.functional.softplus(g)
+    ts = (q, k, v, w, b, g)
+    if dtype is not None:
+        ts = tuple(t.to(dtype) for t in ts)
+    return ts, 1.0 / D ** 0.5

@@ -187,8 +187,12 @@ size_t gdn2_bwd_workspace_bytes(const gdn2_desc* d) {
          align_up(x.n_chunks * x.D * 4);
 }
 
-int gdn2_fwd(const gdn2_desc* d, const float* q, const float* k, const float* v, const float* w,
-             const float* b, const float* g, const float* h0, float* o, float* h_final, void* residual,
+}  // extern "C"
+
+namespace {
+// Forward of one segment; q..g are fp32 or (bf16 = true) bfloat16 bits.
+int fwd_impl(const gdn2_desc* d, const void* q, const void* k, const void* v, const void* w, const void* b,
+             const void* g, bool bf16, const float* h0, float* o, float* h_final, void* residual,
              void* workspace, void* stream) {
   int st = validate(d);
   if (st) return st;
@@ -231,7 +235,7 @@ int gdn2_fwd(const gdn2_desc* d, const float* q, const float* k, const float* v,
   wa.aqk_f = aqk; wa.aqkT_f = aqkT; wa.A = A; wa.gl = gl;
   wa.n_chunks = (int)x.n_chunks;
   wa.cfg = cfg;
-  hipError_t e = timed(0, s, [&] { return gdn2::launch_wy_fwd(d->D, wa, s); });
+  hipError_t e = timed(0, s, [&] { return gdn2::launch_wy_fwd(d->D, wa, s, bf16); });
   if (e != hipSuccess) return hip_fail(e, "wy_fwd launch");
 
   gdn2::ScanFwdArgs sa{wp, kgT, uT, gl, h0, h_final, hpre, vnew, (int)x.nc, (int)x.n_bh, cfg};
@@ -242,6 +246,21 @@ int gdn2_fwd(const gdn2_desc* d, const float* q, const float* k, const float* v,
   e = timed(5, s, [&] { return gdn2::launch_out_fwd(d->D, oa, s); });
   if (e != hipSuccess) return hip_fail(e, "out_fwd launch");
   return GDN2_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int gdn2_fwd(const gdn2_desc* d, const float* q, const float* k, const float* v, const float* w,
+             const float* b, const float* g, const float* h0, float* o, float* h_final, void* residual,
+             void* workspace, void* stream) {
+  return fwd_impl(d, q, k, v, w, b, g, false, h0, o, h_final, residual, workspace, stream);
+}
+
+int gdn2_fwd_bf16(const gdn2_desc* d, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                  const uint16_t* w, const uint16_t* b, const uint16_t* g, const float* h0, float* o,
+                  float* h_final, void* residual, void* workspace, void* stream) {
+  return fwd_impl(d, q, k, v, w, b, g, true, h0, o, h_final, residual, workspace, stream);
 }
 
 int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v, const float* w,

@@ -182,6 +182,30 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   for (int f = tid; f < T * T / 4; f += NT) st4(sA + (f >> 4) * LT + 4 * (f & 15), ld4(a.A + sb + 4 * f));
   chunk_cumsum<D, LD, NT>(a.g + tb, sG);          // ends with a barrier
 
+  // the P2 operands' global loads are issued now, so that they overlap P1: item f of the
+  // row-major inputs is float4 f; item f of a FRAG(x^T) input is float4 f as well, landing at
+  // row 16 (f/256 % 4) + 4 (f%64 / 16) + e, column 16 (f / 1024) + f % 16 of the row-major tile
+  constexpr int NIT = T * D / 4 / NT;
+  float4 xb[NIT], xk[NIT], xw[NIT], xv[NIT], xdw[NIT], xdv[NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int f = tid + it * NT;
+    xb[it] = ld4(b + 4 * f);
+    xk[it] = ld4(k + 4 * f);
+    xw[it] = ld4(w + 4 * f);
+    xv[it] = ld4(v + 4 * f);
+    xdw[it] = ld4(dwp + 4 * f);
+    xdv[it] = ld4(a.dv_new_f + tb + 4 * f);
+  }
+  auto put_fragT = [&](float* dst, const float4& x, int f) {
+    const int lane = f & 63, blk = f >> 6;
+    const int n = 16 * (blk >> 2) + (lane & 15), m = 16 * (blk & 3) + 4 * (lane >> 4);
+    dst[(m + 0) * LD + n] = x.x;
+    dst[(m + 1) * LD + n] = x.y;
+    dst[(m + 2) * LD + n] = x.z;
+    dst[(m + 3) * LD + n] = x.w;
+  };
+
   // P1: dAqk = (dO v_new^T) * causal
   for (int t = wv; t < 16; t += NW) {
     const int ti = t >> 2, tj = t & 3;
@@ -201,11 +225,12 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
 
   // P2: dA = san(dWp kb^T + dv_new (w v)^T), the two products with operands staged in turn:
   //     X1 = kb = b k e^{min(gc,0)}, X2 = dWp; then X1 = w v, X2 = dv_new (kept for dwv)
-  for (int f = tid; f < T * D / 4; f += NT) {
-    const int i = f / (D / 4), d = 4 * (f % (D / 4));
-    st4(sX1 + i * LD + d, mul4(mul4(ld4(b + i * D + d), ld4(k + i * D + d)), expnp4(ld4(sG + i * LD + d))));
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int f = tid + it * NT, i = f / (D / 4), d = 4 * (f % (D / 4));
+    st4(sX1 + i * LD + d, mul4(mul4(xb[it], xk[it]), expnp4(ld4(sG + i * LD + d))));
+    put_fragT(sX2, xdw[it], f);
   }
-  load_fragT<LD>(sX2, dwp, D, T, 0, T, tid, NT);
   __syncthreads();
   f4 accA[2];
 #pragma unroll
@@ -219,11 +244,12 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     drain(accA[m2]);
   }
   __syncthreads();
-  for (int f = tid; f < T * D / 4; f += NT) {
-    const int i = f / (D / 4), d = 4 * (f % (D / 4));
-    st4(sX1 + i * LD + d, mul4(ld4(w + i * D + d), ld4(v + i * D + d)));
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int f = tid + it * NT, i = f / (D / 4), d = 4 * (f % (D / 4));
+    st4(sX1 + i * LD + d, mul4(xw[it], xv[it]));
+    put_fragT(sX2, xdv[it], f);
   }
-  load_fragT<LD>(sX2, a.dv_new_f + tb, D, T, 0, T, tid, NT);
   __syncthreads();
 #pragma unroll
   for (int m2 = 0; m2 < 2; ++m2) {
@@ -239,6 +265,16 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
       sDA[(16 * ti + 4 * g + e) * LT + 16 * tj + r] = sanitize(accA[m2][e] + acc[e], clip);
   }
   __syncthreads();
+
+  // q, k, b of this lane's column at the rows of all four row tiles (B4 and the gates),
+  // loaded here so that they arrive during P3 / P4
+  float4 qv[4], kv[4], bv[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    qv[t] = col4(q, t);
+    kv[t] = col4(k, t);
+    bv[t] = col4(b, t);
+  }
 
   // P3: tmp = san(dA A^T) into X1 (as T x LT)
   float* sTmp = sX1;
@@ -286,14 +322,6 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     dbk4[m] = dq4[m];
     dk4[m] = dq4[m];
     dgc4[m] = dq4[m];
-  }
-  // q, k, b of this lane's column at the rows of all four row tiles (B4 and the gates)
-  float4 qv[4], kv[4], bv[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    qv[t] = col4(q, t);
-    kv[t] = col4(k, t);
-    bv[t] = col4(b, t);
   }
   const bool lean = cf.diag == DIAG_LEAN;
   for (int pi = 0; pi < cf.pieces.n; ++pi) {

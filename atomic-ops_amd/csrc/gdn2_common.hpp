@@ -191,6 +191,17 @@ __device__ __forceinline__ void mma16(f4& acc, const float4& a, const float4& b)
 __device__ __forceinline__ float4 f4_to_float4(const f4& x) { return make_float4(x[0], x[1], x[2], x[3]); }
 __device__ __forceinline__ float4 scale4(const float4& x, float s) { return make_float4(s * x.x, s * x.y, s * x.z, s * x.w); }
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+
+// Raw operator inputs are fp32 or bfloat16 (stored as uint16_t bits); the kernels widen them
+// to fp32 on load and compute in fp32 from there.
+__device__ __forceinline__ float in_val(const float* p) { return *p; }
+__device__ __forceinline__ float in_val(const uint16_t* p) { return __uint_as_float((uint32_t)*p << 16); }
+__device__ __forceinline__ float4 in_ld4(const float* p) { return ld4(p); }
+__device__ __forceinline__ float4 in_ld4(const uint16_t* p) {
+  const uint2 u = *reinterpret_cast<const uint2*>(p);
+  return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                     __uint_as_float(u.y & 0xffff0000u));
+}
 __device__ __forceinline__ void st4(float* p, const float4& x) { *reinterpret_cast<float4*>(p) = x; }
 
 template <int MODE>
@@ -297,14 +308,14 @@ __device__ __forceinline__ void load_fragT(float* dst, const float* __restrict__
 // Thread t owns float4 column t % (D/4) over a run of RUN consecutive rows: it sums its run,
 // then adds the totals of the runs above it in order.  Same code in every kernel, so every
 // kernel sees bit-identical gc.
-template <int D, int LD, int NTHREADS>
-__device__ __forceinline__ void chunk_cumsum(const float* __restrict__ g, float* sG) {
+template <int D, int LD, int NTHREADS, typename TIn>
+__device__ __forceinline__ void chunk_cumsum(const TIn* __restrict__ g, float* sG) {
   constexpr int NQ = D / 4, NSEG = NTHREADS / NQ, RUN = T / NSEG;
   static_assert(NTHREADS % NQ == 0 && T % NSEG == 0 && RUN >= 1, "cumsum split");
   const int t = threadIdx.x, d = 4 * (t % NQ), s = t / NQ;
   float4 x[RUN];
 #pragma unroll
-  for (int i = 0; i < RUN; ++i) x[i] = ld4(g + (s * RUN + i) * D + d);
+  for (int i = 0; i < RUN; ++i) x[i] = in_ld4(g + (s * RUN + i) * D + d);
 #pragma unroll
   for (int i = 1; i < RUN; ++i) x[i] = add4(x[i - 1], x[i]);
   st4(sG + (s * RUN + RUN - 1) * LD + d, x[RUN - 1]);

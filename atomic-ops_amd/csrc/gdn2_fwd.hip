@@ -7,6 +7,7 @@
 //                   leaf forward substitution in registers + block doubling (MFMA for blocks
 //                   of 16 and up), then Wp = A (b k e^gc) and U = A (w v) on MFMA.
 //                   Semantics: fwd/scores.py:42-87, fwd/solve.py:9-48, fwd/cd_slim.py:14-21.
+//                   The raw inputs are fp32 or bfloat16 (template TIn), widened to fp32 on load.
 //   out_fwd_kernel  one workgroup per chunk after the state scan:
 //                   o = san(s Qg h_pre + Aqk v_new)                   (fwd/cd_slim.py:24-27)
 //   (the forward state scan is in gdn2_scan.hip)
@@ -36,18 +37,18 @@ struct WyLayout {
 //   KIND 0 (off-diagonal, anchor a): ra = e^{min(gc_i - gc_a, 0)}, cb = e^{min(gc_a - gc_j, 0)}
 //   KIND 1 (BTL diagonal block [s0, s1)): r = gc_s0, half = (gc_s0 - gc_{s1-1}) / 2,
 //          ra = e^{(gc_i - r) + half}, cb = e^{(r - gc_j) - half}
-template <int D, int LD, int DOT, int KIND>
-__device__ __forceinline__ void score_pair(f4& accq, f4& acck, const float* __restrict__ q, const float* sBK,
-                                           const float* __restrict__ kk, const float* sG, const Piece& pc, int i,
+template <int D, int LD, int DOT, int KIND, typename TIn>
+__device__ __forceinline__ void score_pair(f4& accq, f4& acck, const TIn* __restrict__ q, const float* sBK,
+                                           const TIn* __restrict__ kk, const float* sG, const Piece& pc, int i,
                                            int j) {
   const int g = lane_id() >> 4;
   const float* gi = sG + i * LD;
   const float* gj = sG + j * LD;
   const float* ga = sG + (KIND == 0 ? pc.anchor : pc.s0) * LD;
   const float* gz = sG + (KIND == 0 ? pc.anchor : pc.s1 - 1) * LD;
-  const float* qi = q + i * D;
+  const TIn* qi = q + i * D;
   const float* bi = sBK + i * LD;
-  const float* kj = kk + j * D;
+  const TIn* kj = kk + j * D;
 #pragma unroll 2
   for (int kb = 0; kb < D / 16; ++kb) {
     const int d = 16 * kb + 4 * g;
@@ -65,8 +66,8 @@ __device__ __forceinline__ void score_pair(f4& accq, f4& acck, const float* __re
       cb = make_float4(fast_exp((va.x - vj.x) - h.x), fast_exp((va.y - vj.y) - h.y), fast_exp((va.z - vj.z) - h.z),
                        fast_exp((va.w - vj.w) - h.w));
     }
-    const float4 bv = mul4(ld4(kj + d), cb);
-    mma16<DOT>(accq, mul4(ld4(qi + d), ra), bv);
+    const float4 bv = mul4(in_ld4(kj + d), cb);
+    mma16<DOT>(accq, mul4(in_ld4(qi + d), ra), bv);
     mma16<DOT>(acck, mul4(ld4(bi + d), ra), bv);
   }
   drain(accq, acck);
@@ -90,7 +91,7 @@ __device__ __forceinline__ void leaf_solve(const float* sSe, float* sI, int tid)
   for (int i = 0; i < MB; ++i) sI[(base + i) * LT + base + c] = x[i];
 }
 
-template <int D, int DOT>
+template <int D, int DOT, typename TIn>
 __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
   using Lay = WyLayout<D>;
   constexpr int LD = Lay::LD, LT = Lay::LT, NT = 512, NW = NT / WAVE, NKB = D / 16;
@@ -106,11 +107,11 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
   const int chunk = blockIdx.x;
   const size_t tb = (size_t)chunk * T * D;
   const size_t sb = (size_t)chunk * T * T;
-  const float* __restrict__ q = a.q + tb;
-  const float* __restrict__ k = a.k + tb;
-  const float* __restrict__ b = a.b + tb;
-  const float* __restrict__ w = a.w + tb;
-  const float* __restrict__ v = a.v + tb;
+  const TIn* __restrict__ q = static_cast<const TIn*>(a.q) + tb;
+  const TIn* __restrict__ k = static_cast<const TIn*>(a.k) + tb;
+  const TIn* __restrict__ b = static_cast<const TIn*>(a.b) + tb;
+  const TIn* __restrict__ w = static_cast<const TIn*>(a.w) + tb;
+  const TIn* __restrict__ v = static_cast<const TIn*>(a.v) + tb;
   const int tid = threadIdx.x, wv = wave_id(), l = lane_id(), r = l & 15, g = l >> 4;
 
   // row-fragment items of this thread (item f is lane f%64 of 16x16 block f/64, so fragment
@@ -121,15 +122,15 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
   for (int it = 0; it < NIT; ++it) {
     const int f = tid + it * NT, blk = f >> 6, ln = f & 63;
     const int o = (16 * (blk / NKB) + (ln & 15)) * D + 16 * (blk % NKB) + 4 * (ln >> 4);
-    xk[it] = ld4(k + o);
-    xb[it] = ld4(b + o);
-    xw[it] = ld4(w + o);
-    xv[it] = ld4(v + o);
-    xq[it] = ld4(q + o);
+    xk[it] = in_ld4(k + o);
+    xb[it] = in_ld4(b + o);
+    xw[it] = in_ld4(w + o);
+    xv[it] = in_ld4(v + o);
+    xq[it] = in_ld4(q + o);
   }
 
   // 1. gc = cumsum(g) inside the chunk
-  chunk_cumsum<D, LD, NT>(a.g + tb, sG);
+  chunk_cumsum<D, LD, NT>(static_cast<const TIn*>(a.g) + tb, sG);
 
   // 2a. row fragments (cd_slim.py:17-21): FA(Kg) with kg = san(k e^{min(gl-gc,0)}),
   //     FA(Qg) with qg = san(q e^{min(gc,0)}); b*k and w*v into LDS.
@@ -163,8 +164,8 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
       for (int e = 0; e < 4; ++e) {
         const int i = i0 + e;
         const float gi = sG[i * LD + d];
-        kt[e] = sanitize(k[i * D + d] * exp_nonpos(gl - gi), clip);
-        qt[e] = sanitize(q[i * D + d] * exp_nonpos(gi), clip);
+        kt[e] = sanitize(in_val(k + i * D + d) * exp_nonpos(gl - gi), clip);
+        qt[e] = sanitize(in_val(q + i * D + d) * exp_nonpos(gi), clip);
       }
       if (a.kgT_f) st4(a.kgT_f + tb + 4 * f, make_float4(kt[0], kt[1], kt[2], kt[3]));
       if (a.qgT_f) st4(a.qgT_f + tb + 4 * f, make_float4(qt[0], qt[1], qt[2], qt[3]));
@@ -183,8 +184,8 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
       const int rem = t % tpp, ti = rem / nb, tj = rem % nb;
       const int i = pc.row0 + 16 * ti + r, j = pc.col0 + 16 * tj + r;
       f4 accq = {0.f, 0.f, 0.f, 0.f}, acck = {0.f, 0.f, 0.f, 0.f};
-      if (pc.kind == 0) score_pair<D, LD, DOT, 0>(accq, acck, q, sBK, k, sG, pc, i, j);
-      else score_pair<D, LD, DOT, 1>(accq, acck, q, sBK, k, sG, pc, i, j);
+      if (pc.kind == 0) score_pair<D, LD, DOT, 0, TIn>(accq, acck, q, sBK, k, sG, pc, i, j);
+      else score_pair<D, LD, DOT, 1, TIn>(accq, acck, q, sBK, k, sG, pc, i, j);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int o = (pc.row0 + 16 * ti + 4 * g + e) * LT + pc.col0 + 16 * tj + r;
@@ -203,8 +204,8 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
           float sq = 0.f, sk = 0.f;
           for (int d = 0; d < D; ++d) {
             const float E = expf(fminf(fmaxf(sG[row * LD + d] - sG[col * LD + d], -dc), dc));
-            const float kj = k[col * D + d];
-            sq += (q[row * D + d] * E) * kj;
+            const float kj = in_val(k + col * D + d);
+            sq += (in_val(q + row * D + d) * E) * kj;
             sk += (sBK[row * LD + d] * E) * kj;
           }
           sS[row * LT + col] = cf.scale * sq;
@@ -435,11 +436,16 @@ hipError_t launch_gemm_probe(int mode, const float* A, const float* B, float* C,
   return hipGetLastError();
 }
 
-hipError_t launch_wy_fwd(int D, const WyFwdArgs& a, hipStream_t s) {
+hipError_t launch_wy_fwd(int D, const WyFwdArgs& a, hipStream_t s, bool bf16_inputs) {
   dispatch_mode(a.cfg.dot_mode, [&](auto m) {
     constexpr int M = decltype(m)::value;
-    if (D == 128) hipLaunchKernelGGL((wy_fwd_kernel<128, M>), dim3(a.n_chunks), dim3(512), 0, s, a);
-    else hipLaunchKernelGGL((wy_fwd_kernel<64, M>), dim3(a.n_chunks), dim3(512), 0, s, a);
+    if (bf16_inputs) {
+      if (D == 128) hipLaunchKernelGGL((wy_fwd_kernel<128, M, uint16_t>), dim3(a.n_chunks), dim3(512), 0, s, a);
+      else hipLaunchKernelGGL((wy_fwd_kernel<64, M, uint16_t>), dim3(a.n_chunks), dim3(512), 0, s, a);
+    } else {
+      if (D == 128) hipLaunchKernelGGL((wy_fwd_kernel<128, M, float>), dim3(a.n_chunks), dim3(512), 0, s, a);
+      else hipLaunchKernelGGL((wy_fwd_kernel<64, M, float>), dim3(a.n_chunks), dim3(512), 0, s, a);
+    }
     return 0;
   });
   return hipGetLastError();

@@ -32,7 +32,7 @@ struct Cfg {
 //   aqk / akk / wp / u / kg / qg are written only for the stage-level entry point.  Any
 //   pointer may be null (not written).
 struct WyFwdArgs {
-  const float *q, *k, *v, *w, *b, *g;
+  const void *q, *k, *v, *w, *b, *g;   // fp32, or bfloat16 bits for the bf16-input variant
   float *wp_f, *wpT_f, *uT_f, *kg_f, *kgT_f, *qg_f, *qgT_f, *aqk_f, *aqkT_f;
   float *A, *gl;
   float *aqk, *akk, *wp, *u, *kg, *qg;
@@ -92,7 +92,7 @@ struct BwdWyArgs {
   Cfg cfg;
 };
 
-hipError_t launch_wy_fwd(int D, const WyFwdArgs& a, hipStream_t s);
+hipError_t launch_wy_fwd(int D, const WyFwdArgs& a, hipStream_t s, bool bf16_inputs = false);
 hipError_t launch_scan_fwd(int D, const ScanFwdArgs& a, hipStream_t s);
 hipError_t launch_out_fwd(int D, const OutFwdArgs& a, hipStream_t s);
 hipError_t launch_bwd_pre(int D, const BwdPreArgs& a, hipStream_t s);

@@ -8,9 +8,13 @@ The timed loop runs K steps bracketed by device synchronisation, without profili
 Prints ONE JSON line.  ``value`` is the canonical-FLOP throughput of the whole step in
 TFLOP/s (F_grad = B*H*L*(32*T*D + 18*D^2 + 4*T^2)); ``ms_per_step`` is the latency.
 ``roofline`` describes the dominant kernel, timed live with HIP events recorded on the launch
-stream by the library (gdn2_prof_begin / gdn2_prof_end) in a second pass of K steps.  ``cpu_baseline`` times the torch
-float32 CPU restatement of the reference algorithm (oracle/gdn2_oracle.py) on a bounded
-sample of the same workload on the host cores.
+stream by the library (gdn2_prof_begin / gdn2_prof_end) in a second pass of K steps.
+``cpu_baseline`` times the torch float32 CPU restatement of the reference algorithm
+(oracle/gdn2_oracle.py) on a bounded sample of the same workload on the host cores.
+Beside the headline line's fields: ``config3_sweep`` (grad-eval latency at B4 D128 for
+H in {2,4,6} x L in {2048,4096}, next to the reference's published TPU v5e latencies) and
+``config4_long_context_fwd`` (forward-only B8 H16 L32768 D128 with bf16 inputs, 8 calls of
+4096 tokens carrying the state; tokens/s and canonical GB/s).  ``--no-sweep`` skips both.
 """
 from __future__ import annotations
 
@@ -80,6 +84,88 @@ def cpu_baseline(threads: int):
             "ms_scaled_to_workload": sec * 1e3 * 24}
 
 
+# Published grad-eval latencies of the reference on TPU v5e at B4 D128 (the
+# reference runs bt=128 there), by (H, L).
+REF_TPU_MS = {(2, 2048): 1.701, (2, 4096): 2.943, (4, 2048): 2.702, (4, 4096): 10.493, (6, 2048): 2.888,
+              (6, 4096): 13.818}
+
+
+def _median_ms(fn, reps=4, rounds=3, warm=2):
+    """The reference's protocol: warmups, then the median over rounds of the mean of reps calls."""
+    import torch
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    per = []
+    for _ in range(rounds):
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        per.append((time.perf_counter() - t0) * 1e3 / reps)
+    return sorted(per)[len(per) // 2]
+
+
+def sweep_config3(cfg, seed):
+    """BASELINE.json configs[2]: grad-eval latency at B4 D128, H in {2,4,6} x L in {2048,4096}
+    (L=4096 runs as two segments of 32 chunks, as in the reference)."""
+    import torch
+    from atomic_gdn2 import make_blr_trainable
+    from atomic_gdn2.synthetic import make_inputs
+    out = []
+    for H in (2, 4, 6):
+        for L in (2048, 4096):
+            (q, k, v, w, b, g), scale = make_inputs(4, H, L, 128, seed=seed)
+            xs = [t.requires_grad_(True) for t in (q, k, v, w, b, g)]
+            fn = make_blr_trainable(cfg, scale)
+
+            def step():
+                o, hf = fn(*xs)
+                return torch.autograd.grad((o, hf), xs, grad_outputs=(2.0 * o, 2.0 * hf))
+
+            ms = _median_ms(step)
+            ff, fb = canonical_flops(4, H, L, 128)
+            ref = REF_TPU_MS[(H, L)]
+            out.append({"B": 4, "H": H, "L": L, "ms": round(ms, 4), "tflops": round((ff + fb) / (ms * 1e-3) / 1e12, 2),
+                        "ref_tpu_v5e_ms": ref, "speedup_vs_ref": round(ref / ms, 2)})
+            del xs, q, k, v, w, b, g
+    return out
+
+
+def bench_config4(cfg, seed):
+    """forward-only long context, B8 H16 D128, bf16 inputs, fp32
+    state; L = 32768 as 8 calls of 4096 tokens, each call's h0 = the previous h_final.  Inputs
+    are drawn on the device (same distributions) per call."""
+    import torch
+    from atomic_gdn2 import make_blr_trainable, _lib
+    from atomic_gdn2.synthetic import make_inputs_device
+    B, H, D, Lc, ncall = 8, 16, 128, 4096, 8
+    calls = [make_inputs_device(B, H, Lc, D, seed=seed * 100 + c, dtype=torch.bfloat16)[0] for c in range(ncall)]
+    fn = make_blr_trainable(cfg, D ** -0.5)
+
+    def run():
+        h = None
+        with torch.no_grad():
+            for xs in calls:
+                o, h = fn(*xs, h)
+        return o, h
+
+    ms = _median_ms(run, reps=2, rounds=3, warm=1)
+    _lib.prof_begin(ncall * 4)
+    run()
+    torch.cuda.synchronize()
+    prof = _lib.prof_end()
+    N = B * H * Lc * ncall * D
+    S = B * H * D * D * 4
+    byts = 6 * N * 2 + N * 4 + 16 * S
+    flops = B * H * Lc * ncall * (10 * 64 * D + 6 * D * D)
+    kern = {n: round(t / c, 4) for n, (t, c) in prof.items() if c}
+    return {"B": B, "H": H, "L": Lc * ncall, "D": D, "calls": ncall, "input_dtype": "bf16", "ms": round(ms, 3),
+            "tokens_per_s": round(B * Lc * ncall / (ms * 1e-3), 1),
+            "canonical_gb_per_s": round(byts / (ms * 1e-3) / 1e9, 1),
+            "tflops": round(flops / (ms * 1e-3) / 1e12, 2), "kernel_ms_per_call": kern}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -87,6 +173,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the config-3 sweep and the config-4 run")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every (batch, head) sequence is independent, so a "
@@ -175,6 +262,9 @@ def main():
                      "unit": "TFLOP/s", "frac": round(ach / PEAK_FP32_MFMA, 4), "traffic": traffic},
         "reference_tpu_v5e_ms": 2.888,
     }
+    if not args.no_sweep:
+        out["config3_sweep"] = sweep_config3(cfg, args.seed)
+        out["config4_long_context_fwd"] = bench_config4(cfg, args.seed)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(min(16, os.cpu_count() or 1))
     print(json.dumps(out), flush=True)

@@ -84,6 +84,16 @@ int gdn2_fwd(const gdn2_desc* d, const float* q, const float* k, const float* v,
              const float* b, const float* g, const float* h0, float* o, float* h_final,
              void* residual, void* workspace, void* stream);
 
+/* Forward of one segment with bfloat16 inputs (raw bf16 bits, same layouts): q..g are widened
+ * to fp32 on load; state, accumulation and outputs are fp32 exactly as in gdn2_fwd, which this
+ * equals bit for bit on the same (bf16-representable) values.  For the forward-only
+ * long-context path (bf16 activations, fp32 state carried between calls through h0/h_final):
+ * the forward half of make_blr_trainable (atomic_gdn2/pipeline.py:51-64) called with bf16
+ * inputs, without the up-front cast to fp32.  residual may be NULL (no backward). */
+int gdn2_fwd_bf16(const gdn2_desc* d, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                  const uint16_t* w, const uint16_t* b, const uint16_t* g, const float* h0, float* o,
+                  float* h_final, void* residual, void* workspace, void* stream);
+
 /* Backward of one segment: cotangents d_o (B,H,L,D) and d_hf (B,H,D,D) -> the raw
  * (sanitized at cfg.clip) gradients of q, k, v, w, b, g and h0, all float32. */
 int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v, const float* w,

@@ -378,3 +378,61 @@ def test_two_segments_l4096():
     sl = [a[:, 1:2] for a in arrs]
     ref = oracle_grad(cfg, scale, sl)
     compare({n: hip[n][:, 1:2] for n in ("o", "h_final") + NAMES}, ref, GATE)
+
+
+# ---------------------------------------------------------------- forward-only / bf16 inputs
+def _fwd(cfg, scale, xs, h0=None):
+    from atomic_gdn2 import make_blr_trainable
+    with torch.no_grad():
+        o, hf = make_blr_trainable(cfg, scale)(*xs, h0)
+    torch.cuda.synchronize()
+    return o, hf
+
+
+def test_forward_only_equals_training_forward_bitwise():
+    """The no-grad path (one kernel sequence over all L, no residual) equals the training path's
+    segment loop bit for bit (segments of one chunk here)."""
+    from atomic_gdn2 import make_blr_trainable
+    banner("forward-only vs segmented training forward")
+    cfg = base_cfg(max_chunks_per_call=1)
+    arrs, scale = mk_inputs(1, 512, 2, 128, 3, layout="bhld"), 128 ** -0.5
+    xs = [t.requires_grad_(True) for t in to_dev(arrs)]
+    o1, h1 = make_blr_trainable(cfg, scale)(*xs)
+    o2, h2 = _fwd(cfg, scale, [t.detach() for t in xs])
+    assert torch.equal(o1.detach(), o2) and torch.equal(h1.detach(), h2)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_bf16_inputs_forward(D):
+    """bf16 inputs are widened on load: bit-equal to the fp32 path on the same (bf16-rounded)
+    values, and within 2e-3 of the float64 oracle on those values."""
+    from oracle import gdn2_oracle as O
+    banner(f"bf16 forward D={D}")
+    cfg = base_cfg()
+    scale = D ** -0.5
+    arrs = mk_inputs(2, 256, 2, D, 4, layout="bhld")
+    xb = [t.to(torch.bfloat16) for t in to_dev(arrs)]
+    h0 = torch.randn(2, 2, D, D, device="cuda", generator=torch.Generator("cuda").manual_seed(5)) * 0.1
+    ob, hb = _fwd(cfg, scale, xb, h0)
+    of, hf = _fwd(cfg, scale, [t.float() for t in xb], h0)
+    assert ob.dtype == torch.float32 and hb.dtype == torch.float32
+    assert torch.equal(ob, of) and torch.equal(hb, hf)
+    t = [x.double().cpu() for x in xb]
+    ro, rh = O.forward_ref(*t, scale, h0.double().cpu(), O.OracleCfg.from_cfg(cfg))
+    assert rel_l2(ob, ro) < 2e-3 and rel_l2(hb, rh) < 2e-3
+
+
+def test_long_context_calls_carry_state_bitwise():
+    """Config-4 protocol in miniature: one sequence as 4 external bf16 calls with h0 = previous
+    h_final equals a single call over the whole length, bit for bit."""
+    banner("long-context external segmentation")
+    cfg = base_cfg()
+    scale = 128 ** -0.5
+    arrs = mk_inputs(1, 1024, 2, 128, 6, layout="bhld")
+    xb = [t.to(torch.bfloat16) for t in to_dev(arrs)]
+    o_all, h_all = _fwd(cfg, scale, xb)
+    h, outs = None, []
+    for s in range(4):
+        o, h = _fwd(cfg, scale, [t[:, :, 256 * s:256 * (s + 1)].contiguous() for t in xb], h)
+        outs.append(o)
+    assert torch.equal(torch.cat(outs, dim=2), o_all) and torch.equal(h, h_all)
