@@ -174,7 +174,19 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sweep", action="store_true", help="skip the config-3 sweep and the config-4 run")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run 5 plain device copies of a 256 MiB fp32 buffer (reference for the "
+                         "FETCH_SIZE / WRITE_SIZE counters) and exit")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        import torch
+        src = torch.ones(64 * 2 ** 20, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4, "copies": 5}))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every (batch, head) sequence is independent, so a "
               "multi-GPU run is B/H sharding with no communication (see DESIGN.md); run with --gpus 1",
