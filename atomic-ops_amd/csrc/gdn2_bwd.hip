@@ -17,73 +17,126 @@
 
 namespace gdn2 {
 
-template <int LD>
-__device__ __forceinline__ void load_rows(float* dst, const float* __restrict__ src, int rows, int cols,
-                                          int tid, int nt) {
-  const float4* s4p = reinterpret_cast<const float4*>(src);
-  for (int e = tid; e < rows * cols / 4; e += nt) {
-    const int i = (4 * e) / cols, d = (4 * e) % cols;
-    *reinterpret_cast<float4*>(dst + i * LD + d) = s4p[e];
-  }
-}
-
 // ------------------------------------------------------------------------------------
-template <int D>
-struct StateLayout {
-  static constexpr int LD = D + 4, RB = 32;
-  static constexpr int OFF_DO = 0, OFF_DV = T * LD, OFF_VN = 2 * T * LD;
-  static constexpr int OFF_HP = 3 * T * LD, OFF_DH = OFF_HP + RB * LD;
-  static constexpr int TOTAL = OFF_DH + RB * LD;
-};
-
+// bwd_state: one workgroup per chunk, D/16 waves.  Wave w owns key tile w (key rows
+// 16 w .. 16 w + 15) of the three outputs and accumulates, over the value blocks kb,
+//   dQg^T tile (w, ti) += h_pre[w-rows, kb] . (s dO)[ti-rows, kb]^T
+//   dWp^T tile (w, ti) += h_pre[w-rows, kb] . (-dv_new)[ti-rows, kb]^T
+//   dKg^T tile (w, ti) += dh_next[w-rows, kb] . v_new[ti-rows, kb]^T
+// The MFMA operands must be value-contiguous per lane.  The A operands of one kb (the 64 x 16
+// slabs of s dO, -dv_new and v_new, 12 KB), which every wave needs, are staged once per
+// workgroup in LDS in operand order (double-buffered, one barrier per kb); v_new arrives as
+// FA(v_new^T), whose blocks are the needed blocks in the MFMA result layout, and is
+// transposed while it is written to LDS.  The B operands are per wave: dh_next (FA, from the
+// reverse scan) straight from global memory, h_pre (FA(h_pre^T) from the forward scan)
+// through a per-wave LDS transpose.  Two or more workgroups share a CU, so one's barrier
+// waits and loads overlap the others' MFMAs.  The accumulator of tile (ti, w) is block
+// (w, ti) of FA(out^T): one float4 store.
+// ------------------------------------------------------------------------------------
 template <int D, int B3>
-__global__ __launch_bounds__(512) void bwd_state_kernel(BwdStateArgs a) {
-  using Lay = StateLayout<D>;
-  constexpr int LD = Lay::LD, RB = Lay::RB, NT = 512, NW = 8, NKB = D / 16;
-  __shared__ __attribute__((aligned(16))) float smem[Lay::TOTAL];
-  float* sdO = smem + Lay::OFF_DO;
-  float* sDV = smem + Lay::OFF_DV;
-  float* sVn = smem + Lay::OFF_VN;
-  float* sHp = smem + Lay::OFF_HP;
-  float* sDH = smem + Lay::OFF_DH;
+__global__ __launch_bounds__(D / 16 * WAVE) void bwd_state_kernel(BwdStateArgs a) {
+  constexpr int NKB = D / 16, NW = D / 16, NT = NW * WAVE, SLAB = 12 * WAVE;   // float4 per slab
+  constexpr int NST = (SLAB + NT - 1) / NT;                                      // staged per thread
+  __shared__ float4 sA[2 * SLAB];                   // [buf][mat * 4 + ti][lane]
+  __shared__ __attribute__((aligned(16))) float sTr[NW * 16 * TRP];
   const Cfg& cf = a.cfg;
-  const int chunk = blockIdx.x, tid = threadIdx.x, wv = wave_id(), l = lane_id(), r = l & 15, g = l >> 4;
+  const int chunk = blockIdx.x, tid = threadIdx.x, kt = wave_id(), l = lane_id(), r = l & 15, g = l >> 4;
   const size_t tb = (size_t)chunk * T * D, hb = (size_t)chunk * D * D;
-  load_rows<LD>(sdO, a.dout + tb, T, D, tid, NT);
-  load_fragT<LD>(sDV, a.dv_new_f + tb, D, T, 0, T, tid, NT);
-  load_fragT<LD>(sVn, a.v_new_f + tb, D, T, 0, T, tid, NT);
-  for (int rb = 0; rb < D / RB; ++rb) {
-    if (rb) __syncthreads();
-    load_fragT<LD>(sHp, a.h_pre_f + hb, D, D, rb * RB, RB, tid, NT);
-    load_fragT<LD>(sDH, a.dh_next_f + hb, D, D, rb * RB, RB, tid, NT);
-    __syncthreads();
-    // 3 outputs x 4 row tiles x (RB/16) key tiles of this block of key rows.  A operand: rows
-    // of s dO / -dv_new / v_new; B operand: key rows of h_pre / dh_next (value-contiguous).
-    // The accumulator of tile (ti, key tile kt) is block (kt, ti) of the output's FA(^T).
-    for (int t = wv; t < 3 * 4 * (RB / 16); t += NW) {
-      const int mat = t / (4 * (RB / 16)), ti = (t / (RB / 16)) % 4, tj = t % (RB / 16);
-      const float* pa = (mat == 0 ? sdO : mat == 1 ? sDV : sVn) + (16 * ti + r) * LD + 4 * g;
-      const float* pb = (mat == 2 ? sDH : sHp) + (16 * tj + r) * LD + 4 * g;
-      const float mul = mat == 0 ? cf.scale : (mat == 1 ? -1.f : 1.f);
-      f4 acc = {0.f, 0.f, 0.f, 0.f};
+  const float sc = cf.scale;
+  float* tr = sTr + kt * 16 * TRP;
+
+  // staging item f of a slab: mat = f / 256 (0: s dO, 1: -dv_new, 2: v_new), ti = f / 64 % 4,
+  // lane f % 64 of the operand block (ti, kb)
+  float4 st[NST];
+  auto fetch = [&](int kb) {
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) mma16<B3>(acc, scale4(ld4(pa + 16 * kb), mul), ld4(pb + 16 * kb));
-      drain(acc);
-      float* out = mat == 0 ? a.dqg : (mat == 1 ? a.dwp : a.dkg);
-      st4(out + tb + frag_blk(rb * (RB / 16) + tj, ti, T) + 4 * l, f4_to_float4(acc));
+    for (int j = 0; j < NST; ++j) {
+      const int f = tid + j * NT;
+      if (f < SLAB) {
+        const int mat = f >> 8, ti = (f >> 6) & 3, ln = f & 63;
+        if (mat == 0)
+          st[j] = ld4(a.dout + tb + (16 * ti + (ln & 15)) * D + 16 * kb + 4 * (ln >> 4));
+        else if (mat == 1)
+          st[j] = ld4(a.dv_new_f + tb + frag_blk(ti, kb, D) + 4 * ln);
+        else
+          st[j] = ld4(a.v_new_f + tb + frag_blk(kb, ti, T) + 4 * ln);
+      }
     }
-    // sum_v dh_next * h_pre for the RB key rows: 16 threads per row, then a fixed-order combine
-    {
-      const int row = tid / 16, part = tid % 16;
-      float s = 0.f;
-      for (int v = part; v < D; v += 16) s = fmaf(sDH[row * LD + v], sHp[row * LD + v], s);
-      s += __shfl_xor(s, 8, 16);
-      s += __shfl_xor(s, 4, 16);
-      s += __shfl_xor(s, 2, 16);
-      s += __shfl_xor(s, 1, 16);
-      if (part == 0) a.dlast[(size_t)chunk * D + rb * RB + row] = s;
+  };
+  auto put = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < NST; ++j) {
+      const int f = tid + j * NT;
+      if (f < SLAB) {
+        const int mat = f >> 8, ti = (f >> 6) & 3, ln = f & 63;
+        float4* dst = sA + buf * SLAB + (mat * 4 + ti) * WAVE;
+        if (mat == 0) {
+          dst[ln] = scale4(st[j], sc);
+        } else if (mat == 1) {
+          dst[ln] = scale4(st[j], -1.f);
+        } else {
+          // lane ln = (rr, gg) holds v_new[16 ti + 4 gg + e][16 kb + rr]: operand lane
+          // (4 gg + e) + 16 (rr / 4), component rr % 4
+          float* df = reinterpret_cast<float*>(dst);
+          const int rr = ln & 15, gg = ln >> 4, base = 4 * (4 * gg + 16 * (rr >> 2)) + (rr & 3);
+          df[base] = st[j].x;
+          df[base + 4] = st[j].y;
+          df[base + 8] = st[j].z;
+          df[base + 12] = st[j].w;
+        }
+      }
     }
+  };
+
+  f4 acc[3][4];
+#pragma unroll
+  for (int m = 0; m < 3; ++m)
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) acc[m][ti] = f4{0.f, 0.f, 0.f, 0.f};
+  float part = 0.f;
+  fetch(0);
+  put(0);
+  float4 hpT = ld4(a.h_pre_f + hb + frag_blk(0, kt, D) + 4 * l);
+  float4 dh = ld4(a.dh_next_f + hb + frag_blk(kt, 0, D) + 4 * l);
+  __syncthreads();
+#pragma unroll 1
+  for (int kb = 0; kb < NKB; ++kb) {
+    const int nk = kb + 1 < NKB ? kb + 1 : kb;       // last step re-fetches (unused)
+    fetch(nk);
+    // h_pre block (kt, kb) from FA(h_pre^T) block (kb, kt), its MFMA result layout
+    const float4 hp = wave_transpose16(tr, hpT, r, g);
+    const float4 dhc = dh;
+    hpT = ld4(a.h_pre_f + hb + frag_blk(nk, kt, D) + 4 * l);
+    dh = ld4(a.dh_next_f + hb + frag_blk(kt, nk, D) + 4 * l);
+    const float4* cur = sA + (kb & 1) * SLAB;
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) {
+      mma16<B3>(acc[0][ti], cur[ti * WAVE + l], hp);
+      mma16<B3>(acc[1][ti], cur[(4 + ti) * WAVE + l], hp);
+      mma16<B3>(acc[2][ti], cur[(8 + ti) * WAVE + l], dhc);
+    }
+    // sum_v dh_next * h_pre over this lane's 4 values of key row 16 kt + r
+    part = fmaf(dhc.x, hp.x, part);
+    part = fmaf(dhc.y, hp.y, part);
+    part = fmaf(dhc.z, hp.z, part);
+    part = fmaf(dhc.w, hp.w, part);
+    if (kb + 1 < NKB) put((kb + 1) & 1);
+    __syncthreads();
   }
+  drain(acc[0][0], acc[0][1], acc[0][2], acc[0][3]);
+  drain(acc[1][0], acc[1][1], acc[1][2], acc[1][3]);
+  drain(acc[2][0], acc[2][1], acc[2][2], acc[2][3]);
+#pragma unroll
+  for (int ti = 0; ti < 4; ++ti) {
+    const size_t o = tb + frag_blk(kt, ti, T) + 4 * l;
+    st4(a.dqg + o, f4_to_float4(acc[0][ti]));
+    st4(a.dwp + o, f4_to_float4(acc[1][ti]));
+    st4(a.dkg + o, f4_to_float4(acc[2][ti]));
+  }
+  // the four lanes of key row 16 kt + r hold the value blocks 4 g .. 4 g + 3 of every kb
+  part += __shfl_xor(part, 16);
+  part += __shfl_xor(part, 32);
+  if (g == 0) a.dlast[(size_t)chunk * D + 16 * kt + r] = part;
 }
 
 // ------------------------------------------------------------------------------------
@@ -183,8 +236,8 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   chunk_cumsum<D, LD, NT>(a.g + tb, sG);          // ends with a barrier
 
   // the P2 operands' global loads are issued now, so that they overlap P1: item f of the
-  // row-major inputs is float4 f; item f of a FRAG(x^T) input is float4 f as well, landing at
-  // row 16 (f/256 % 4) + 4 (f%64 / 16) + e, column 16 (f / 1024) + f % 16 of the row-major tile
+  // row-major inputs is float4 f; item f of a FRAG(x^T) (dWp) or FRAG(x) (dv_new) input is
+  // float4 f as well, placed into the row-major tile by put_fragT / put_frag
   constexpr int NIT = T * D / 4 / NT;
   float4 xb[NIT], xk[NIT], xw[NIT], xv[NIT], xdw[NIT], xdv[NIT];
 #pragma unroll
@@ -197,6 +250,10 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     xdw[it] = ld4(dwp + 4 * f);
     xdv[it] = ld4(a.dv_new_f + tb + 4 * f);
   }
+  auto put_frag = [&](float* dst, const float4& x, int f) {
+    const int lane = f & 63, blk = f >> 6;
+    st4(dst + (16 * (blk / NKB) + (lane & 15)) * LD + 16 * (blk % NKB) + 4 * (lane >> 4), x);
+  };
   auto put_fragT = [&](float* dst, const float4& x, int f) {
     const int lane = f & 63, blk = f >> 6;
     const int n = 16 * (blk >> 2) + (lane & 15), m = 16 * (blk & 3) + 4 * (lane >> 4);
@@ -248,7 +305,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   for (int it = 0; it < NIT; ++it) {
     const int f = tid + it * NT, i = f / (D / 4), d = 4 * (f % (D / 4));
     st4(sX1 + i * LD + d, mul4(xw[it], xv[it]));
-    put_fragT(sX2, xdv[it], f);
+    put_frag(sX2, xdv[it], f);
   }
   __syncthreads();
 #pragma unroll
@@ -635,8 +692,8 @@ hipError_t launch_bwd_pre(int D, const BwdPreArgs& a, hipStream_t s) {
 hipError_t launch_bwd_state(int D, const BwdStateArgs& a, hipStream_t s) {
   dispatch_mode(a.cfg.b3_mode, [&](auto m) {
     constexpr int M = decltype(m)::value;
-    if (D == 128) hipLaunchKernelGGL((bwd_state_kernel<128, M>), dim3(a.n_chunks), dim3(512), 0, s, a);
-    else hipLaunchKernelGGL((bwd_state_kernel<64, M>), dim3(a.n_chunks), dim3(512), 0, s, a);
+    if (D == 128) hipLaunchKernelGGL((bwd_state_kernel<128, M>), dim3(a.n_chunks), dim3(8 * WAVE), 0, s, a);
+    else hipLaunchKernelGGL((bwd_state_kernel<64, M>), dim3(a.n_chunks), dim3(4 * WAVE), 0, s, a);
     return 0;
   });
   return hipGetLastError();

@@ -304,6 +304,20 @@ __device__ __forceinline__ void load_fragT(float* dst, const float* __restrict__
   }
 }
 
+// 16x16 tile held in the MFMA result layout (lane l = r + 16 g: column r, rows 4 g .. 4 g + 3)
+// -> the same tile in the A-operand layout (lane l: row r, columns 4 g .. 4 g + 3), through a
+// per-wave LDS tile with row stride TRP (conflict-free column reads).  Only the issuing wave
+// touches `tr`, and LDS operations of one wave complete in order.
+constexpr int TRP = 20;
+__device__ __forceinline__ float4 wave_transpose16(float* tr, const float4 x, int r, int g) {
+  st4(tr + r * TRP + 4 * g, x);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  return make_float4(tr[(4 * g) * TRP + r], tr[(4 * g + 1) * TRP + r], tr[(4 * g + 2) * TRP + r],
+                     tr[(4 * g + 3) * TRP + r]);
+}
+
 // In-chunk cumulative sum of g over the T rows of a (T x D) tile, into LDS sG (ld = LD).
 // Thread t owns float4 column t % (D/4) over a run of RUN consecutive rows: it sums its run,
 // then adds the totals of the runs above it in order.  Same code in every kernel, so every

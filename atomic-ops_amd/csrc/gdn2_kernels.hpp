@@ -67,8 +67,8 @@ struct BwdPreArgs {
   Cfg cfg;
 };
 
-// Reverse state scan: reads FA(Wp^T), FA(Kg), gl, X, Y; writes dv_new as FA(dv_new^T)
-// (D x T), dh_next as FA(dh_next^T) (D x D), dh0 row-major.
+// Reverse state scan: reads FA(Wp^T), FA(Kg), gl, X, Y; writes dv_new as FA(dv_new) (T x D),
+// dh_next as FA(dh_next) (D x D), dh0 row-major.
 struct ScanBwdArgs {
   const float *wpT_f, *kg_f, *gl, *x_f, *y_f, *dhf;
   float *dv_new_f, *dh_next_f, *dh0;
@@ -76,6 +76,8 @@ struct ScanBwdArgs {
   Cfg cfg;
 };
 
+// Reads FA(dv_new) (T x D), FA(v_new^T) (D x T), FA(h_pre^T), FA(dh_next) (D x D) and dO
+// (row-major);
 // dqg / dwp / dkg are (T x D) per chunk, written as FA(dqg^T) / FA(dwp^T) / FA(dkg^T).
 struct BwdStateArgs {
   const float *dout, *dv_new_f, *v_new_f, *h_pre_f, *dh_next_f;

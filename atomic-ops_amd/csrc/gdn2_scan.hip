@@ -140,6 +140,16 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_fwd_kernel(ScanFwdArgs a) 
   for (int e = 0; e < 4; ++e) a.hf[(size_t)bh * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r] = h[e];
 }
 
+// Lane lt of block u of a FA(X^T) tile set in LDS (xs[u][lane], X of T x 16 columns) ->
+// lane lt of block u of FA(X): X[16 u + r][4 g .. 4 g + 3] is lane 4 g + e + 16 (r / 4),
+// component r % 4 of xs[u].
+__device__ __forceinline__ float4 frag_transpose_lds(const float4* xs, int u, int lt) {
+  const float* f = reinterpret_cast<const float*>(xs + u * WAVE);
+  const int rr = lt & 15, gg = lt >> 4, c = 16 * (rr >> 2), e = rr & 3;
+  return make_float4(f[4 * (4 * gg + c) + e], f[4 * (4 * gg + 1 + c) + e], f[4 * (4 * gg + 2 + c) + e],
+                     f[4 * (4 * gg + 3 + c) + e]);
+}
+
 struct BwdOps {
   float4 kg[4];    // FA(Kg) block (ti, w):    Kg[16ti + r][16w + 4g .. +3]
   float4 wpT[4];   // FA(Wp^T) block (w, u):   Wp^T[16w + r][16u + 4g .. +3]
@@ -155,6 +165,7 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
   constexpr int NW = D / 16, NVB = D / 16;
   __shared__ float4 sP[NW * 4 * WAVE];     // partial (Kg dh) tiles, [wave][ti][lane]
   __shared__ float4 sDB[4 * WAVE];         // dv_new tiles in B-operand layout, [u][lane]
+  __shared__ __attribute__((aligned(16))) float sTr[NW * 16 * TRP];   // per-wave transpose tiles
   const float clip = a.cfg.clip;
   const int nc = a.nc;
   const int lin = xcd_remap(gridDim.x);
@@ -184,8 +195,6 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
   auto step = [&](const BwdOps& op, int s, BwdOps& nx, int sn) {
     const size_t ch = chunk(s), tb = ch * T * D;
     const size_t chn = chunk(sn), tbn = chn * T * D;
-    // dh entering this chunk's step (mega.py:35)
-    st4(a.dh_next_f + ch * D * D + frag_blk(vb, w, D) + 4 * l, f4_to_float4(dh));
     const float4 db = f4_to_float4(dh);
     f4 p[4];
 #pragma unroll
@@ -196,6 +205,8 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
       nx.kg[ti] = ld4(a.kg_f + tbn + frag_blk(ti, w, D) + 4 * l);
       GDN2_SCHED_FENCE();
     }
+    // dh entering this chunk's step (mega.py:35) as FA(dh_next) block (w, slice)
+    const float4 dhv = wave_transpose16(sTr + w * 16 * TRP, db, r, g);
     drain(p[0], p[1], p[2], p[3]);
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) sP[(w * 4 + ti) * WAVE + l] = f4_to_float4(p[ti]);
@@ -207,7 +218,6 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
       for (int w2 = 1; w2 < NW; ++w2) sm = add4(sm, sP[w2 * 4 * WAVE + tid]);
       const float4 dv = san4(add4(op.xx, sm), clip);
       sDB[tid] = dv;
-      st4(a.dv_new_f + tb + frag_blk(vb, tp, T) + 4 * lp, dv);
     }
     nx.xx = ld4(a.x_f + tbn + frag_blk(vb, tp, T) + 4 * lp);
     nx.yy = ld4(a.y_f + chn * D * D + frag_blk(vb, w, D) + 4 * l);
@@ -221,11 +231,16 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
       nx.wpT[u] = ld4(a.wpT_f + tbn + frag_blk(w, u, T) + 4 * l);
       GDN2_SCHED_FENCE();
     }
+    float4 dvv = db;
+    if (red) dvv = frag_transpose_lds(sDB, tp, lp);     // FA(dv_new) block (tp, slice)
     drain(z);
     const float gmv[4] = {op.gm.x, op.gm.y, op.gm.z, op.gm.w};
     const float yv[4] = {op.yy.x, op.yy.y, op.yy.z, op.yy.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) dh[e] = sanitize((yv[e] + dh[e] * exp_nonpos(gmv[e])) - z[e], clip);
+    // stores last: the next step's waits for the prefetch loads above then do not also cover them
+    st4(a.dh_next_f + ch * D * D + frag_blk(w, vb, D) + 4 * l, dhv);
+    if (red) st4(a.dv_new_f + tb + frag_blk(tp, vb, D) + 4 * lp, dvv);
   };
 
   BwdOps A, B;
