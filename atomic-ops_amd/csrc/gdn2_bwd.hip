@@ -186,7 +186,8 @@ __device__ __forceinline__ float4 pick4(const float4 (&x)[4], int t) {
                      sel4(x[0].z, x[1].z, x[2].z, x[3].z, t), sel4(x[0].w, x[1].w, x[2].w, x[3].w, t));
 }
 
-template <int D, int B3>
+// STD: the pieces are the standard geometry's (bt = score_bs = 64, bs2 = 32), see std_pieces()
+template <int D, int B3, bool STD>
 __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   using Lay = BwdWyLayout<D>;
   using St = Strip<D>;
@@ -381,10 +382,10 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     dgc4[m] = dq4[m];
   }
   const bool lean = cf.diag == DIAG_LEAN;
-  for (int pi = 0; pi < cf.pieces.n; ++pi) {
-    const Piece pc = cf.pieces.p[pi];
+  // One piece of the two-level score factorisation; with the standard geometry the three
+  // pieces are compile-time constants, so every branch and index below folds away.
+  auto b4_piece = [&](const Piece pc) __attribute__((always_inline)) {
     const int nb = pc.P / 16, tr0 = pc.row0 / 16, tc0 = pc.col0 / 16;
-    if (pc.kind == 1 && lean) continue;
     // legs at this lane's positions; qt = q ra, bkt = (b k) ra over the piece rows,
     // kt = k cb over the piece columns (k blocks of 16)
     float4 ra[2], cbl[2], qt[2], bkt[2], kt[2];
@@ -469,6 +470,20 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
         }
       }
     }
+  };
+  if constexpr (STD) {
+    constexpr Piece P0{0, 0, 32, 1, 0, 0, 32, 0}, P1{32, 32, 32, 1, 32, 32, 64, 0}, P2{32, 0, 32, 0, 32, 0, 0, 0};
+    if (!lean) {
+      b4_piece(P0);
+      b4_piece(P1);
+    }
+    b4_piece(P2);
+  } else {
+    for (int pi = 0; pi < cf.pieces.n; ++pi) {
+      const Piece pc = cf.pieces.p[pi];
+      if (pc.kind == 1 && lean) continue;
+      b4_piece(pc);
+    }
   }
 
   // lean diagonal blocks (b4.py:20-30): exact E = exp(clip(gc_i - gc_j, +-diff_clip)) per element
@@ -527,6 +542,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   float* __restrict__ o_dv = a.dv + tb;
   float* sDgc = sX1;
   const float gl = sG[(T - 1) * LD + dcol];
+  const float dlast = owned(3) && g == 3 ? a.dlast[(size_t)chunk * D + dcol] : 0.f;
   float part = 0.f, fix3 = 0.f, fix4 = 0.f;
 #pragma unroll
   for (int m = 0; m < NTW; ++m) {
@@ -592,7 +608,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     float colsum = 0.f;
     for (int w2 = strip; w2 < NW; w2 += St::NS) colsum += sColP[w2 * 16 + r];
     const float dec = exp_nonpos(gl), mdec = gl < 0.f ? 1.f : 0.f;
-    colsum += dec * a.dlast[(size_t)chunk * D + dcol] * mdec;
+    colsum += dec * dlast * mdec;
     sDgc[(T - 1) * LD + dcol] = sanitize(fix3 + colsum, clip) + fix4;
   }
   __syncthreads();
@@ -699,11 +715,31 @@ hipError_t launch_bwd_state(int D, const BwdStateArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// The piece list of the standard geometry (make_pieces(64, 64, 32)): the two 32 x 32 diagonal
+// blocks and the level-2 block below the first.
+static bool std_pieces(const PieceList& pl) {
+  const int ref[3][7] = {{0, 0, 32, 1, 0, 0, 32}, {32, 32, 32, 1, 32, 32, 64}, {32, 0, 32, 0, 32, 0, 0}};
+  if (pl.n != 3) return false;
+  for (int i = 0; i < 3; ++i) {
+    const Piece& p = pl.p[i];
+    const int got[7] = {p.row0, p.col0, p.P, p.kind, p.anchor, p.s0, p.s1};
+    for (int j = 0; j < 7; ++j)
+      if (got[j] != ref[i][j]) return false;
+  }
+  return true;
+}
+
 hipError_t launch_bwd_wy(int D, const BwdWyArgs& a, hipStream_t s) {
+  const bool std_geom = std_pieces(a.cfg.pieces);
   dispatch_mode(a.cfg.b3_mode, [&](auto m) {
     constexpr int M = decltype(m)::value;
-    if (D == 128) hipLaunchKernelGGL((bwd_wy_kernel<128, M>), dim3(a.n_chunks), dim3(512), 0, s, a);
-    else hipLaunchKernelGGL((bwd_wy_kernel<64, M>), dim3(a.n_chunks), dim3(512), 0, s, a);
+    if (D == 128) {
+      if (std_geom) hipLaunchKernelGGL((bwd_wy_kernel<128, M, true>), dim3(a.n_chunks), dim3(512), 0, s, a);
+      else hipLaunchKernelGGL((bwd_wy_kernel<128, M, false>), dim3(a.n_chunks), dim3(512), 0, s, a);
+    } else {
+      if (std_geom) hipLaunchKernelGGL((bwd_wy_kernel<64, M, true>), dim3(a.n_chunks), dim3(512), 0, s, a);
+      else hipLaunchKernelGGL((bwd_wy_kernel<64, M, false>), dim3(a.n_chunks), dim3(512), 0, s, a);
+    }
     return 0;
   });
   return hipGetLastError();
