@@ -134,6 +134,11 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
 
   // 2a. row fragments (cd_slim.py:17-21): FA(Kg) with kg = san(k e^{min(gl-gc,0)}),
   //     FA(Qg) with qg = san(q e^{min(gc,0)}); b*k and w*v into LDS.
+  // 2b. column fragments FA(Kg^T), FA(Qg^T) (D x T): the wave holds one whole 16x16 block of k
+  //     and q per item (block wv + 8 it), which a per-wave LDS transpose (in S, free until the
+  //     scores) turns into lane l of the transposed block: 4 consecutive tokens of one channel.
+  float* tr = sS + wv * 16 * TRP;
+  const bool colf = a.kgT_f || a.qgT_f;
 #pragma unroll
   for (int it = 0; it < NIT; ++it) {
     const int f = tid + it * NT, blk = f >> 6, ln = f & 63;
@@ -151,24 +156,23 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
       if (a.qg_f) st4(a.qg_f + tb + 4 * f, qg);
       if (a.qg) st4(a.qg + tb + i * D + d, qg);
     }
-  }
-  // 2b. column fragments FA(Kg^T), FA(Qg^T) (D x T): lane ln of block (key block, token block)
-  //     holds 4 consecutive tokens of one key channel.
-  if (a.kgT_f || a.qgT_f) {
-    for (int f = tid; f < T * D / 4; f += NT) {
-      const int blk = f >> 6, ln = f & 63;
-      const int d = 16 * (blk >> 2) + (ln & 15), i0 = 16 * (blk & 3) + 4 * (ln >> 4);
-      const float gl = sG[(T - 1) * LD + d];
+    if (colf) {
+      // lane (r, g): channel dc = 16 bj + r at tokens i0 + e, e = 0..3
+      const int bi = blk / NKB, bj = blk % NKB, dc = 16 * bj + r, i0 = 16 * bi + 4 * g;
+      const float4 kc = wave_transpose16(tr, xk[it], r, g);
+      const float4 qc = wave_transpose16(tr, xq[it], r, g);
+      const float gl = sG[(T - 1) * LD + dc];
+      const float kv4[4] = {kc.x, kc.y, kc.z, kc.w}, qv4[4] = {qc.x, qc.y, qc.z, qc.w};
       float kt[4], qt[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int i = i0 + e;
-        const float gi = sG[i * LD + d];
-        kt[e] = sanitize(in_val(k + i * D + d) * exp_nonpos(gl - gi), clip);
-        qt[e] = sanitize(in_val(q + i * D + d) * exp_nonpos(gi), clip);
+        const float gi = sG[(i0 + e) * LD + dc];
+        kt[e] = sanitize(kv4[e] * exp_nonpos(gl - gi), clip);
+        qt[e] = sanitize(qv4[e] * exp_nonpos(gi), clip);
       }
-      if (a.kgT_f) st4(a.kgT_f + tb + 4 * f, make_float4(kt[0], kt[1], kt[2], kt[3]));
-      if (a.qgT_f) st4(a.qgT_f + tb + 4 * f, make_float4(qt[0], qt[1], qt[2], qt[3]));
+      const size_t o = tb + frag_blk(bj, bi, T) + 4 * l;
+      if (a.kgT_f) st4(a.kgT_f + o, make_float4(kt[0], kt[1], kt[2], kt[3]));
+      if (a.qgT_f) st4(a.qgT_f + o, make_float4(qt[0], qt[1], qt[2], qt[3]));
     }
   }
   if (a.gl && tid < D) a.gl[(size_t)chunk * D + tid] = sG[(T - 1) * LD + tid];
