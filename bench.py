@@ -14,12 +14,15 @@ stream by the library (gdn2_prof_begin / gdn2_prof_end) in a second pass of K st
 Beside the headline line's fields: ``config3_sweep`` (grad-eval latency at B4 D128 for
 H in {2,4,6} x L in {2048,4096}, next to the reference's published TPU v5e latencies) and
 ``config4_long_context_fwd`` (forward-only B8 H16 L32768 D128 with bf16 inputs, 8 calls of
-4096 tokens carrying the state; tokens/s and canonical GB/s).  ``--no-sweep`` skips both.
+4096 tokens carrying the state; tokens/s and canonical GB/s), and ``config5_e2e_lm`` (one
+training step of the reference's 8-block benchmark LM around the operator, B8 L2048).
+``--no-sweep`` skips configs 3 and 4, ``--no-e2e`` config 5.
 """
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -166,6 +169,31 @@ def bench_config4(cfg, seed):
             "tflops": round(flops / (ms * 1e-3) / 1e12, 2), "kernel_ms_per_call": kern}
 
 
+def bench_e2e_lm(seed, reps=4, rounds=3, warm=2):
+    """one training step of the reference's benchmark LM (8 GDN-2
+    blocks, 34,873,952 parameters, B8 L2048, vocab 256, CE + clip_by_global_norm(1.0) + AdamW)
+    on uniform synthetic tokens, the optimizer state evolving across the timed steps as in the
+    reference's protocol (candidate_e2e.py timed_step)."""
+    import torch
+    from atomic_gdn2 import e2e_lm
+    torch.backends.cuda.matmul.allow_tf32 = False
+    cfg = e2e_lm.LMConfig()
+    model = e2e_lm.make_lm(cfg, seed=seed)
+    step = e2e_lm.TrainStep(model)
+    ids = e2e_lm.synthetic_tokens(cfg, batch=8, length=2048, seed=seed)
+    loss = [None]
+
+    def run():
+        loss[0] = step(ids)
+
+    ms = _median_ms(run, reps=reps, rounds=rounds, warm=warm)
+    final = float(loss[0])
+    return {"params": e2e_lm.n_params(model), "batch": 8, "length": 2048, "ms_per_step": round(ms, 3),
+            "input_tokens_per_s": round(8 * 2048 / (ms * 1e-3), 1), "final_loss": round(final, 4),
+            "finite": bool(math.isfinite(final)), "operator_cfg": "bt64 wy_eps1e-3 bf16x3 solve/bwd",
+            "matmul": "fp32", "reference_tpu_v5e_ms": 204.659}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -174,6 +202,7 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sweep", action="store_true", help="skip the config-3 sweep and the config-4 run")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end LM training step")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 5 plain device copies of a 256 MiB fp32 buffer (reference for the "
                          "FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -277,6 +306,8 @@ def main():
     if not args.no_sweep:
         out["config3_sweep"] = sweep_config3(cfg, args.seed)
         out["config4_long_context_fwd"] = bench_config4(cfg, args.seed)
+    if not args.no_e2e:
+        out["config5_e2e_lm"] = bench_e2e_lm(args.seed)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(min(16, os.cpu_count() or 1))
     print(json.dumps(out), flush=True)
