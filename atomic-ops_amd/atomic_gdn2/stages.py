@@ -1,0 +1,50 @@
+"""The chunk-parallel WY stage on the HIP kernels, exposed for stage-level checks.
+
+``build_scores`` stands in for the reference's Kernel A entry point (``fwd/scores.py:90-100``,
+``build_scores(q, k, b, gc, scale, cfg) -> (Aqk, Akk)`` on chunked (B,H,nc,bt,D) arrays) and
+``wy_stage`` also returns the WY inverse and recompute of ``fwd/solve.py`` and
+``fwd/cd_slim.py:12-21``.  Both run ``gdn2_wy_stage`` (include/gdn2.h), which takes the raw
+gate g and forms the in-chunk cumsum itself, so these take g, not gc.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from .pipeline import _check_device, _f32
+
+
+def wy_stage(q, k, v, w, b, g, scale, cfg):
+    """q..g: (B,H,L,D) or chunked (B,H,nc,bt,D) on a ROCm device.  Returns a dict of chunked
+    float32 tensors: aqk, akk, A (B,H,nc,bt,bt); wp, u, kg, qg (B,H,nc,bt,D); gl (B,H,nc,D)."""
+    _check_device(q)
+    if q.dim() == 5:
+        B, H, nc, bt, D = q.shape
+        q, k, v, w, b, g = (t.reshape(B, H, nc * bt, D) for t in (q, k, v, w, b, g))
+    xs = [_f32(t) for t in (q, k, v, w, b, g)]
+    B, H, L, D = xs[0].shape
+    bt = cfg.bt
+    if L % bt:
+        raise ValueError(f"L={L} must be divisible by bt={bt}")
+    nc = L // bt
+    dev = xs[0].device
+    mk = lambda *s: torch.empty(*s, dtype=torch.float32, device=dev)
+    out = dict(aqk=mk(B, H, nc, bt, bt), akk=mk(B, H, nc, bt, bt), A=mk(B, H, nc, bt, bt),
+               wp=mk(B, H, nc, bt, D), u=mk(B, H, nc, bt, D), kg=mk(B, H, nc, bt, D),
+               qg=mk(B, H, nc, bt, D), gl=mk(B, H, nc, D))
+    desc = _lib.make_desc(cfg, B, H, L, D, float(scale))
+    with torch.cuda.device(dev):
+        _lib.residual_layout(desc)                       # validates the descriptor
+        _lib.check(_lib.lib().gdn2_wy_stage(ctypes.byref(desc), *map(_lib.ptr, xs),
+                                            *(_lib.ptr(out[n]) for n in ("aqk", "akk", "A", "wp", "u", "kg", "qg", "gl")),
+                                            _lib.stream_handle(dev)), "gdn2_wy_stage")
+    return out
+
+
+def build_scores(q, k, b, g, scale, cfg):
+    """(Aqk, Akk), masked and sanitized, chunked (B,H,nc,bt,bt)."""
+    z = torch.zeros_like(q)
+    st = wy_stage(q, k, z, z, b, g, scale, cfg)
+    return st["aqk"], st["akk"]
