@@ -236,21 +236,21 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   for (int f = tid; f < T * T / 4; f += NT) st4(sA + (f >> 4) * LT + 4 * (f & 15), ld4(a.A + sb + 4 * f));
   chunk_cumsum<D, LD, NT>(a.g + tb, sG);          // ends with a barrier
 
-  // the P2 operands' global loads are issued now, so that they overlap P1: item f of the
-  // row-major inputs is float4 f; item f of a FRAG(x^T) (dWp) or FRAG(x) (dv_new) input is
-  // float4 f as well, placed into the row-major tile by put_fragT / put_frag
+  // The P2 operands' global loads are spread between P1's MFMAs (a burst of loads stalls the
+  // issuing wave while the CU's memory path is busy).  Item f of the row-major inputs is float4
+  // f; item f of a FRAG(x^T) (dWp) or FRAG(x) (dv_new) input is float4 f as well, placed into
+  // the row-major tile by put_fragT / put_frag.
   constexpr int NIT = T * D / 4 / NT;
   float4 xb[NIT], xk[NIT], xw[NIT], xv[NIT], xdw[NIT], xdv[NIT];
-#pragma unroll
-  for (int it = 0; it < NIT; ++it) {
-    const int f = tid + it * NT;
-    xb[it] = ld4(b + 4 * f);
-    xk[it] = ld4(k + 4 * f);
-    xw[it] = ld4(w + 4 * f);
-    xv[it] = ld4(v + 4 * f);
-    xdw[it] = ld4(dwp + 4 * f);
-    xdv[it] = ld4(a.dv_new_f + tb + 4 * f);
-  }
+  auto prefetch = [&](int item) {
+    const int arr = item / NIT, it = item % NIT, f = tid + it * NT;
+    if (arr == 0) xb[it] = ld4(b + 4 * f);
+    else if (arr == 1) xk[it] = ld4(k + 4 * f);
+    else if (arr == 2) xw[it] = ld4(w + 4 * f);
+    else if (arr == 3) xv[it] = ld4(v + 4 * f);
+    else if (arr == 4) xdw[it] = ld4(dwp + 4 * f);
+    else xdv[it] = ld4(a.dv_new_f + tb + 4 * f);
+  };
   auto put_frag = [&](float* dst, const float4& x, int f) {
     const int lane = f & 63, blk = f >> 6;
     st4(dst + (16 * (blk / NKB) + (lane & 15)) * LD + 16 * (blk % NKB) + 4 * (lane >> 4), x);
@@ -264,14 +264,24 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     dst[(m + 3) * LD + n] = x.w;
   };
 
-  // P1: dAqk = (dO v_new^T) * causal
-  for (int t = wv; t < 16; t += NW) {
-    const int ti = t >> 2, tj = t & 3;
+  // P1: dAqk = (dO v_new^T) * causal; 16 tiles, two per wave
+  static_assert(NW == 8, "P1 assumes two dAqk tiles per wave");
+  constexpr int NITEMS = 6 * NIT, NSLOT = 2 * NKB;
+#pragma unroll
+  for (int m2 = 0; m2 < 2; ++m2) {
+    const int t = wv + NW * m2, ti = t >> 2, tj = t & 3;
     const float* ar = sX2 + (16 * ti + r) * LD + 4 * g;
     const float* br = sX1 + (16 * tj + r) * LD + 4 * g;
     f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) mma16<B3>(acc, ld4(ar + 16 * kb), ld4(br + 16 * kb));
+    for (int kb = 0; kb < NKB; ++kb) {
+      mma16<B3>(acc, ld4(ar + 16 * kb), ld4(br + 16 * kb));
+      __builtin_amdgcn_sched_barrier(0);
+      const int sl = m2 * NKB + kb;
+#pragma unroll
+      for (int item = NITEMS * sl / NSLOT; item < NITEMS * (sl + 1) / NSLOT; ++item) prefetch(item);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     drain(acc);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
