@@ -554,10 +554,31 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   const float gl = sG[(T - 1) * LD + dcol];
   const float dlast = owned(3) && g == 3 ? a.dlast[(size_t)chunk * D + dcol] : 0.f;
   float part = 0.f, fix3 = 0.f, fix4 = 0.f;
+  // The dWp operand of the dkb chain depends on the k block only: loaded once.  Each tile's
+  // global operands are loaded one tile ahead, before the current tile's stores (the memory
+  // counter is in order, so a wait on a load issued after stores would wait for them too).
+  float4 dwpc[4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) dwpc[kb] = fcol4(dwp, kb);
+  float4 nw4 = col4(w, St::rtile(wv, 0)), nv4 = col4(v, St::rtile(wv, 0));
+  float4 ndq4 = fcol4(dqgp, St::rtile(wv, 0)), ndk4 = fcol4(dkgp, St::rtile(wv, 0));
+  // The five gradient tiles leave through a per-wave 16x16 LDS transpose (in the dAqk buffer,
+  // free once every wave has left B4) as one float4 row store per lane instead of four
+  // scalar column stores.
+  static_assert(NW * 16 * TRP <= T * LT, "transpose tiles fit in the dAqk buffer");
+  __syncthreads();
+  float* tr = sDAq + wv * 16 * TRP;
 #pragma unroll
   for (int m = 0; m < NTW; ++m) {
     const int rt = St::rtile(wv, m), i0 = 16 * rt + 4 * g;
-    const float4 w4 = col4(w, rt), v4 = col4(v, rt), dqg4 = fcol4(dqgp, rt), dkg4 = fcol4(dkgp, rt);
+    const float4 w4 = nw4, v4 = nv4, dqg4 = ndq4, dkg4 = ndk4;
+    if (m + 1 < NTW) {
+      const int rn = St::rtile(wv, m + 1);
+      nw4 = col4(w, rn);
+      nv4 = col4(v, rn);
+      ndq4 = fcol4(dqgp, rn);
+      ndk4 = fcol4(dkgp, rn);
+    }
     f4 dkb = {0.f, 0.f, 0.f, 0.f}, dwv = {0.f, 0.f, 0.f, 0.f};
     // straight-line MFMA chain: skip the zero k blocks only where rt is a compile-time value
     constexpr bool RT_STATIC = St::NS == NW;          // rt == m for every wave
@@ -566,7 +587,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
       const float* ac = sA + (16 * kb + 4 * g) * LT + 16 * rt + r;
       const float4 av = make_float4(ac[0], ac[LT], ac[2 * LT], ac[3 * LT]);
       const float* pv = sX2 + (16 * kb + 4 * g) * LD + dcol;
-      mma16<B3>(dkb, av, fcol4(dwp, kb));
+      mma16<B3>(dkb, av, dwpc[kb]);
       mma16<B3>(dwv, av, make_float4(pv[0], pv[LD], pv[2 * LD], pv[3 * LD]));
     }
     drain(dkb, dwv);
@@ -574,12 +595,13 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     const float qa[4] = {q4.x, q4.y, q4.z, q4.w}, ka[4] = {k4.x, k4.y, k4.z, k4.w}, ba[4] = {b4.x, b4.y, b4.z, b4.w};
     const float wa[4] = {w4.x, w4.y, w4.z, w4.w}, va[4] = {v4.x, v4.y, v4.z, v4.w};
     const float qga[4] = {dqg4.x, dqg4.y, dqg4.z, dqg4.w}, kga[4] = {dkg4.x, dkg4.y, dkg4.z, dkg4.w};
+    float ow[4], ov[4], oq[4], ok[4], ob[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int i = i0 + e, x = i * D + dcol;
+      const int i = i0 + e;
       const float be = ba[e], ke = ka[e], qe = qa[e];
-      o_dw[x] = sanitize(dwv[e] * va[e], clip);     // mega.py:57
-      o_dv[x] = sanitize(dwv[e] * wa[e], clip);     // mega.py:58
+      ow[e] = sanitize(dwv[e] * va[e], clip);     // mega.py:57
+      ov[e] = sanitize(dwv[e] * wa[e], clip);     // mega.py:58
       const float gi = sG[i * LD + dcol];
       const float egc = exp_nonpos(gi), ekg = exp_nonpos(gl - gi);
       const float mgc = gi < 0.f ? 1.f : 0.f, mkg = (gl - gi) < 0.f ? 1.f : 0.f;
@@ -597,9 +619,9 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
       const float dk4v = sanitize(dk4[m][e] + dbkv * be, clip);
       const float db4v = sanitize(dbkv * ke, clip);
       const float dgc4v = sanitize(dgc4[m][e], clip);
-      o_dq[x] = sanitize(dq3 + dqv, clip);
-      o_dk[x] = sanitize(dk3 + dk4v, clip);
-      o_db[x] = sanitize(db3 + db4v, clip);
+      oq[e] = sanitize(dq3 + dqv, clip);
+      ok[e] = sanitize(dk3 + dk4v, clip);
+      ob[e] = sanitize(db3 + db4v, clip);
       if (i == T - 1) {
         fix3 = dgc3;
         fix4 = dgc4v;
@@ -607,6 +629,13 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
         sDgc[i * LD + dcol] = sanitize(dgc3, clip) + dgc4v;
       }
     }
+    // lane (r, g) after the transpose: row 16 rt + r, columns 16 strip + 4 g .. + 3
+    const int ro = (16 * rt + r) * D + 16 * strip + 4 * g;
+    st4(o_dw + ro, wave_transpose16(tr, make_float4(ow[0], ow[1], ow[2], ow[3]), r, g));
+    st4(o_dv + ro, wave_transpose16(tr, make_float4(ov[0], ov[1], ov[2], ov[3]), r, g));
+    st4(o_dq + ro, wave_transpose16(tr, make_float4(oq[0], oq[1], oq[2], oq[3]), r, g));
+    st4(o_dk + ro, wave_transpose16(tr, make_float4(ok[0], ok[1], ok[2], ok[3]), r, g));
+    st4(o_db + ro, wave_transpose16(tr, make_float4(ob[0], ob[1], ob[2], ob[3]), r, g));
   }
   // last-row decay gradient: sum over all rows of the column (lanes g, then the waves of the
   // strip in order) + e^gamma sum_v(dh_next h_pre) [gl < 0]
