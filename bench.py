@@ -190,7 +190,7 @@ def bench_e2e_lm(seed, reps=4, rounds=3, warm=2):
     final = float(loss[0])
     return {"params": e2e_lm.n_params(model), "batch": 8, "length": 2048, "ms_per_step": round(ms, 3),
             "input_tokens_per_s": round(8 * 2048 / (ms * 1e-3), 1), "final_loss": round(final, 4),
-            "finite": bool(math.isfinite(final)), "operator_cfg": "bt64 wy_eps1e-3 bf16x3 solve/bwd",
+            "finite": bool(math.isfinite(final)), "operator_cfg": "bt64 wy_eps1e-3 dot=highest",
             "matmul": "fp32", "reference_tpu_v5e_ms": 204.659}
 
 
