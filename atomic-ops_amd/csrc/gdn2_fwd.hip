@@ -91,6 +91,87 @@ __device__ __forceinline__ void leaf_solve(const float* sSe, float* sI, int tid)
   for (int i = 0; i < MB; ++i) sI[(base + i) * LT + base + c] = x[i];
 }
 
+// The WY inverse A = (I + Se)^-1 (fwd/solve.py:9-59) of Se = (1-eps) Akk, strictly lower in
+// sK, into sI (zero on entry): leaf inverses by forward substitution, block doubling with sM as
+// the temp (T x LT), then A = san(A) in place and, if A_out is given, row-major to A_out.
+// Starts with the leaf solves and ends with a barrier.
+template <int LT, int NT, int NW>
+__device__ __forceinline__ void wy_inverse(const Cfg& cf, const float* sK, float* sI, float* sM, float* A_out,
+                                           int tid, int wv, int r, int g) {
+  const int smode = cf.solve_mode;
+  if (tid < T) {
+    switch (cf.mb) {
+      case 1: leaf_solve<1, LT>(sK, sI, tid); break;
+      case 2: leaf_solve<2, LT>(sK, sI, tid); break;
+      case 4: leaf_solve<4, LT>(sK, sI, tid); break;
+      case 8: leaf_solve<8, LT>(sK, sI, tid); break;
+      case 16: leaf_solve<16, LT>(sK, sI, tid); break;
+      default: {
+        // mb = 32 / 64: column c of the leaf in LDS (same arithmetic order as above)
+        const int mb = cf.mb, base = (tid / mb) * mb, c = tid % mb;
+        for (int i = 0; i < mb; ++i) {
+          float s = 0.f;
+          for (int j = 0; j < i; ++j) s = fmaf(sK[(base + i) * LT + base + j], sI[(base + j) * LT + base + c], s);
+          sI[(base + i) * LT + base + c] = (i == c ? 1.f : 0.f) - s;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // 5b. block doubling X <- [[X11, 0], [-X22 (S21 X11), X22]] (solve.py:30-43), products in the
+  //     solve dot mode: MFMA tiles for blocks of 16 and up, scalar below.
+  for (int bb = cf.mb; bb < T; bb *= 2) {
+    const int nm = T / (2 * bb);
+    if (bb < 16) {
+      const int per = bb * bb;
+      for (int e = tid; e < nm * per; e += NT) {
+        const int m = e / per, i = (e % per) / bb, j = e % bb, i0 = m * 2 * bb;
+        const float* srow = sK + (i0 + bb + i) * LT + i0;
+        const float* tcol = sI + i0 * LT + i0 + j;
+        sM[(i0 + bb + i) * LT + i0 + j] = dot_mode_scalar(
+            smode, j, bb, [&](int kk) { return srow[kk]; }, [&](int kk) { return tcol[kk * LT]; });
+      }
+      __syncthreads();
+      for (int e = tid; e < nm * per; e += NT) {
+        const int m = e / per, i = (e % per) / bb, j = e % bb, i0 = m * 2 * bb;
+        const float* brow = sI + (i0 + bb + i) * LT + i0 + bb;
+        const float* mcol = sM + (i0 + bb) * LT + i0 + j;
+        sI[(i0 + bb + i) * LT + i0 + j] = -dot_mode_scalar(
+            smode, 0, i + 1, [&](int kk) { return brow[kk]; }, [&](int kk) { return mcol[kk * LT]; });
+      }
+      __syncthreads();
+    } else {
+      const int nt = bb / 16, tpm = nt * nt;
+      for (int t = wv; t < nm * tpm; t += NW) {
+        const int m = t / tpm, ti = (t % tpm) / nt, tj = t % nt, i0 = 2 * bb * m;
+        f4 acc = {0.f, 0.f, 0.f, 0.f};
+        mma_tile_rt(smode, acc, rm(sK, LT).shift(i0 + bb + 16 * ti, i0), rm(sI, LT).shift(i0, i0 + 16 * tj), bb);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sM[(i0 + bb + 16 * ti + 4 * g + e) * LT + i0 + 16 * tj + r] = acc[e];
+      }
+      __syncthreads();
+      for (int t = wv; t < nm * tpm; t += NW) {
+        const int m = t / tpm, ti = (t % tpm) / nt, tj = t % nt, i0 = 2 * bb * m;
+        f4 acc = {0.f, 0.f, 0.f, 0.f};
+        mma_tile_rt(smode, acc, rm(sI, LT).shift(i0 + bb + 16 * ti, i0 + bb),
+                    rm(sM, LT).shift(i0 + bb, i0 + 16 * tj), bb);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sI[(i0 + bb + 16 * ti + 4 * g + e) * LT + i0 + 16 * tj + r] = -acc[e];
+      }
+      __syncthreads();
+    }
+  }
+  // 5c. A = san(inverse)
+  for (int f = tid; f < T * T / 4; f += NT) {
+    const int i = f / (T / 4), j = 4 * (f % (T / 4));
+    const float4 x = san4(ld4(sI + i * LT + j), cf.clip);
+    st4(sI + i * LT + j, x);
+    if (A_out) st4(A_out + i * T + j, x);
+  }
+  __syncthreads();
+}
+
 template <int D, int DOT, typename TIn>
 __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
   using Lay = WyLayout<D>;
@@ -253,78 +334,7 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
     const int i = f / (D / 4), d = 4 * (f % (D / 4));
     st4(sBK + i * LD + d, mul4(ld4(sBK + i * LD + d), expnp4(ld4(sG + i * LD + d))));
   }
-  if (tid < T) {
-    switch (cf.mb) {
-      case 1: leaf_solve<1, LT>(sK, sI, tid); break;
-      case 2: leaf_solve<2, LT>(sK, sI, tid); break;
-      case 4: leaf_solve<4, LT>(sK, sI, tid); break;
-      case 8: leaf_solve<8, LT>(sK, sI, tid); break;
-      case 16: leaf_solve<16, LT>(sK, sI, tid); break;
-      default: {
-        // mb = 32 / 64: column c of the leaf in LDS (same arithmetic order as above)
-        const int mb = cf.mb, base = (tid / mb) * mb, c = tid % mb;
-        for (int i = 0; i < mb; ++i) {
-          float s = 0.f;
-          for (int j = 0; j < i; ++j) s = fmaf(sK[(base + i) * LT + base + j], sI[(base + j) * LT + base + c], s);
-          sI[(base + i) * LT + base + c] = (i == c ? 1.f : 0.f) - s;
-        }
-      }
-    }
-  }
-  __syncthreads();
-
-  // 5b. block doubling X <- [[X11, 0], [-X22 (S21 X11), X22]] (solve.py:30-43), products in the
-  //     solve dot mode: MFMA tiles for blocks of 16 and up, scalar below.
-  float* sM = sS;
-  for (int bb = cf.mb; bb < T; bb *= 2) {
-    const int nm = T / (2 * bb);
-    if (bb < 16) {
-      const int per = bb * bb;
-      for (int e = tid; e < nm * per; e += NT) {
-        const int m = e / per, i = (e % per) / bb, j = e % bb, i0 = m * 2 * bb;
-        const float* srow = sK + (i0 + bb + i) * LT + i0;
-        const float* tcol = sI + i0 * LT + i0 + j;
-        sM[(i0 + bb + i) * LT + i0 + j] = dot_mode_scalar(
-            cf.solve_mode, j, bb, [&](int kk) { return srow[kk]; }, [&](int kk) { return tcol[kk * LT]; });
-      }
-      __syncthreads();
-      for (int e = tid; e < nm * per; e += NT) {
-        const int m = e / per, i = (e % per) / bb, j = e % bb, i0 = m * 2 * bb;
-        const float* brow = sI + (i0 + bb + i) * LT + i0 + bb;
-        const float* mcol = sM + (i0 + bb) * LT + i0 + j;
-        sI[(i0 + bb + i) * LT + i0 + j] = -dot_mode_scalar(
-            cf.solve_mode, 0, i + 1, [&](int kk) { return brow[kk]; }, [&](int kk) { return mcol[kk * LT]; });
-      }
-      __syncthreads();
-    } else {
-      const int nt = bb / 16, tpm = nt * nt;
-      for (int t = wv; t < nm * tpm; t += NW) {
-        const int m = t / tpm, ti = (t % tpm) / nt, tj = t % nt, i0 = 2 * bb * m;
-        f4 acc = {0.f, 0.f, 0.f, 0.f};
-        mma_tile_rt(cf.solve_mode, acc, rm(sK, LT).shift(i0 + bb + 16 * ti, i0), rm(sI, LT).shift(i0, i0 + 16 * tj), bb);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sM[(i0 + bb + 16 * ti + 4 * g + e) * LT + i0 + 16 * tj + r] = acc[e];
-      }
-      __syncthreads();
-      for (int t = wv; t < nm * tpm; t += NW) {
-        const int m = t / tpm, ti = (t % tpm) / nt, tj = t % nt, i0 = 2 * bb * m;
-        f4 acc = {0.f, 0.f, 0.f, 0.f};
-        mma_tile_rt(cf.solve_mode, acc, rm(sI, LT).shift(i0 + bb + 16 * ti, i0 + bb),
-                    rm(sM, LT).shift(i0 + bb, i0 + 16 * tj), bb);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sI[(i0 + bb + 16 * ti + 4 * g + e) * LT + i0 + 16 * tj + r] = -acc[e];
-      }
-      __syncthreads();
-    }
-  }
-  // 5c. A = san(inverse)
-  for (int f = tid; f < T * T / 4; f += NT) {
-    const int i = f / (T / 4), j = 4 * (f % (T / 4));
-    const float4 x = san4(ld4(sI + i * LT + j), clip);
-    st4(sI + i * LT + j, x);
-    if (a.A) st4(a.A + sb + i * T + j, x);
-  }
-  __syncthreads();
+  wy_inverse<LT, NT, NW>(cf, sK, sI, sS, a.A ? a.A + sb : nullptr, tid, wv, r, g);
 
   // 6. Wp = san(A X), U = san(A (w v)); A is unit lower triangular, so row tile ti only needs
   //    k blocks 0..ti.  Lane l's accumulator is lane l of FA(P^T) block (tj, ti); FA(Wp) goes
