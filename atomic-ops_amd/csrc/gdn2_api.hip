@@ -97,13 +97,13 @@ Dims dims(const gdn2_desc* d) {
 
 void residual_sizes(const gdn2_desc* d, size_t sz[GDN2_RES_COUNT]) {
   const Dims x = dims(d);
-  sz[GDN2_RES_AQKT] = x.n_chunks * x.tT * 4;
+  sz[GDN2_RES_AQK] = x.n_chunks * x.tT * 4;
   sz[GDN2_RES_A] = x.n_chunks * x.tT * 4;
   sz[GDN2_RES_HPRE] = x.n_chunks * x.DD * 4;
   sz[GDN2_RES_VNEW] = x.n_chunks * x.tD * 4;
   sz[GDN2_RES_WPT] = x.n_chunks * x.tD * 4;
   sz[GDN2_RES_KG] = x.n_chunks * x.tD * 4;
-  sz[GDN2_RES_QGT] = x.n_chunks * x.tD * 4;
+  sz[GDN2_RES_QG] = x.n_chunks * x.tD * 4;
   sz[GDN2_RES_GL] = x.n_chunks * x.D * 4;
 }
 
@@ -168,14 +168,15 @@ int gdn2_residual_layout(const gdn2_desc* d, size_t offsets[GDN2_RES_COUNT], siz
   return GDN2_OK;
 }
 
-// forward workspace (fragment layouts): [Wp | U^T | Kg^T | Qg | Aqk], and without a residual
-// also [gl | h_pre | v_new] (the scan's per-chunk outputs that the output kernel reads).
+// forward workspace (fragment layouts): [Wp | U^T | Kg^T], and without a residual also
+// [Qg | Aqk | gl | h_pre | v_new] (with a residual those live in it).
 size_t gdn2_fwd_workspace_bytes(const gdn2_desc* d, int with_residual) {
   if (validate(d)) return 0;
   const Dims x = dims(d);
-  size_t n = 4 * align_up(x.n_chunks * x.tD * 4) + align_up(x.n_chunks * x.tT * 4);
+  size_t n = 3 * align_up(x.n_chunks * x.tD * 4);
   if (!with_residual)
-    n += align_up(x.n_chunks * x.D * 4) + align_up(x.n_chunks * x.DD * 4) + align_up(x.n_chunks * x.tD * 4);
+    n += align_up(x.n_chunks * x.tD * 4) + align_up(x.n_chunks * x.tT * 4) + align_up(x.n_chunks * x.D * 4) +
+         align_up(x.n_chunks * x.DD * 4) + align_up(x.n_chunks * x.tD * 4);
   return n;
 }
 
@@ -208,22 +209,23 @@ int fwd_impl(const gdn2_desc* d, const void* q, const void* k, const void* v, co
   float* wp = take(x.n_chunks * x.tD * 4);
   float* uT = take(x.n_chunks * x.tD * 4);
   float* kgT = take(x.n_chunks * x.tD * 4);
-  float* qg = take(x.n_chunks * x.tD * 4);
-  float* aqk = take(x.n_chunks * x.tT * 4);
-  // residuals for the backward -- training only; otherwise gl / h_pre / v_new live in the workspace
-  float *aqkT = nullptr, *A = nullptr, *wpT = nullptr, *kg = nullptr, *qgT = nullptr, *gl, *hpre, *vnew;
+  // residuals for the backward -- training only; otherwise Qg / Aqk / gl / h_pre / v_new live in
+  // the workspace
+  float *A = nullptr, *wpT = nullptr, *kg = nullptr, *qg, *aqk, *gl, *hpre, *vnew;
   if (residual) {
     size_t off[GDN2_RES_COUNT], tot;
     residual_offsets(d, off, &tot);
-    aqkT = at<float>(residual, off[GDN2_RES_AQKT]);
+    aqk = at<float>(residual, off[GDN2_RES_AQK]);
     A = at<float>(residual, off[GDN2_RES_A]);
     hpre = at<float>(residual, off[GDN2_RES_HPRE]);
     vnew = at<float>(residual, off[GDN2_RES_VNEW]);
     wpT = at<float>(residual, off[GDN2_RES_WPT]);
     kg = at<float>(residual, off[GDN2_RES_KG]);
-    qgT = at<float>(residual, off[GDN2_RES_QGT]);
+    qg = at<float>(residual, off[GDN2_RES_QG]);
     gl = at<float>(residual, off[GDN2_RES_GL]);
   } else {
+    qg = take(x.n_chunks * x.tD * 4);
+    aqk = take(x.n_chunks * x.tT * 4);
     gl = take(x.n_chunks * x.D * 4);
     hpre = take(x.n_chunks * x.DD * 4);
     vnew = take(x.n_chunks * x.tD * 4);
@@ -231,8 +233,8 @@ int fwd_impl(const gdn2_desc* d, const void* q, const void* k, const void* v, co
 
   gdn2::WyFwdArgs wa{};
   wa.q = q; wa.k = k; wa.v = v; wa.w = w; wa.b = b; wa.g = g;
-  wa.wp_f = wp; wa.wpT_f = wpT; wa.uT_f = uT; wa.kg_f = kg; wa.kgT_f = kgT; wa.qg_f = qg; wa.qgT_f = qgT;
-  wa.aqk_f = aqk; wa.aqkT_f = aqkT; wa.A = A; wa.gl = gl;
+  wa.wp_f = wp; wa.wpT_f = wpT; wa.uT_f = uT; wa.kg_f = kg; wa.kgT_f = kgT; wa.qg_f = qg;
+  wa.aqk_f = aqk; wa.A = A; wa.gl = gl;
   wa.n_chunks = (int)x.n_chunks;
   wa.cfg = cfg;
   hipError_t e = timed(0, s, [&] { return gdn2::launch_wy_fwd(d->D, wa, s, bf16); });
@@ -278,13 +280,13 @@ int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v,
   size_t off[GDN2_RES_COUNT], tot;
   residual_offsets(d, off, &tot);
   void* res = const_cast<void*>(residual);
-  const float* aqkT = at<float>(res, off[GDN2_RES_AQKT]);
+  const float* aqk = at<float>(res, off[GDN2_RES_AQK]);
   const float* A = at<float>(res, off[GDN2_RES_A]);
   const float* hpre = at<float>(res, off[GDN2_RES_HPRE]);
   const float* vnew = at<float>(res, off[GDN2_RES_VNEW]);
   const float* wpT = at<float>(res, off[GDN2_RES_WPT]);
   const float* kg = at<float>(res, off[GDN2_RES_KG]);
-  const float* qgT = at<float>(res, off[GDN2_RES_QGT]);
+  const float* qg = at<float>(res, off[GDN2_RES_QG]);
   const float* gl = at<float>(res, off[GDN2_RES_GL]);
 
   size_t o2 = 0;
@@ -297,7 +299,7 @@ int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v,
   float* xo = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
   float* yo = at<float>(workspace, o2);
 
-  gdn2::BwdPreArgs pa{aqkT, qgT, d_o, xo, yo, (int)x.n_chunks, cfg};
+  gdn2::BwdPreArgs pa{aqk, qg, d_o, xo, yo, (int)x.n_chunks, cfg};
   hipError_t e = timed(6, s, [&] { return gdn2::launch_bwd_pre(d->D, pa, s); });
   if (e != hipSuccess) return hip_fail(e, "bwd_pre launch");
 

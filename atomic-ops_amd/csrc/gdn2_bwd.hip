@@ -677,7 +677,8 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
 //   X = Aqk^T dO (T x D),  Y = Qg^T (s dO) (D x D)
 // as MFMA tiles whose accumulators are exactly the fragment blocks the scan loads: tile
 // (tp, vb) of X is block (vb, tp) of FA(X^T), tile (kb, vb) of Y is block (vb, kb) of FA(Y^T).
-// A operands straight from FA(Aqk^T) / FA(Qg^T); the B operand (dO columns) from LDS.
+// A operands: blocks of Aqk^T / Qg^T, i.e. blocks of FA(Aqk) / FA(Qg) (the forward's
+// residual) turned around by a per-wave LDS transpose; the B operand (dO columns) from LDS.
 // ------------------------------------------------------------------------------------
 template <int D, int B3>
 __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdPreArgs a) {
@@ -686,6 +687,26 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdPreArgs a) {
   const int chunk = blockIdx.x, tid = threadIdx.x, w = wave_id(), l = lane_id(), r = l & 15, g = l >> 4;
   const size_t tb = (size_t)chunk * T * D, sb = (size_t)chunk * T * T, hb = (size_t)chunk * D * D;
   const float* __restrict__ dout = a.dout + tb;
+  // A operands, once per wave: X row block tp = w (all four k blocks: the blocks u < tp of
+  // Aqk^T are exact zeros), Y row blocks kb = w + NW m.  Block (w, u) of Aqk^T in the operand
+  // layout is block (u, w) of Aqk in the accumulator layout: FA(Aqk) block (u, w) transposed.
+  // The transpose tiles lie in sOT, which is filled after a barrier.
+  static_assert(NW * 16 * TRP <= D * LT, "transpose tiles fit in the dO^T buffer");
+  float* tr = sOT + w * 16 * TRP;
+  float4 ax[4], ay[NYW][4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    ax[u] = ld4(a.aqk_f + sb + frag_blk(u, w, T) + 4 * l);
+#pragma unroll
+    for (int m = 0; m < NYW; ++m) ay[m][u] = ld4(a.qg_f + tb + frag_blk(u, w + NW * m, D) + 4 * l);
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    ax[u] = wave_transpose16(tr, ax[u], r, g);
+#pragma unroll
+    for (int m = 0; m < NYW; ++m) ay[m][u] = wave_transpose16(tr, ay[m][u], r, g);
+  }
+  __syncthreads();
   for (int f = tid; f < T * D / 4; f += NT) {
     const int t = f / (D / 4), c = 4 * (f % (D / 4));
     const float4 x = ld4(dout + t * D + c);
@@ -693,15 +714,6 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdPreArgs a) {
     sOT[(c + 1) * LT + t] = x.y;
     sOT[(c + 2) * LT + t] = x.z;
     sOT[(c + 3) * LT + t] = x.w;
-  }
-  // A operands, loaded once per wave: X row block tp = w (all four k blocks: the blocks u < tp
-  // of Aqk^T are exact zeros), Y row blocks kb = w + NW m
-  float4 ax[4], ay[NYW][4];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    ax[u] = ld4(a.aqkT_f + sb + frag_blk(w, u, T) + 4 * l);
-#pragma unroll
-    for (int m = 0; m < NYW; ++m) ay[m][u] = ld4(a.qgT_f + tb + frag_blk(w + NW * m, u, T) + 4 * l);
   }
   __syncthreads();
   const float scale = a.cfg.scale;

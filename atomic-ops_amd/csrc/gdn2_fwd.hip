@@ -215,11 +215,11 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
 
   // 2a. row fragments (cd_slim.py:17-21): FA(Kg) with kg = san(k e^{min(gl-gc,0)}),
   //     FA(Qg) with qg = san(q e^{min(gc,0)}); b*k and w*v into LDS.
-  // 2b. column fragments FA(Kg^T), FA(Qg^T) (D x T): the wave holds one whole 16x16 block of k
-  //     and q per item (block wv + 8 it), which a per-wave LDS transpose (in S, free until the
-  //     scores) turns into lane l of the transposed block: 4 consecutive tokens of one channel.
+  // 2b. column fragments FA(Kg^T) (D x T): the wave holds one whole 16x16 block of k per item
+  //     (block wv + 8 it), which a per-wave LDS transpose (in S, free until the scores) turns
+  //     into lane l of the transposed block: 4 consecutive tokens of one channel.
   float* tr = sS + wv * 16 * TRP;
-  const bool colf = a.kgT_f || a.qgT_f;
+  const bool colf = a.kgT_f != nullptr;
 #pragma unroll
   for (int it = 0; it < NIT; ++it) {
     const int f = tid + it * NT, blk = f >> 6, ln = f & 63;
@@ -241,19 +241,12 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
       // lane (r, g): channel dc = 16 bj + r at tokens i0 + e, e = 0..3
       const int bi = blk / NKB, bj = blk % NKB, dc = 16 * bj + r, i0 = 16 * bi + 4 * g;
       const float4 kc = wave_transpose16(tr, xk[it], r, g);
-      const float4 qc = wave_transpose16(tr, xq[it], r, g);
       const float gl = sG[(T - 1) * LD + dc];
-      const float kv4[4] = {kc.x, kc.y, kc.z, kc.w}, qv4[4] = {qc.x, qc.y, qc.z, qc.w};
-      float kt[4], qt[4];
+      const float kv4[4] = {kc.x, kc.y, kc.z, kc.w};
+      float kt[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float gi = sG[(i0 + e) * LD + dc];
-        kt[e] = sanitize(kv4[e] * exp_nonpos(gl - gi), clip);
-        qt[e] = sanitize(qv4[e] * exp_nonpos(gi), clip);
-      }
-      const size_t o = tb + frag_blk(bj, bi, T) + 4 * l;
-      if (a.kgT_f) st4(a.kgT_f + o, make_float4(kt[0], kt[1], kt[2], kt[3]));
-      if (a.qgT_f) st4(a.qgT_f + o, make_float4(qt[0], qt[1], qt[2], qt[3]));
+      for (int e = 0; e < 4; ++e) kt[e] = sanitize(kv4[e] * exp_nonpos(gl - sG[(i0 + e) * LD + dc]), clip);
+      st4(a.kgT_f + tb + frag_blk(bj, bi, T) + 4 * l, make_float4(kt[0], kt[1], kt[2], kt[3]));
     }
   }
   if (a.gl && tid < D) a.gl[(size_t)chunk * D + tid] = sG[(T - 1) * LD + tid];
@@ -321,13 +314,11 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
   }
   __syncthreads();
 
-  // 5a. FA(Aqk), FA(Aqk^T); X = b k e^{min(gc,0)} in place (cd_slim.py:17); leaf inverses
-  for (int f = tid; f < T * T / 4; f += NT) {
-    const int blk = f >> 6, ln = f & 63, bi = blk >> 2, bj = blk & 3, rr = ln & 15, gg = ln >> 4;
-    if (a.aqk_f) st4(a.aqk_f + sb + 4 * f, ld4(sS + (16 * bi + rr) * LT + 16 * bj + 4 * gg));
-    if (a.aqkT_f) {
-      const float* p = sS + (16 * bj + 4 * gg) * LT + 16 * bi + rr;
-      st4(a.aqkT_f + sb + 4 * f, make_float4(p[0], p[LT], p[2 * LT], p[3 * LT]));
+  // 5a. FA(Aqk); X = b k e^{min(gc,0)} in place (cd_slim.py:17); leaf inverses
+  if (a.aqk_f) {
+    for (int f = tid; f < T * T / 4; f += NT) {
+      const int blk = f >> 6, ln = f & 63, bi = blk >> 2, bj = blk & 3, rr = ln & 15, gg = ln >> 4;
+      st4(a.aqk_f + sb + 4 * f, ld4(sS + (16 * bi + rr) * LT + 16 * bj + 4 * gg));
     }
   }
   for (int f = tid; f < T * D / 4; f += NT) {

@@ -27,13 +27,13 @@ struct Cfg {
 
 // Per-chunk outputs of the WY build.  "_f" outputs are in fragment layout (gdn2_common.hpp):
 //   wp_f FA(Wp) (T x D), wpT_f FA(Wp^T) (D x T), uT_f FA(U^T) (D x T), kg_f FA(Kg) (T x D),
-//   kgT_f FA(Kg^T) (D x T), qg_f FA(Qg) (T x D), qgT_f FA(Qg^T) (D x T), aqk_f FA(Aqk) (T x T),
-//   aqkT_f FA(Aqk^T) (T x T).  A (T x T) and gl (D) are row-major.  The plain row-major
+//   kgT_f FA(Kg^T) (D x T), qg_f FA(Qg) (T x D), aqk_f FA(Aqk) (T x T).  A (T x T) and gl (D)
+//   are row-major.  The plain row-major
 //   aqk / akk / wp / u / kg / qg are written only for the stage-level entry point.  Any
 //   pointer may be null (not written).
 struct WyFwdArgs {
   const void *q, *k, *v, *w, *b, *g;   // fp32, or bfloat16 bits for the bf16-input variant
-  float *wp_f, *wpT_f, *uT_f, *kg_f, *kgT_f, *qg_f, *qgT_f, *aqk_f, *aqkT_f;
+  float *wp_f, *wpT_f, *uT_f, *kg_f, *kgT_f, *qg_f, *aqk_f;
   float *A, *gl;
   float *aqk, *akk, *wp, *u, *kg, *qg;
   int n_chunks;
@@ -59,9 +59,9 @@ struct OutFwdArgs {
 };
 
 // The reverse scan's dO terms, chunk-parallel: X = Aqk^T dO as FA(X^T) (D x T) and
-// Y = s Qg^T dO as FA(Y^T) (D x D), from FA(Aqk^T), FA(Qg^T) and dO (row-major).
+// Y = s Qg^T dO as FA(Y^T) (D x D), from FA(Aqk), FA(Qg) and dO (row-major).
 struct BwdPreArgs {
-  const float *aqkT_f, *qgT_f, *dout;
+  const float *aqk_f, *qg_f, *dout;
   float *x_f, *y_f;
   int n_chunks;
   Cfg cfg;

@@ -53,20 +53,20 @@ typedef struct gdn2_desc {
 
 /* Residual buffer written by gdn2_fwd and read by gdn2_bwd: sub-buffers at the offsets
  * reported by gdn2_residual_layout (bytes, 256-aligned), float32, per chunk:
- *   AQKT  (B,H,nc, bt*bt)  gated q.k scores, transposed, FRAG(Aqk^T)            (pipeline.py:25)
+ *   AQK   (B,H,nc, bt*bt)  gated q.k scores, FRAG(Aqk)                         (pipeline.py:25)
  *   A     (B,H,nc,bt,bt)   the WY inverse (I + (1-eps) Akk)^-1, row-major        (pipeline.py:25)
  *   HPRE  (B,H,nc, D*D)    state entering each chunk, FRAG(h_pre^T)              (cd_slim.py:22)
  *   VNEW  (B,H,nc, D*bt)   v_new of each chunk, FRAG(v_new^T)                    (cd_slim.py:23)
  *   WPT   (B,H,nc, D*bt)   W = A (b k e^gc), FRAG(W^T)                           (cd_slim.py:17)
  *   KG    (B,H,nc, bt*D)   gated k, FRAG(Kg)                                     (cd_slim.py:20)
- *   QGT   (B,H,nc, D*bt)   gated q, FRAG(Qg^T)                                   (cd_slim.py:21)
+ *   QG    (B,H,nc, bt*D)   gated q, FRAG(Qg)                                     (cd_slim.py:21)
  *   GL    (B,H,nc,D)       gc of the chunk's last row                            (cd_slim.py:19)
  * FRAG(M) of an R x C matrix M is the MFMA fragment order the kernels load with one
  * coalesced float4 per lane: 16x16 blocks in row-major block order (C/16 blocks per block
  * row, 256 floats each); inside a block, floats [4 l, 4 l + 4) with l = r + 16 c hold
  * M[16 bi + r][16 bj + 4 c + e], e = 0..3 (r = 0..15, c = 0..3). */
-enum { GDN2_RES_AQKT = 0, GDN2_RES_A, GDN2_RES_HPRE, GDN2_RES_VNEW, GDN2_RES_WPT, GDN2_RES_KG,
-       GDN2_RES_QGT, GDN2_RES_GL, GDN2_RES_COUNT };
+enum { GDN2_RES_AQK = 0, GDN2_RES_A, GDN2_RES_HPRE, GDN2_RES_VNEW, GDN2_RES_WPT, GDN2_RES_KG,
+       GDN2_RES_QG, GDN2_RES_GL, GDN2_RES_COUNT };
 
 int gdn2_abi_version(void);
 const char* gdn2_last_error(void);
