@@ -45,13 +45,15 @@ __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp
 
 __device__ __forceinline__ float exp_nonpos(float x) { return fast_exp(fminf(x, 0.f)); }
 
-// ---- bfloat16 helpers: round-to-nearest-even, NaN kept quiet ------------------------
-__device__ __forceinline__ uint32_t bf16_bits(float x) {
-  uint32_t u = __float_as_uint(x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+// ---- bfloat16 helpers: round-to-nearest-even (NaN stays NaN) --------------------------
+// Two floats to two bfloat16, packed a | b << 16, by one v_cvt_pk_bf16_f32.
+typedef float f2v __attribute__((ext_vector_type(2)));
+typedef __bf16 b2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t bf16_pack(float a, float b) {
+  const f2v f = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, b2v));
 }
+__device__ __forceinline__ uint32_t bf16_bits(float x) { return bf16_pack(x, 0.f) & 0xffffu; }
 __device__ __forceinline__ float bf16_val(uint32_t h) { return __uint_as_float(h << 16); }
 __device__ __forceinline__ float bf16_round(float x) { return bf16_val(bf16_bits(x)); }
 
@@ -129,22 +131,32 @@ __device__ __forceinline__ void mma_tile_f32(f4& acc, const View& A, const View&
   for (int k0 = 0; k0 < K; k0 += 4) mfma_f32x1(acc, A.at(r, k0 + g), B.at(k0 + g, r));
 }
 
+// hi = bf16(x), lo = bf16(x - hi), four packed conversions per float4
+__device__ __forceinline__ void split4(const float4& x, s4& hi, s4& lo) {
+  const uint32_t h01 = bf16_pack(x.x, x.y), h23 = bf16_pack(x.z, x.w);
+  const uint32_t l01 = bf16_pack(x.x - __uint_as_float(h01 << 16), x.y - __uint_as_float(h01 & 0xffff0000u));
+  const uint32_t l23 = bf16_pack(x.z - __uint_as_float(h23 << 16), x.w - __uint_as_float(h23 & 0xffff0000u));
+  hi = __builtin_bit_cast(s4, make_uint2(h01, h23));
+  lo = __builtin_bit_cast(s4, make_uint2(l01, l23));
+}
+__device__ __forceinline__ s4 round4(const float4& x) {
+  return __builtin_bit_cast(s4, make_uint2(bf16_pack(x.x, x.y), bf16_pack(x.z, x.w)));
+}
+
 template <bool THREE>
 __device__ __forceinline__ void mma_tile_bf16(f4& acc, const View& A, const View& B, int K) {
   const int l = lane_id(), r = l & 15, g = l >> 4;
   for (int k0 = 0; k0 < K; k0 += 16) {
+    const int kk = k0 + 4 * g;
+    const float4 a = make_float4(A.at(r, kk), A.at(r, kk + 1), A.at(r, kk + 2), A.at(r, kk + 3));
+    const float4 b = make_float4(B.at(kk, r), B.at(kk + 1, r), B.at(kk + 2, r), B.at(kk + 3, r));
     s4 ah, bh, al, bl;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float a = A.at(r, k0 + 4 * g + e);
-      const float b = B.at(k0 + 4 * g + e, r);
-      const uint32_t ha = bf16_bits(a), hb = bf16_bits(b);
-      ah[e] = (short)ha;
-      bh[e] = (short)hb;
-      if (THREE) {
-        al[e] = (short)bf16_bits(a - bf16_val(ha));
-        bl[e] = (short)bf16_bits(b - bf16_val(hb));
-      }
+    if (THREE) {
+      split4(a, ah, al);
+      split4(b, bh, bl);
+    } else {
+      ah = round4(a);
+      bh = round4(b);
     }
     if (THREE) mfma_bf16x3(acc, ah, al, bh, bl);
     else mfma_bf16x1(acc, ah, bh);
@@ -159,21 +171,6 @@ __device__ __forceinline__ void mma_tile_bf16(f4& acc, const View& A, const View
 // The 16x16 result layout (lane l holds rows 4g..4g+3 of column l%16) is the B-operand
 // layout of the next k block, so a tile produced by one MFMA chain feeds another directly.
 // mma16 does not drain: callers chain several and drain() before reading the result.
-__device__ __forceinline__ void split4(const float4& x, s4& hi, s4& lo) {
-  const float v[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const uint32_t h = bf16_bits(v[e]);
-    hi[e] = (short)h;
-    lo[e] = (short)bf16_bits(v[e] - bf16_val(h));
-  }
-}
-__device__ __forceinline__ s4 round4(const float4& x) {
-  s4 h;
-  h[0] = (short)bf16_bits(x.x); h[1] = (short)bf16_bits(x.y);
-  h[2] = (short)bf16_bits(x.z); h[3] = (short)bf16_bits(x.w);
-  return h;
-}
 // The dot mode is a template parameter everywhere an MFMA is issued: a runtime switch would
 // put branches between the MFMAs of a chain, and at the merge points the compiler copies
 // the accumulator right after the (opaque) asm MFMA -- a read it cannot know to delay.
