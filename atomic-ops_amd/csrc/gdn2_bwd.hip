@@ -129,9 +129,9 @@ __global__ __launch_bounds__(D / 16 * WAVE) void bwd_state_kernel(BwdStateArgs a
 #pragma unroll
   for (int ti = 0; ti < 4; ++ti) {
     const size_t o = tb + frag_blk(kt, ti, T) + 4 * l;
-    st4(a.dqg + o, f4_to_float4(acc[0][ti]));
-    st4(a.dwp + o, f4_to_float4(acc[1][ti]));
-    st4(a.dkg + o, f4_to_float4(acc[2][ti]));
+    stg4(a.dqg + o, f4_to_float4(acc[0][ti]));
+    stg4(a.dwp + o, f4_to_float4(acc[1][ti]));
+    stg4(a.dkg + o, f4_to_float4(acc[2][ti]));
   }
   // the four lanes of key row 16 kt + r hold the value blocks 4 g .. 4 g + 3 of every kb
   part += __shfl_xor(part, 16);
@@ -220,37 +220,11 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     return make_float4(p[0], p[D], p[2 * D], p[3 * D]);
   };
   // the same for a T x D tensor stored as FA(x^T): one float4 of block (strip, t)
-  auto fcol4 = [&](const float* __restrict__ x, int t) { return ld4(x + frag_blk(strip, t, T) + 4 * l); };
+  auto fcol4 = [&](const float* __restrict__ x, int t) { return ldg4(x + frag_blk(strip, t, T) + 4 * l); };
 
-  // T x D row-major global tile -> LDS (row stride LD), coalesced float4
-  auto copy_rows = [&](float* dst, const float* __restrict__ src) {
-    for (int f = tid; f < T * D / 4; f += NT) {
-      const int i = f / (D / 4), d = 4 * (f % (D / 4));
-      st4(dst + i * LD + d, ld4(src + i * D + d));
-    }
-  };
-
-  // X1 = v_new, X2 = dO, sA = A, sG = gc
-  load_fragT<LD>(sX1, a.v_new_f + tb, D, T, 0, T, tid, NT);
-  copy_rows(sX2, dout);
-  for (int f = tid; f < T * T / 4; f += NT) st4(sA + (f >> 4) * LT + 4 * (f & 15), ld4(a.A + sb + 4 * f));
-  chunk_cumsum<D, LD, NT>(a.g + tb, sG);          // ends with a barrier
-
-  // The P2 operands' global loads are spread between P1's MFMAs (a burst of loads stalls the
-  // issuing wave while the CU's memory path is busy).  Item f of the row-major inputs is float4
-  // f; item f of a FRAG(x^T) (dWp) or FRAG(x) (dv_new) input is float4 f as well, placed into
-  // the row-major tile by put_fragT / put_frag.
-  constexpr int NIT = T * D / 4 / NT;
-  float4 xb[NIT], xk[NIT], xw[NIT], xv[NIT], xdw[NIT], xdv[NIT];
-  auto prefetch = [&](int item) {
-    const int arr = item / NIT, it = item % NIT, f = tid + it * NT;
-    if (arr == 0) xb[it] = ld4(b + 4 * f);
-    else if (arr == 1) xk[it] = ld4(k + 4 * f);
-    else if (arr == 2) xw[it] = ld4(w + 4 * f);
-    else if (arr == 3) xv[it] = ld4(v + 4 * f);
-    else if (arr == 4) xdw[it] = ld4(dwp + 4 * f);
-    else xdv[it] = ld4(a.dv_new_f + tb + 4 * f);
-  };
+  // Item f of a row-major input is float4 f; item f of a FRAG(x^T) (v_new, dWp) or FRAG(x)
+  // (dv_new) input is float4 f as well, placed into the row-major tile by put_fragT / put_frag.
+  constexpr int NIT = T * D / 4 / NT, NIA = T * T / 4 / NT;
   auto put_frag = [&](float* dst, const float4& x, int f) {
     const int lane = f & 63, blk = f >> 6;
     st4(dst + (16 * (blk / NKB) + (lane & 15)) * LD + 16 * (blk % NKB) + 4 * (lane >> 4), x);
@@ -262,6 +236,45 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     dst[(m + 1) * LD + n] = x.y;
     dst[(m + 2) * LD + n] = x.z;
     dst[(m + 3) * LD + n] = x.w;
+  };
+
+  // X1 = v_new, X2 = dO, sA = A, sG = gc.  Every load is issued before the cumsum waits for
+  // its g: one memory round trip for the whole prologue.
+  {
+    float4 xvn[NIT], xdo[NIT], xa[NIA];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      xvn[it] = ldg4(a.v_new_f + tb + 4 * (tid + it * NT));
+      xdo[it] = ldg4(dout + 4 * (tid + it * NT));
+    }
+#pragma unroll
+    for (int it = 0; it < NIA; ++it) xa[it] = ldg4(a.A + sb + 4 * (tid + it * NT));
+    chunk_cumsum<D, LD, NT, true>(a.g + tb, sG);
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const int f = tid + it * NT;
+      put_fragT(sX1, xvn[it], f);
+      st4(sX2 + (f / (D / 4)) * LD + 4 * (f % (D / 4)), xdo[it]);
+    }
+#pragma unroll
+    for (int it = 0; it < NIA; ++it) {
+      const int f = tid + it * NT;
+      st4(sA + (f >> 4) * LT + 4 * (f & 15), xa[it]);
+    }
+  }
+  __syncthreads();
+
+  // The P2 operands' global loads are spread between P1's MFMAs (a burst of loads stalls the
+  // issuing wave while the CU's memory path is busy).
+  float4 xb[NIT], xk[NIT], xw[NIT], xv[NIT], xdw[NIT], xdv[NIT];
+  auto prefetch = [&](int item) {
+    const int arr = item / NIT, it = item % NIT, f = tid + it * NT;
+    if (arr == 0) xb[it] = ld4(b + 4 * f);
+    else if (arr == 1) xk[it] = ld4(k + 4 * f);
+    else if (arr == 2) xw[it] = ld4(w + 4 * f);
+    else if (arr == 3) xv[it] = ld4(v + 4 * f);
+    else if (arr == 4) xdw[it] = ld4(dwp + 4 * f);
+    else xdv[it] = ldg4(a.dv_new_f + tb + 4 * f);
   };
 
   // P1: dAqk = (dO v_new^T) * causal; 16 tiles, two per wave
@@ -631,11 +644,11 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     }
     // lane (r, g) after the transpose: row 16 rt + r, columns 16 strip + 4 g .. + 3
     const int ro = (16 * rt + r) * D + 16 * strip + 4 * g;
-    st4(o_dw + ro, wave_transpose16(tr, make_float4(ow[0], ow[1], ow[2], ow[3]), r, g));
-    st4(o_dv + ro, wave_transpose16(tr, make_float4(ov[0], ov[1], ov[2], ov[3]), r, g));
-    st4(o_dq + ro, wave_transpose16(tr, make_float4(oq[0], oq[1], oq[2], oq[3]), r, g));
-    st4(o_dk + ro, wave_transpose16(tr, make_float4(ok[0], ok[1], ok[2], ok[3]), r, g));
-    st4(o_db + ro, wave_transpose16(tr, make_float4(ob[0], ob[1], ob[2], ob[3]), r, g));
+    stg4(o_dw + ro, wave_transpose16(tr, make_float4(ow[0], ow[1], ow[2], ow[3]), r, g));
+    stg4(o_dv + ro, wave_transpose16(tr, make_float4(ov[0], ov[1], ov[2], ov[3]), r, g));
+    stg4(o_dq + ro, wave_transpose16(tr, make_float4(oq[0], oq[1], oq[2], oq[3]), r, g));
+    stg4(o_dk + ro, wave_transpose16(tr, make_float4(ok[0], ok[1], ok[2], ok[3]), r, g));
+    stg4(o_db + ro, wave_transpose16(tr, make_float4(ob[0], ob[1], ob[2], ob[3]), r, g));
   }
   // last-row decay gradient: sum over all rows of the column (lanes g, then the waves of the
   // strip in order) + e^gamma sum_v(dh_next h_pre) [gl < 0]
@@ -668,7 +681,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     float4 off = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int s2 = NSEG - 1; s2 > sg; --s2) off = add4(off, ld4(sTot + s2 * LD + d));
 #pragma unroll
-    for (int i = 0; i < RUN; ++i) st4(a.dg + tb + (sg * RUN + i) * D + d, san4(add4(x[i], off), clip));
+    for (int i = 0; i < RUN; ++i) stg4(a.dg + tb + (sg * RUN + i) * D + d, san4(add4(x[i], off), clip));
   }
 }
 
@@ -696,9 +709,9 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdPreArgs a) {
   float4 ax[4], ay[NYW][4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
-    ax[u] = ld4(a.aqk_f + sb + frag_blk(u, w, T) + 4 * l);
+    ax[u] = ldg4(a.aqk_f + sb + frag_blk(u, w, T) + 4 * l);
 #pragma unroll
-    for (int m = 0; m < NYW; ++m) ay[m][u] = ld4(a.qg_f + tb + frag_blk(u, w + NW * m, D) + 4 * l);
+    for (int m = 0; m < NYW; ++m) ay[m][u] = ldg4(a.qg_f + tb + frag_blk(u, w + NW * m, D) + 4 * l);
   }
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
@@ -737,11 +750,11 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdPreArgs a) {
       for (int u = 0; u < 4; ++u) mma16<B3>(accy[m], ay[m][u], bs[u]);
     }
     drain(accx);
-    st4(a.x_f + tb + frag_blk(vb, w, T) + 4 * l, f4_to_float4(accx));
+    stg4(a.x_f + tb + frag_blk(vb, w, T) + 4 * l, f4_to_float4(accx));
 #pragma unroll
     for (int m = 0; m < NYW; ++m) {
       drain(accy[m]);
-      st4(a.y_f + hb + frag_blk(vb, w + NW * m, D) + 4 * l, f4_to_float4(accy[m]));
+      stg4(a.y_f + hb + frag_blk(vb, w + NW * m, D) + 4 * l, f4_to_float4(accy[m]));
     }
   }
 }

@@ -201,7 +201,27 @@ __device__ __forceinline__ float4 in_ld4(const uint16_t* p) {
   return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
                      __uint_as_float(u.y & 0xffff0000u));
 }
+// Global load with the non-temporal hint, for the last read of a value by any kernel of the
+// operator: the line is not kept in the caches, which leaves room for values read again (in
+// this kernel, or by a later one).
+typedef unsigned u2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float4 ldg4(const float* p) {
+  const f4 v = __builtin_nontemporal_load(reinterpret_cast<const f4*>(p));
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ float4 in_ldg4(const float* p) { return ldg4(p); }
+__device__ __forceinline__ float4 in_ldg4(const uint16_t* p) {
+  const u2v u = __builtin_nontemporal_load(reinterpret_cast<const u2v*>(p));
+  return make_float4(__uint_as_float(u[0] << 16), __uint_as_float(u[0] & 0xffff0000u), __uint_as_float(u[1] << 16),
+                     __uint_as_float(u[1] & 0xffff0000u));
+}
 __device__ __forceinline__ void st4(float* p, const float4& x) { *reinterpret_cast<float4*>(p) = x; }
+// Global store with the non-temporal (streaming) hint, for outputs that only a later kernel
+// reads: they then do not evict from L2 the inputs that the writing kernel reads again.
+__device__ __forceinline__ void stg4(float* p, const float4& x) {
+  const f4 v = {x.x, x.y, x.z, x.w};
+  __builtin_nontemporal_store(v, reinterpret_cast<f4*>(p));
+}
 
 template <int MODE>
 __device__ __forceinline__ void mma_tile(f4& acc, const View& A, const View& B, int K) {
@@ -321,20 +341,26 @@ __device__ __forceinline__ float4 wave_transpose16(float* tr, const float4 x, in
 // Thread t owns float4 column t % (D/4) over a run of RUN consecutive rows: it sums its run,
 // then adds the totals of the runs above it in order.  Same code in every kernel, so every
 // kernel sees bit-identical gc.
-template <int D, int LD, int NTHREADS, typename TIn>
+// LAST_READ: g is not read again by a later kernel (loaded with the non-temporal hint).
+template <int D, int LD, int NTHREADS, bool LAST_READ = false, typename TIn>
 __device__ __forceinline__ void chunk_cumsum(const TIn* __restrict__ g, float* sG) {
   constexpr int NQ = D / 4, NSEG = NTHREADS / NQ, RUN = T / NSEG;
   static_assert(NTHREADS % NQ == 0 && T % NSEG == 0 && RUN >= 1, "cumsum split");
   const int t = threadIdx.x, d = 4 * (t % NQ), s = t / NQ;
   float4 x[RUN];
 #pragma unroll
-  for (int i = 0; i < RUN; ++i) x[i] = in_ld4(g + (s * RUN + i) * D + d);
+  for (int i = 0; i < RUN; ++i) x[i] = LAST_READ ? in_ldg4(g + (s * RUN + i) * D + d) : in_ld4(g + (s * RUN + i) * D + d);
 #pragma unroll
   for (int i = 1; i < RUN; ++i) x[i] = add4(x[i - 1], x[i]);
   st4(sG + (s * RUN + RUN - 1) * LD + d, x[RUN - 1]);
   __syncthreads();
+  // the run totals above are read all at once, then added in order
+  float4 tot[NSEG - 1];
+#pragma unroll
+  for (int s2 = 0; s2 < NSEG - 1; ++s2) tot[s2] = ld4(sG + (s2 * RUN + RUN - 1) * LD + d);
   float4 off = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int s2 = 0; s2 < s; ++s2) off = add4(off, ld4(sG + (s2 * RUN + RUN - 1) * LD + d));
+#pragma unroll
+  for (int s2 = 0; s2 < NSEG - 1; ++s2) off = s2 < s ? add4(off, tot[s2]) : off;
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < RUN; ++i) st4(sG + (s * RUN + i) * LD + d, add4(off, x[i]));

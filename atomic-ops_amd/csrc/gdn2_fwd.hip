@@ -49,7 +49,14 @@ __device__ __forceinline__ void score_pair(f4& accq, f4& acck, const TIn* __rest
   const TIn* qi = q + i * D;
   const float* bi = sBK + i * LD;
   const TIn* kj = kk + j * D;
-#pragma unroll 2
+  // the raw q / k operands of the whole chain are loaded first (one memory round trip)
+  float4 qa[D / 16], ka[D / 16];
+#pragma unroll
+  for (int kb = 0; kb < D / 16; ++kb) {
+    qa[kb] = in_ld4(qi + 16 * kb + 4 * g);
+    ka[kb] = in_ld4(kj + 16 * kb + 4 * g);
+  }
+#pragma unroll
   for (int kb = 0; kb < D / 16; ++kb) {
     const int d = 16 * kb + 4 * g;
     const float4 vi = ld4(gi + d), vj = ld4(gj + d), va = ld4(ga + d);
@@ -66,8 +73,8 @@ __device__ __forceinline__ void score_pair(f4& accq, f4& acck, const TIn* __rest
       cb = make_float4(fast_exp((va.x - vj.x) - h.x), fast_exp((va.y - vj.y) - h.y), fast_exp((va.z - vj.z) - h.z),
                        fast_exp((va.w - vj.w) - h.w));
     }
-    const float4 bv = mul4(in_ld4(kj + d), cb);
-    mma16<DOT>(accq, mul4(in_ld4(qi + d), ra), bv);
+    const float4 bv = mul4(ka[kb], cb);
+    mma16<DOT>(accq, mul4(qa[kb], ra), bv);
     mma16<DOT>(acck, mul4(ld4(bi + d), ra), bv);
   }
   drain(accq, acck);
@@ -167,7 +174,7 @@ __device__ __forceinline__ void wy_inverse(const Cfg& cf, const float* sK, float
     const int i = f / (T / 4), j = 4 * (f % (T / 4));
     const float4 x = san4(ld4(sI + i * LT + j), cf.clip);
     st4(sI + i * LT + j, x);
-    if (A_out) st4(A_out + i * T + j, x);
+    if (A_out) stg4(A_out + i * T + j, x);
   }
   __syncthreads();
 }
@@ -229,13 +236,13 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
     st4(sY + i * LD + d, mul4(xw[it], xv[it]));
     if (a.kg_f || a.kg) {
       const float4 kg = san4(mul4(xk[it], expnp4(sub4(ld4(sG + (T - 1) * LD + d), gc))), clip);
-      if (a.kg_f) st4(a.kg_f + tb + 4 * f, kg);
-      if (a.kg) st4(a.kg + tb + i * D + d, kg);
+      if (a.kg_f) stg4(a.kg_f + tb + 4 * f, kg);
+      if (a.kg) stg4(a.kg + tb + i * D + d, kg);
     }
     if (a.qg_f || a.qg) {
       const float4 qg = san4(mul4(xq[it], expnp4(gc)), clip);
-      if (a.qg_f) st4(a.qg_f + tb + 4 * f, qg);
-      if (a.qg) st4(a.qg + tb + i * D + d, qg);
+      if (a.qg_f) stg4(a.qg_f + tb + 4 * f, qg);
+      if (a.qg) stg4(a.qg + tb + i * D + d, qg);
     }
     if (colf) {
       // lane (r, g): channel dc = 16 bj + r at tokens i0 + e, e = 0..3
@@ -246,7 +253,7 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
       float kt[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) kt[e] = sanitize(kv4[e] * exp_nonpos(gl - sG[(i0 + e) * LD + dc]), clip);
-      st4(a.kgT_f + tb + frag_blk(bj, bi, T) + 4 * l, make_float4(kt[0], kt[1], kt[2], kt[3]));
+      stg4(a.kgT_f + tb + frag_blk(bj, bi, T) + 4 * l, make_float4(kt[0], kt[1], kt[2], kt[3]));
     }
   }
   if (a.gl && tid < D) a.gl[(size_t)chunk * D + tid] = sG[(T - 1) * LD + tid];
@@ -309,8 +316,8 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
     st4(sS + i * LT + j, aq4);
     st4(sK + i * LT + j, scale4(ak4, cf.ome));
     st4(sI + i * LT + j, make_float4(0.f, 0.f, 0.f, 0.f));
-    if (a.aqk) st4(a.aqk + sb + i * T + j, aq4);
-    if (a.akk) st4(a.akk + sb + i * T + j, ak4);
+    if (a.aqk) stg4(a.aqk + sb + i * T + j, aq4);
+    if (a.akk) stg4(a.akk + sb + i * T + j, ak4);
   }
   __syncthreads();
 
@@ -318,7 +325,7 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
   if (a.aqk_f) {
     for (int f = tid; f < T * T / 4; f += NT) {
       const int blk = f >> 6, ln = f & 63, bi = blk >> 2, bj = blk & 3, rr = ln & 15, gg = ln >> 4;
-      st4(a.aqk_f + sb + 4 * f, ld4(sS + (16 * bi + rr) * LT + 16 * bj + 4 * gg));
+      stg4(a.aqk_f + sb + 4 * f, ld4(sS + (16 * bi + rr) * LT + 16 * bj + 4 * gg));
     }
   }
   for (int f = tid; f < T * D / 4; f += NT) {
@@ -352,7 +359,7 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
         o[0] = p.x; o[D] = p.y; o[2 * D] = p.z; o[3 * D] = p.w;
       }
       float* fT = mat ? a.uT_f : a.wpT_f;
-      if (fT) st4(fT + tb + frag_blk(tj, ti, T) + 4 * l, p);
+      if (fT) stg4(fT + tb + frag_blk(tj, ti, T) + 4 * l, p);
       if (mat == 0 && a.wp_f) {
         sW[(4 * g + 0) * 20 + r] = p.x;
         sW[(4 * g + 1) * 20 + r] = p.y;
@@ -361,7 +368,7 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        st4(a.wp_f + tb + frag_blk(ti, tj, D) + 4 * l, ld4(sW + r * 20 + 4 * g));
+        stg4(a.wp_f + tb + frag_blk(ti, tj, D) + 4 * l, ld4(sW + r * 20 + 4 * g));
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -383,29 +390,48 @@ __global__ __launch_bounds__(256) void out_fwd_kernel(OutFwdArgs a) {
   __shared__ float4 sA[T * T / 4];
   const int chunk = blockIdx.x, tid = threadIdx.x, w = wave_id(), l = lane_id(), r = l & 15, g = l >> 4;
   const size_t tb = (size_t)chunk * T * D, sb = (size_t)chunk * T * T, hb = (size_t)chunk * D * D;
-  const float4* q4 = reinterpret_cast<const float4*>(a.qg_f + tb);
-  const float4* a4 = reinterpret_cast<const float4*>(a.aqk_f + sb);
-  for (int f = tid; f < T * D / 4; f += NW * WAVE) sQ[f] = q4[f];
-  for (int f = tid; f < T * T / 4; f += NW * WAVE) sA[f] = a4[f];
-  __syncthreads();
-  const float scale = a.cfg.scale, clip = a.cfg.clip;
-  for (int cb = w; cb < D / 16; cb += NW) {
-    float4 hT[NKB], vT[4];
+  static_assert(NKB % NW == 0, "whole value blocks per wave");
+  constexpr int NQ4 = T * D / 4 / (NW * WAVE), NA4 = T * T / 4 / (NW * WAVE), NCB = NKB / NW;
+  // every operand of the first value block and the staged tiles in flight at once; the next
+  // value block's A operands are loaded before the current block's MFMAs
+  float4 xq[NQ4], xa[NA4], hT[NKB], vT[4];
+  auto load_block = [&](int cb) {
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) hT[kb] = ld4(a.h_pre_f + hb + frag_blk(cb, kb, D) + 4 * l);
 #pragma unroll
     for (int u = 0; u < 4; ++u) vT[u] = ld4(a.v_new_f + tb + frag_blk(cb, u, T) + 4 * l);
+  };
+#pragma unroll
+  for (int j = 0; j < NQ4; ++j) xq[j] = ld4(a.qg_f + tb + 4 * (tid + j * NW * WAVE));
+#pragma unroll
+  for (int j = 0; j < NA4; ++j) xa[j] = ld4(a.aqk_f + sb + 4 * (tid + j * NW * WAVE));
+  load_block(w);
+#pragma unroll
+  for (int j = 0; j < NQ4; ++j) sQ[tid + j * NW * WAVE] = xq[j];
+#pragma unroll
+  for (int j = 0; j < NA4; ++j) sA[tid + j * NW * WAVE] = xa[j];
+  __syncthreads();
+  const float scale = a.cfg.scale, clip = a.cfg.clip;
+#pragma unroll
+  for (int ic = 0; ic < NCB; ++ic) {
+    const int cb = w + NW * ic;
+    float4 hc[NKB], vc[4];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) hc[kb] = hT[kb];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) vc[u] = vT[u];
+    if (ic + 1 < NCB) load_block(cb + NW);
 #pragma unroll
     for (int tq = 0; tq < 4; ++tq) {
       f4 acc1 = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) mma16<DOT>(acc1, hT[kb], sQ[(tq * NKB + kb) * WAVE + l]);
+      for (int kb = 0; kb < NKB; ++kb) mma16<DOT>(acc1, hc[kb], sQ[(tq * NKB + kb) * WAVE + l]);
 #pragma unroll
-      for (int u = 0; u <= tq; ++u) mma16<DOT>(acc2, vT[u], sA[(tq * 4 + u) * WAVE + l]);
+      for (int u = 0; u <= tq; ++u) mma16<DOT>(acc2, vc[u], sA[(tq * 4 + u) * WAVE + l]);
       drain(acc1, acc2);
       const float4 ov = make_float4(sanitize(scale * acc1[0] + acc2[0], clip), sanitize(scale * acc1[1] + acc2[1], clip),
                                     sanitize(scale * acc1[2] + acc2[2], clip), sanitize(scale * acc1[3] + acc2[3], clip));
-      st4(a.o + tb + (size_t)(16 * tq + r) * D + 16 * cb + 4 * g, ov);
+      stg4(a.o + tb + (size_t)(16 * tq + r) * D + 16 * cb + 4 * g, ov);
     }
   }
 }

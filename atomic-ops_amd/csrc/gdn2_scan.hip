@@ -86,7 +86,7 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_fwd_kernel(ScanFwdArgs a) 
   auto step = [&](const FwdOps& op, int c, FwdOps& nx, int cn) {
     const size_t ch = (size_t)bh * nc + c, tb = ch * T * D;
     const size_t tbn = base(cn) * T * D;
-    st4(a.h_pre_f + ch * D * D + frag_blk(vb, w, D) + 4 * l, f4_to_float4(h));
+    stg4(a.h_pre_f + ch * D * D + frag_blk(vb, w, D) + 4 * l, f4_to_float4(h));
     // partial Wp h over this wave's 16 key rows
     const float4 hb = f4_to_float4(h);
     f4 pv[4];
@@ -109,7 +109,7 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_fwd_kernel(ScanFwdArgs a) 
       for (int w2 = 1; w2 < NW; ++w2) s = add4(s, sPv[w2 * 4 * WAVE + tid]);
       const float4 vn = sub4(op.uu, s);
       sVB[tid] = vn;
-      st4(a.v_new_f + tb + frag_blk(vb, tp, T) + 4 * lp, vn);
+      stg4(a.v_new_f + tb + frag_blk(vb, tp, T) + 4 * lp, vn);
     }
     nx.uu = ld4(a.uT_f + tbn + frag_blk(vb, tp, T) + 4 * lp);
     nx.gm = ld4(a.gl + base(cn) * D + 16 * w + 4 * g);
@@ -239,8 +239,8 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
 #pragma unroll
     for (int e = 0; e < 4; ++e) dh[e] = sanitize((yv[e] + dh[e] * exp_nonpos(gmv[e])) - z[e], clip);
     // stores last: the next step's waits for the prefetch loads above then do not also cover them
-    st4(a.dh_next_f + ch * D * D + frag_blk(w, vb, D) + 4 * l, dhv);
-    if (red) st4(a.dv_new_f + tb + frag_blk(tp, vb, D) + 4 * lp, dvv);
+    stg4(a.dh_next_f + ch * D * D + frag_blk(w, vb, D) + 4 * l, dhv);
+    if (red) stg4(a.dv_new_f + tb + frag_blk(tp, vb, D) + 4 * lp, dvv);
   };
 
   BwdOps A, B;
