@@ -577,7 +577,8 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   float4 ndq4 = fcol4(dqgp, St::rtile(wv, 0)), ndk4 = fcol4(dkgp, St::rtile(wv, 0));
   // The five gradient tiles leave through a per-wave 16x16 LDS transpose (in the dAqk buffer,
   // free once every wave has left B4) as one float4 row store per lane instead of four
-  // scalar column stores.
+  // scalar column stores.  Plain stores: streaming stores complete later, and the next
+  // tile's load waits would cover them.
   static_assert(NW * 16 * TRP <= T * LT, "transpose tiles fit in the dAqk buffer");
   __syncthreads();
   float* tr = sDAq + wv * 16 * TRP;
@@ -644,11 +645,11 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     }
     // lane (r, g) after the transpose: row 16 rt + r, columns 16 strip + 4 g .. + 3
     const int ro = (16 * rt + r) * D + 16 * strip + 4 * g;
-    stg4(o_dw + ro, wave_transpose16(tr, make_float4(ow[0], ow[1], ow[2], ow[3]), r, g));
-    stg4(o_dv + ro, wave_transpose16(tr, make_float4(ov[0], ov[1], ov[2], ov[3]), r, g));
-    stg4(o_dq + ro, wave_transpose16(tr, make_float4(oq[0], oq[1], oq[2], oq[3]), r, g));
-    stg4(o_dk + ro, wave_transpose16(tr, make_float4(ok[0], ok[1], ok[2], ok[3]), r, g));
-    stg4(o_db + ro, wave_transpose16(tr, make_float4(ob[0], ob[1], ob[2], ob[3]), r, g));
+    st4(o_dw + ro, wave_transpose16(tr, make_float4(ow[0], ow[1], ow[2], ow[3]), r, g));
+    st4(o_dv + ro, wave_transpose16(tr, make_float4(ov[0], ov[1], ov[2], ov[3]), r, g));
+    st4(o_dq + ro, wave_transpose16(tr, make_float4(oq[0], oq[1], oq[2], oq[3]), r, g));
+    st4(o_dk + ro, wave_transpose16(tr, make_float4(ok[0], ok[1], ok[2], ok[3]), r, g));
+    st4(o_db + ro, wave_transpose16(tr, make_float4(ob[0], ob[1], ob[2], ob[3]), r, g));
   }
   // last-row decay gradient: sum over all rows of the column (lanes g, then the waves of the
   // strip in order) + e^gamma sum_v(dh_next h_pre) [gl < 0]

@@ -114,10 +114,15 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_fwd_kernel(ScanFwdArgs a) 
     nx.uu = ld4(a.uT_f + tbn + frag_blk(vb, tp, T) + 4 * lp);
     nx.gm = ld4(a.gl + base(cn) * D + 16 * w + 4 * g);
     __syncthreads();
+    // the B operands are read before the chain: the fences below would otherwise hold each
+    // LDS read back until the previous MFMA has issued
+    float4 vb4[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) vb4[u] = sVB[u * WAVE + l];
     f4 hn = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      mma16<MODE>(hn, op.kg[u], sVB[u * WAVE + l]);
+      mma16<MODE>(hn, op.kg[u], vb4[u]);
       GDN2_SCHED_FENCE();
       nx.kg[u] = ld4(a.kgT_f + tbn + frag_blk(w, u, T) + 4 * l);
       GDN2_SCHED_FENCE();
@@ -223,10 +228,13 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
     nx.yy = ld4(a.y_f + chn * D * D + frag_blk(vb, w, D) + 4 * l);
     nx.gm = ld4(a.gl + chn * D + 16 * w + 4 * g);
     __syncthreads();
+    float4 db4[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) db4[u] = sDB[u * WAVE + l];
     f4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      mma16<MODE>(z, op.wpT[u], sDB[u * WAVE + l]);
+      mma16<MODE>(z, op.wpT[u], db4[u]);
       GDN2_SCHED_FENCE();
       nx.wpT[u] = ld4(a.wpT_f + tbn + frag_blk(w, u, T) + 4 * l);
       GDN2_SCHED_FENCE();
