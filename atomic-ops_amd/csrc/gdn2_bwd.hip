@@ -265,21 +265,28 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   __syncthreads();
 
   // The P2 operands' global loads are spread between P1's MFMAs (a burst of loads stalls the
-  // issuing wave while the CU's memory path is busy).
-  float4 xb[NIT], xk[NIT], xw[NIT], xv[NIT], xdw[NIT], xdv[NIT];
+  // issuing wave while the CU's memory path is busy).  b and k arrive as this lane's column
+  // at the rows of the four row tiles (the layout B4 and the gates use, so they stay in
+  // registers to the end); w, v, dWp, dv_new as row-major / fragment items.
+  float4 kv[4], bv[4];
+  float4 xw[NIT], xv[NIT], xdw[NIT], xdv[NIT];
+  constexpr int NRT = T / 16;
   auto prefetch = [&](int item) {
-    const int arr = item / NIT, it = item % NIT, f = tid + it * NT;
-    if (arr == 0) xb[it] = ld4(b + 4 * f);
-    else if (arr == 1) xk[it] = ld4(k + 4 * f);
-    else if (arr == 2) xw[it] = ld4(w + 4 * f);
-    else if (arr == 3) xv[it] = ld4(v + 4 * f);
-    else if (arr == 4) xdw[it] = ld4(dwp + 4 * f);
+    if (item < 2 * NRT) {
+      if (item < NRT) bv[item] = col4(b, item);
+      else kv[item - NRT] = col4(k, item - NRT);
+      return;
+    }
+    const int arr = (item - 2 * NRT) / NIT, it = (item - 2 * NRT) % NIT, f = tid + it * NT;
+    if (arr == 0) xw[it] = ld4(w + 4 * f);
+    else if (arr == 1) xv[it] = ld4(v + 4 * f);
+    else if (arr == 2) xdw[it] = ld4(dwp + 4 * f);
     else xdv[it] = ldg4(a.dv_new_f + tb + 4 * f);
   };
 
   // P1: dAqk = (dO v_new^T) * causal; 16 tiles, two per wave
   static_assert(NW == 8, "P1 assumes two dAqk tiles per wave");
-  constexpr int NITEMS = 6 * NIT, NSLOT = 2 * NKB;
+  constexpr int NITEMS = 2 * NRT + 4 * NIT, NSLOT = 2 * NKB;
 #pragma unroll
   for (int m2 = 0; m2 < 2; ++m2) {
     const int t = wv + NW * m2, ti = t >> 2, tj = t & 3;
@@ -306,12 +313,19 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
 
   // P2: dA = san(dWp kb^T + dv_new (w v)^T), the two products with operands staged in turn:
   //     X1 = kb = b k e^{min(gc,0)}, X2 = dWp; then X1 = w v, X2 = dv_new (kept for dwv)
+  // X1 = kb at this wave's column strip and owned row tiles (every element written once)
 #pragma unroll
-  for (int it = 0; it < NIT; ++it) {
-    const int f = tid + it * NT, i = f / (D / 4), d = 4 * (f % (D / 4));
-    st4(sX1 + i * LD + d, mul4(mul4(xb[it], xk[it]), expnp4(ld4(sG + i * LD + d))));
-    put_fragT(sX2, xdw[it], f);
+  for (int t = 0; t < NRT; ++t) {
+    if (!owned(t)) continue;
+    const float bb[4] = {bv[t].x, bv[t].y, bv[t].z, bv[t].w}, kk[4] = {kv[t].x, kv[t].y, kv[t].z, kv[t].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 16 * t + 4 * g + e;
+      sX1[i * LD + dcol] = (bb[e] * kk[e]) * exp_nonpos(sG[i * LD + dcol]);
+    }
   }
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) put_fragT(sX2, xdw[it], tid + it * NT);
   __syncthreads();
   f4 accA[2];
 #pragma unroll
@@ -347,15 +361,11 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   }
   __syncthreads();
 
-  // q, k, b of this lane's column at the rows of all four row tiles (B4 and the gates),
-  // loaded here so that they arrive during P3 / P4
-  float4 qv[4], kv[4], bv[4];
+  // q of this lane's column at the rows of all four row tiles (B4 and the gates), loaded
+  // here so that it arrives during P3 / P4
+  float4 qv[4];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    qv[t] = col4(q, t);
-    kv[t] = col4(k, t);
-    bv[t] = col4(b, t);
-  }
+  for (int t = 0; t < 4; ++t) qv[t] = col4(q, t);
 
   // P3: tmp = san(dA A^T) into X1 (as T x LT)
   float* sTmp = sX1;
@@ -394,6 +404,18 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     for (int e = 0; e < 4; ++e) sDA[(16 * ti + 4 * g + e) * LT + 16 * tj + r] = ov[e];
   }
   __syncthreads();
+
+  // Global operands of the gate phase: the dWp operand of the dkb chain depends on the k
+  // block only (loaded once); each tile's other operands are loaded one tile ahead, before the
+  // current tile's stores (the memory counter is in order, so a wait on a load issued after
+  // stores would wait for them too).  The first ones are issued here, to arrive during B4.
+  const float* __restrict__ dqgp = a.dqg + tb;
+  const float* __restrict__ dkgp = a.dkg + tb;
+  float4 dwpc[4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) dwpc[kb] = fcol4(dwp, kb);
+  float4 nw4 = col4(w, St::rtile(wv, 0)), nv4 = col4(v, St::rtile(wv, 0));
+  float4 ndq4 = fcol4(dqgp, St::rtile(wv, 0)), ndk4 = fcol4(dkgp, St::rtile(wv, 0));
 
   // B4: VJP of the two-level scores on the owned tiles (b4.py:45-97)
   f4 dq4[NTW], dbk4[NTW], dk4[NTW], dgc4[NTW];
@@ -556,8 +578,6 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   // row tile rt only sees k blocks >= rt), then the gate gradients (mega.py:45-51) and the
   // combine with B4 (mega.py:52-59); dgc -> X1 for B5.  Row T-1 also needs the last-row decay
   // term (mega.py:50), a sum over all rows: its dgc is finished after the loop.
-  const float* __restrict__ dqgp = a.dqg + tb;
-  const float* __restrict__ dkgp = a.dkg + tb;
   float* __restrict__ o_dq = a.dq + tb;
   float* __restrict__ o_dk = a.dk + tb;
   float* __restrict__ o_db = a.db + tb;
@@ -567,14 +587,6 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   const float gl = sG[(T - 1) * LD + dcol];
   const float dlast = owned(3) && g == 3 ? a.dlast[(size_t)chunk * D + dcol] : 0.f;
   float part = 0.f, fix3 = 0.f, fix4 = 0.f;
-  // The dWp operand of the dkb chain depends on the k block only: loaded once.  Each tile's
-  // global operands are loaded one tile ahead, before the current tile's stores (the memory
-  // counter is in order, so a wait on a load issued after stores would wait for them too).
-  float4 dwpc[4];
-#pragma unroll
-  for (int kb = 0; kb < 4; ++kb) dwpc[kb] = fcol4(dwp, kb);
-  float4 nw4 = col4(w, St::rtile(wv, 0)), nv4 = col4(v, St::rtile(wv, 0));
-  float4 ndq4 = fcol4(dqgp, St::rtile(wv, 0)), ndk4 = fcol4(dkgp, St::rtile(wv, 0));
   // The five gradient tiles leave through a per-wave 16x16 LDS transpose (in the dAqk buffer,
   // free once every wave has left B4) as one float4 row store per lane instead of four
   // scalar column stores.  Plain stores: streaming stores complete later, and the next
