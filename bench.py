@@ -109,6 +109,30 @@ def _median_ms(fn, reps=4, rounds=3, warm=2):
     return sorted(per)[len(per) // 2]
 
 
+def seeds_config2(cfg):
+    """Config 2 under the reference's protocol over seeds 0, 1, 2: per seed the median over 3
+    rounds of 4 gradient evaluations (2 warmups), then mean and SD across the seeds."""
+    import torch
+    from atomic_gdn2 import make_blr_trainable
+    from atomic_gdn2.synthetic import make_inputs
+    per = []
+    for seed in (0, 1, 2):
+        (q, k, v, w, b, g), scale = make_inputs(B_, H_, L_, D_, seed=seed)
+        xs = [t.requires_grad_(True) for t in (q, k, v, w, b, g)]
+        fn = make_blr_trainable(cfg, scale)
+
+        def step():
+            o, hf = fn(*xs)
+            return torch.autograd.grad((o, hf), xs, grad_outputs=(2.0 * o, 2.0 * hf))
+
+        per.append(_median_ms(step))
+        del xs, q, k, v, w, b, g
+    mean = sum(per) / len(per)
+    sd = (sum((x - mean) ** 2 for x in per) / (len(per) - 1)) ** 0.5
+    return {"seeds": [0, 1, 2], "ms": [round(x, 4) for x in per], "mean_ms": round(mean, 4), "sd_ms": round(sd, 4),
+            "protocol": "2 warmups, then the median over 3 rounds of the mean of 4 calls, per seed"}
+
+
 def sweep_config3(cfg, seed):
     """BASELINE.json configs[2]: grad-eval latency at B4 D128, H in {2,4,6} x L in {2048,4096}
     (L=4096 runs as two segments of 32 chunks, as in the reference)."""
@@ -304,6 +328,7 @@ def main():
         "reference_tpu_v5e_ms": 2.888,
     }
     if not args.no_sweep:
+        out["config2_seeds"] = seeds_config2(cfg)
         out["config3_sweep"] = sweep_config3(cfg, args.seed)
         out["config4_long_context_fwd"] = bench_config4(cfg, args.seed)
     if not args.no_e2e:
