@@ -1,6 +1,6 @@
 """Benchmark of the GDN-2 operator's gradient evaluation on one MI355X.
 
-Workload: (B,H,L,D) = (4,6,2048,128) fp32, chunk 64, wy_eps = 0,
+Workload (benchmark config 2): (B,H,L,D) = (4,6,2048,128) fp32, chunk 64, wy_eps = 0,
 zero h0, synthetic seeded inputs (atomic_gdn2.synthetic); one step = forward + backward of
 sum(o^2) + sum(h_final^2) w.r.t. q, k, v, w, b, g, all dot modes 'highest' (fp32 MFMA).
 The timed loop runs K steps bracketed by device synchronisation, without profiling events.
@@ -87,8 +87,8 @@ def cpu_baseline(threads: int):
             "ms_scaled_to_workload": sec * 1e3 * 24}
 
 
-# Published grad-eval latencies of the reference on TPU v5e at B4 D128 (the
-# reference runs bt=128 there), by (H, L).
+# Published grad-eval latencies of the reference on TPU v5e at B4 D128 (README.md:23-30 of the
+# reference, column NEW; it runs bt=128 there), by (H, L).
 REF_TPU_MS = {(2, 2048): 1.701, (2, 4096): 2.943, (4, 2048): 2.702, (4, 4096): 10.493, (6, 2048): 2.888,
               (6, 4096): 13.818}
 
@@ -134,7 +134,7 @@ def seeds_config2(cfg):
 
 
 def sweep_config3(cfg, seed):
-    """BASELINE.json configs[2]: grad-eval latency at B4 D128, H in {2,4,6} x L in {2048,4096}
+    """Config 3: grad-eval latency at B4 D128, H in {2,4,6} x L in {2048,4096}
     (L=4096 runs as two segments of 32 chunks, as in the reference)."""
     import torch
     from atomic_gdn2 import make_blr_trainable
@@ -160,7 +160,7 @@ def sweep_config3(cfg, seed):
 
 
 def bench_config4(cfg, seed):
-    """forward-only long context, B8 H16 D128, bf16 inputs, fp32
+    """Config 4: forward-only long context, B8 H16 D128, bf16 inputs, fp32
     state; L = 32768 as 8 calls of 4096 tokens, each call's h0 = the previous h_final.  Inputs
     are drawn on the device (same distributions) per call."""
     import torch
@@ -194,7 +194,7 @@ def bench_config4(cfg, seed):
 
 
 def bench_e2e_lm(seed, reps=4, rounds=3, warm=2):
-    """one training step of the reference's benchmark LM (8 GDN-2
+    """Config 5: one training step of the reference's benchmark LM (8 GDN-2
     blocks, 34,873,952 parameters, B8 L2048, vocab 256, CE + clip_by_global_norm(1.0) + AdamW)
     on uniform synthetic tokens, the optimizer state evolving across the timed steps as in the
     reference's protocol (candidate_e2e.py timed_step)."""
@@ -242,7 +242,7 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every (batch, head) sequence is independent, so a "
-              "multi-GPU run is B/H sharding with no communication (see DESIGN.md); run with --gpus 1",
+              "multi-GPU run is B/H sharding with no communication; run with --gpus 1",
               file=sys.stderr)
         sys.exit(2)
 
