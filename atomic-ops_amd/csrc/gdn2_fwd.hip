@@ -102,9 +102,11 @@ __device__ __forceinline__ void leaf_solve(const float* sSe, float* sI, int tid)
 // sK, into sI (zero on entry): leaf inverses by forward substitution, block doubling with sM as
 // the temp (T x LT), then A = san(A) in place and, if A_out is given, row-major to A_out.
 // Starts with the leaf solves and ends with a barrier.
-template <int LT, int NT, int NW>
+// `during_leaves` runs in every thread before the barrier that ends the leaf solves (one wave
+// solves; the others are otherwise idle there).
+template <int LT, int NT, int NW, class F>
 __device__ __forceinline__ void wy_inverse(const Cfg& cf, const float* sK, float* sI, float* sM, float* A_out,
-                                           int tid, int wv, int r, int g) {
+                                           int tid, int wv, int r, int g, F&& during_leaves) {
   const int smode = cf.solve_mode;
   if (tid < T) {
     switch (cf.mb) {
@@ -124,6 +126,7 @@ __device__ __forceinline__ void wy_inverse(const Cfg& cf, const float* sK, float
       }
     }
   }
+  during_leaves();
   __syncthreads();
 
   // 5b. block doubling X <- [[X11, 0], [-X22 (S21 X11), X22]] (solve.py:30-43), products in the
@@ -205,15 +208,13 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
   // row-fragment items of this thread (item f is lane f%64 of 16x16 block f/64, so fragment
   // stores are contiguous); all raw inputs are loaded up front, before the cumsum's g
   constexpr int NIT = T * D / 4 / NT;
-  float4 xk[NIT], xb[NIT], xw[NIT], xv[NIT], xq[NIT];
+  float4 xk[NIT], xb[NIT], xq[NIT];
 #pragma unroll
   for (int it = 0; it < NIT; ++it) {
     const int f = tid + it * NT, blk = f >> 6, ln = f & 63;
     const int o = (16 * (blk / NKB) + (ln & 15)) * D + 16 * (blk % NKB) + 4 * (ln >> 4);
     xk[it] = in_ld4(k + o);
     xb[it] = in_ld4(b + o);
-    xw[it] = in_ld4(w + o);
-    xv[it] = in_ld4(v + o);
     xq[it] = in_ld4(q + o);
   }
 
@@ -233,7 +234,6 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
     const int i = 16 * (blk / NKB) + (ln & 15), d = 16 * (blk % NKB) + 4 * (ln >> 4);
     const float4 gc = ld4(sG + i * LD + d);
     st4(sBK + i * LD + d, mul4(xb[it], xk[it]));
-    st4(sY + i * LD + d, mul4(xw[it], xv[it]));
     if (a.kg_f || a.kg) {
       const float4 kg = san4(mul4(xk[it], expnp4(sub4(ld4(sG + (T - 1) * LD + d), gc))), clip);
       if (a.kg_f) stg4(a.kg_f + tb + 4 * f, kg);
@@ -301,6 +301,16 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
   }
   __syncthreads();
 
+  // w and v for U (items as in the prologue); they arrive during the masks and the inverse
+  float4 xw[NIT], xv[NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int f = tid + it * NT, blk = f >> 6, ln = f & 63;
+    const int o = (16 * (blk / NKB) + (ln & 15)) * D + 16 * (blk % NKB) + 4 * (ln >> 4);
+    xw[it] = in_ld4(w + o);
+    xv[it] = in_ld4(v + o);
+  }
+
   // 4. masks + sanitize (scores.py:84-87); Se = (1-eps) Akk for the solve (solve.py:25)
   for (int f = tid; f < T * T / 4; f += NT) {
     const int i = f / (T / 4), j = 4 * (f % (T / 4));
@@ -332,7 +342,16 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
     const int i = f / (D / 4), d = 4 * (f % (D / 4));
     st4(sBK + i * LD + d, mul4(ld4(sBK + i * LD + d), expnp4(ld4(sG + i * LD + d))));
   }
-  wy_inverse<LT, NT, NW>(cf, sK, sI, sS, a.A ? a.A + sb : nullptr, tid, wv, r, g);
+  // w v is needed only by U at the end: its loads were issued after the scores, so that they
+  // stream in during the masks and the inverse instead of adding to the load burst at the start
+  wy_inverse<LT, NT, NW>(cf, sK, sI, sS, a.A ? a.A + sb : nullptr, tid, wv, r, g, [&]() {
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const int f = tid + it * NT, blk = f >> 6, ln = f & 63;
+      const int i = 16 * (blk / NKB) + (ln & 15), d = 16 * (blk % NKB) + 4 * (ln >> 4);
+      st4(sY + i * LD + d, mul4(xw[it], xv[it]));
+    }
+  });
 
   // 6. Wp = san(A X), U = san(A (w v)); A is unit lower triangular, so row tile ti only needs
   //    k blocks 0..ti.  Lane l's accumulator is lane l of FA(P^T) block (tj, ti); FA(Wp) goes
