@@ -98,6 +98,49 @@ __device__ __forceinline__ void leaf_solve(const float* sSe, float* sI, int tid)
   for (int i = 0; i < MB; ++i) sI[(base + i) * LT + base + c] = x[i];
 }
 
+// One doubling level (blocks of 2 BB, BB = 16 or 32) on MFMA: wave w takes block m = w / NTL
+// and column strip tj = w % NTL (NTL = BB / 16) and computes the strip of M = S21 X11 (tiles
+// (ti, tj), k over BB) in its accumulators, which are in the B-operand layout of the second
+// product, then the strip of X21 = -X22 M.  Straight-line chains (BB is a compile-time value).
+template <int MODE, int LT, int BB>
+__device__ __forceinline__ void doubling_level_mfma(const float* sK, float* sI, int wv, int r, int g) {
+  constexpr int NM = T / (2 * BB), NTL = BB / 16;
+  if (wv >= NM * NTL) return;
+  const int m = wv / NTL, tj = wv % NTL, i0 = 2 * BB * m;
+  f4 mt[NTL];
+#pragma unroll
+  for (int ti = 0; ti < NTL; ++ti) {
+    mt[ti] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < NTL; ++kb) {
+      const float4 a = ld4(sK + (i0 + BB + 16 * ti + r) * LT + i0 + 16 * kb + 4 * g);
+      const float* bc = sI + (i0 + 16 * kb + 4 * g) * LT + i0 + 16 * tj + r;
+      mma16<MODE>(mt[ti], a, make_float4(bc[0], bc[LT], bc[2 * LT], bc[3 * LT]));
+    }
+  }
+  float4 mb4[NTL];
+#pragma unroll
+  for (int ti = 0; ti < NTL; ++ti) {
+    drain(mt[ti]);
+    mb4[ti] = f4_to_float4(mt[ti]);
+  }
+#pragma unroll
+  for (int ti = 0; ti < NTL; ++ti) {
+    f4 x = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < NTL; ++kb)
+      mma16<MODE>(x, ld4(sI + (i0 + BB + 16 * ti + r) * LT + i0 + BB + 16 * kb + 4 * g), mb4[kb]);
+    drain(x);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sI[(i0 + BB + 16 * ti + 4 * g + e) * LT + i0 + 16 * tj + r] = -x[e];
+  }
+}
+template <int MODE, int LT>
+__device__ __forceinline__ void doubling_level_mfma(const float* sK, float* sI, int bb, int wv, int r, int g) {
+  if (bb == 16) doubling_level_mfma<MODE, LT, 16>(sK, sI, wv, r, g);
+  else doubling_level_mfma<MODE, LT, 32>(sK, sI, wv, r, g);
+}
+
 // The WY inverse A = (I + Se)^-1 (fwd/solve.py:9-59) of Se = (1-eps) Akk, strictly lower in
 // sK, into sI (zero on entry): leaf inverses by forward substitution, block doubling with sM as
 // the temp (T x LT), then A = san(A) in place and, if A_out is given, row-major to A_out.
@@ -130,7 +173,9 @@ __device__ __forceinline__ void wy_inverse(const Cfg& cf, const float* sK, float
   __syncthreads();
 
   // 5b. block doubling X <- [[X11, 0], [-X22 (S21 X11), X22]] (solve.py:30-43), products in the
-  //     solve dot mode: MFMA tiles for blocks of 16 and up, scalar below.
+  //     solve dot mode: scalar below blocks of 16 (two passes), on MFMA from 16 up (one pass:
+  //     each column strip of a block computed by one wave, which keeps M = S21 X11 to itself
+  //     between the two products).
   for (int bb = cf.mb; bb < T; bb *= 2) {
     const int nm = T / (2 * bb);
     if (bb < 16) {
@@ -150,27 +195,14 @@ __device__ __forceinline__ void wy_inverse(const Cfg& cf, const float* sK, float
         sI[(i0 + bb + i) * LT + i0 + j] = -dot_mode_scalar(
             smode, 0, i + 1, [&](int kk) { return brow[kk]; }, [&](int kk) { return mcol[kk * LT]; });
       }
-      __syncthreads();
     } else {
-      const int nt = bb / 16, tpm = nt * nt;
-      for (int t = wv; t < nm * tpm; t += NW) {
-        const int m = t / tpm, ti = (t % tpm) / nt, tj = t % nt, i0 = 2 * bb * m;
-        f4 acc = {0.f, 0.f, 0.f, 0.f};
-        mma_tile_rt(smode, acc, rm(sK, LT).shift(i0 + bb + 16 * ti, i0), rm(sI, LT).shift(i0, i0 + 16 * tj), bb);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sM[(i0 + bb + 16 * ti + 4 * g + e) * LT + i0 + 16 * tj + r] = acc[e];
+      switch (smode) {
+        case DOT_HIGHEST: doubling_level_mfma<DOT_HIGHEST, LT>(sK, sI, bb, wv, r, g); break;
+        case DOT_BF16X3: doubling_level_mfma<DOT_BF16X3, LT>(sK, sI, bb, wv, r, g); break;
+        default: doubling_level_mfma<DOT_DEFAULT, LT>(sK, sI, bb, wv, r, g); break;
       }
-      __syncthreads();
-      for (int t = wv; t < nm * tpm; t += NW) {
-        const int m = t / tpm, ti = (t % tpm) / nt, tj = t % nt, i0 = 2 * bb * m;
-        f4 acc = {0.f, 0.f, 0.f, 0.f};
-        mma_tile_rt(smode, acc, rm(sI, LT).shift(i0 + bb + 16 * ti, i0 + bb),
-                    rm(sM, LT).shift(i0 + bb, i0 + 16 * tj), bb);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sI[(i0 + bb + 16 * ti + 4 * g + e) * LT + i0 + 16 * tj + r] = -acc[e];
-      }
-      __syncthreads();
     }
+    __syncthreads();
   }
   // 5c. A = san(inverse)
   for (int f = tid; f < T * T / 4; f += NT) {
