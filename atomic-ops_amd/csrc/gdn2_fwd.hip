@@ -98,6 +98,31 @@ __device__ __forceinline__ void leaf_solve(const float* sSe, float* sI, int tid)
   for (int i = 0; i < MB; ++i) sI[(base + i) * LT + base + c] = x[i];
 }
 
+// One doubling level with blocks of 2 BB, BB < 16, as scalar dot products in two passes:
+// M = S21 X11 into sM, then X21 = -X22 M.  Every dot runs over the whole block width: X11 is
+// zero above its diagonal and X22 above its diagonal (the solve writes only the lower part of
+// sI, zeroed beforehand), so the added terms are exact zeros and the sums are those of the
+// triangular ranges; with compile-time bounds the operand reads are issued together.
+template <int LT, int NT, int BB>
+__device__ __forceinline__ void doubling_level_scalar(int smode, const float* sK, float* sI, float* sM, int tid) {
+  constexpr int NM = T / (2 * BB), PER = BB * BB;
+  for (int e = tid; e < NM * PER; e += NT) {
+    const int m = e / PER, i = (e % PER) / BB, j = e % BB, i0 = m * 2 * BB;
+    const float* srow = sK + (i0 + BB + i) * LT + i0;
+    const float* tcol = sI + i0 * LT + i0 + j;
+    sM[(i0 + BB + i) * LT + i0 + j] =
+        dot_mode_scalar(smode, 0, BB, [&](int kk) { return srow[kk]; }, [&](int kk) { return tcol[kk * LT]; });
+  }
+  __syncthreads();
+  for (int e = tid; e < NM * PER; e += NT) {
+    const int m = e / PER, i = (e % PER) / BB, j = e % BB, i0 = m * 2 * BB;
+    const float* brow = sI + (i0 + BB + i) * LT + i0 + BB;
+    const float* mcol = sM + (i0 + BB) * LT + i0 + j;
+    sI[(i0 + BB + i) * LT + i0 + j] =
+        -dot_mode_scalar(smode, 0, BB, [&](int kk) { return brow[kk]; }, [&](int kk) { return mcol[kk * LT]; });
+  }
+}
+
 // One doubling level (blocks of 2 BB, BB = 16 or 32) on MFMA: wave w takes block m = w / NTL
 // and column strip tj = w % NTL (NTL = BB / 16) and computes the strip of M = S21 X11 (tiles
 // (ti, tj), k over BB) in its accumulators, which are in the B-operand layout of the second
@@ -179,21 +204,11 @@ __device__ __forceinline__ void wy_inverse(const Cfg& cf, const float* sK, float
   for (int bb = cf.mb; bb < T; bb *= 2) {
     const int nm = T / (2 * bb);
     if (bb < 16) {
-      const int per = bb * bb;
-      for (int e = tid; e < nm * per; e += NT) {
-        const int m = e / per, i = (e % per) / bb, j = e % bb, i0 = m * 2 * bb;
-        const float* srow = sK + (i0 + bb + i) * LT + i0;
-        const float* tcol = sI + i0 * LT + i0 + j;
-        sM[(i0 + bb + i) * LT + i0 + j] = dot_mode_scalar(
-            smode, j, bb, [&](int kk) { return srow[kk]; }, [&](int kk) { return tcol[kk * LT]; });
-      }
-      __syncthreads();
-      for (int e = tid; e < nm * per; e += NT) {
-        const int m = e / per, i = (e % per) / bb, j = e % bb, i0 = m * 2 * bb;
-        const float* brow = sI + (i0 + bb + i) * LT + i0 + bb;
-        const float* mcol = sM + (i0 + bb) * LT + i0 + j;
-        sI[(i0 + bb + i) * LT + i0 + j] = -dot_mode_scalar(
-            smode, 0, i + 1, [&](int kk) { return brow[kk]; }, [&](int kk) { return mcol[kk * LT]; });
+      switch (bb) {
+        case 1: doubling_level_scalar<LT, NT, 1>(smode, sK, sI, sM, tid); break;
+        case 2: doubling_level_scalar<LT, NT, 2>(smode, sK, sI, sM, tid); break;
+        case 4: doubling_level_scalar<LT, NT, 4>(smode, sK, sI, sM, tid); break;
+        default: doubling_level_scalar<LT, NT, 8>(smode, sK, sI, sM, tid); break;
       }
     } else {
       switch (smode) {
