@@ -407,17 +407,8 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
     float* sW = sS + wv * (16 * 20);
     constexpr int NTJ = D / 16, NTM = (T / 16) * NTJ;
     const bool want_w = a.wp_f || a.wpT_f || a.wp, want_u = a.uT_f || a.u;
-    for (int t = wv; t < 2 * NTM; t += NW) {
-      const int mat = t / NTM, ti = (t % NTM) / NTJ, tj = t % NTJ;
-      if (mat ? !want_u : !want_w) continue;
-      const float* X = mat ? sY : sBK;
-      f4 acc = {0.f, 0.f, 0.f, 0.f};
-      for (int kb = 0; kb <= ti; ++kb) {
-        const float4 av = ld4(sI + (16 * ti + r) * LT + 16 * kb + 4 * g);
-        const float* xb = X + (16 * kb + 4 * g) * LD + 16 * tj + r;
-        mma16<DOT>(acc, av, make_float4(xb[0], xb[LD], xb[2 * LD], xb[3 * LD]));
-      }
-      drain(acc);
+    // the epilogue of tile (mat, ti, tj): sanitize, then the requested layouts
+    auto store_tile = [&](int mat, int ti, int tj, const f4& acc) __attribute__((always_inline)) {
       const float4 p = san4(f4_to_float4(acc), clip);     // p.e = P[16 ti + 4 g + e][16 tj + r]
       float* rowmaj = mat ? a.u : a.wp;
       if (rowmaj) {
@@ -438,6 +429,47 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+    };
+    if constexpr (NTJ == NW) {
+      // wave w owns column strip tj = w of both products: the strip's B operands (k blocks
+      // 0..3) are read once, and the four row tiles' chains (lengths 1..4) are interleaved
+      // k-block-major; each tile still accumulates its k blocks in ascending order
+      const int tj = wv;
+#pragma unroll
+      for (int mat = 0; mat < 2; ++mat) {
+        if (mat ? !want_u : !want_w) continue;
+        const float* X = mat ? sY : sBK;
+        float4 xb[4];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          const float* xc = X + (16 * kb + 4 * g) * LD + 16 * tj + r;
+          xb[kb] = make_float4(xc[0], xc[LD], xc[2 * LD], xc[3 * LD]);
+        }
+        f4 acc[4];
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti) acc[ti] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int ti = kb; ti < 4; ++ti) mma16<DOT>(acc[ti], ld4(sI + (16 * ti + r) * LT + 16 * kb + 4 * g), xb[kb]);
+        drain(acc[0], acc[1], acc[2], acc[3]);
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti) store_tile(mat, ti, tj, acc[ti]);
+      }
+    } else {
+      for (int t = wv; t < 2 * NTM; t += NW) {
+        const int mat = t / NTM, ti = (t % NTM) / NTJ, tj = t % NTJ;
+        if (mat ? !want_u : !want_w) continue;
+        const float* X = mat ? sY : sBK;
+        f4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int kb = 0; kb <= ti; ++kb) {
+          const float4 av = ld4(sI + (16 * ti + r) * LT + 16 * kb + 4 * g);
+          const float* xb = X + (16 * kb + 4 * g) * LD + 16 * tj + r;
+          mma16<DOT>(acc, av, make_float4(xb[0], xb[LD], xb[2 * LD], xb[3 * LD]));
+        }
+        drain(acc);
+        store_tile(mat, ti, tj, acc);
       }
     }
   }
