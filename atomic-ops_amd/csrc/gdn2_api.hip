@@ -169,14 +169,13 @@ int gdn2_residual_layout(const gdn2_desc* d, size_t offsets[GDN2_RES_COUNT], siz
 }
 
 // forward workspace (fragment layouts): [Wp | U^T | Kg^T], and without a residual also
-// [Qg | Aqk | gl | h_pre | v_new] (with a residual those live in it).
+// [Qg | Aqk | gl] (with a residual those live in it).
 size_t gdn2_fwd_workspace_bytes(const gdn2_desc* d, int with_residual) {
   if (validate(d)) return 0;
   const Dims x = dims(d);
   size_t n = 3 * align_up(x.n_chunks * x.tD * 4);
   if (!with_residual)
-    n += align_up(x.n_chunks * x.tD * 4) + align_up(x.n_chunks * x.tT * 4) + align_up(x.n_chunks * x.D * 4) +
-         align_up(x.n_chunks * x.DD * 4) + align_up(x.n_chunks * x.tD * 4);
+    n += align_up(x.n_chunks * x.tD * 4) + align_up(x.n_chunks * x.tT * 4) + align_up(x.n_chunks * x.D * 4);
   return n;
 }
 
@@ -209,9 +208,9 @@ int fwd_impl(const gdn2_desc* d, const void* q, const void* k, const void* v, co
   float* wp = take(x.n_chunks * x.tD * 4);
   float* uT = take(x.n_chunks * x.tD * 4);
   float* kgT = take(x.n_chunks * x.tD * 4);
-  // residuals for the backward -- training only; otherwise Qg / Aqk / gl / h_pre / v_new live in
-  // the workspace
-  float *A = nullptr, *wpT = nullptr, *kg = nullptr, *qg, *aqk, *gl, *hpre, *vnew;
+  // residuals for the backward -- training only; otherwise Qg / Aqk / gl live in the workspace
+  // and h_pre / v_new are not stored at all (the scan consumes them itself)
+  float *A = nullptr, *wpT = nullptr, *kg = nullptr, *qg, *aqk, *gl, *hpre = nullptr, *vnew = nullptr;
   if (residual) {
     size_t off[GDN2_RES_COUNT], tot;
     residual_offsets(d, off, &tot);
@@ -227,8 +226,6 @@ int fwd_impl(const gdn2_desc* d, const void* q, const void* k, const void* v, co
     qg = take(x.n_chunks * x.tD * 4);
     aqk = take(x.n_chunks * x.tT * 4);
     gl = take(x.n_chunks * x.D * 4);
-    hpre = take(x.n_chunks * x.DD * 4);
-    vnew = take(x.n_chunks * x.tD * 4);
   }
 
   gdn2::WyFwdArgs wa{};
@@ -240,13 +237,18 @@ int fwd_impl(const gdn2_desc* d, const void* q, const void* k, const void* v, co
   hipError_t e = timed(0, s, [&] { return gdn2::launch_wy_fwd(d->D, wa, s, bf16); });
   if (e != hipSuccess) return hip_fail(e, "wy_fwd launch");
 
-  gdn2::ScanFwdArgs sa{wp, kgT, uT, gl, h0, h_final, hpre, vnew, (int)x.nc, (int)x.n_bh, cfg};
+  // Training keeps h_pre and v_new for the backward: the scan carries only the state and the
+  // output follows chunk-parallel.  Without a residual the scan computes the output itself and
+  // h_pre / v_new never leave it.
+  gdn2::ScanFwdArgs sa{wp, kgT, uT, gl, h0, qg, aqk, h_final, residual ? nullptr : o, hpre, vnew,
+                       (int)x.nc, (int)x.n_bh, cfg};
   e = timed(1, s, [&] { return gdn2::launch_scan_fwd(d->D, sa, s); });
   if (e != hipSuccess) return hip_fail(e, "scan_fwd launch");
-
-  gdn2::OutFwdArgs oa{qg, aqk, hpre, vnew, o, (int)x.n_chunks, cfg};
-  e = timed(5, s, [&] { return gdn2::launch_out_fwd(d->D, oa, s); });
-  if (e != hipSuccess) return hip_fail(e, "out_fwd launch");
+  if (residual) {
+    gdn2::OutFwdArgs oa{qg, aqk, hpre, vnew, o, (int)x.n_chunks, cfg};
+    e = timed(5, s, [&] { return gdn2::launch_out_fwd(d->D, oa, s); });
+    if (e != hipSuccess) return hip_fail(e, "out_fwd launch");
+  }
   return GDN2_OK;
 }
 }  // namespace

@@ -34,7 +34,7 @@ namespace gdn2 {
 // (w, ti) of FA(out^T): one float4 store.
 // ------------------------------------------------------------------------------------
 template <int D, int B3>
-__global__ __launch_bounds__(D / 16 * WAVE) void bwd_state_kernel(BwdStateArgs a) {
+__global__ __launch_bounds__(D / 16 * WAVE) __attribute__((amdgpu_waves_per_eu(D == 128 ? 4 : 1))) void bwd_state_kernel(BwdStateArgs a) {
   constexpr int NKB = D / 16, NW = D / 16, NT = NW * WAVE, SLAB = 12 * WAVE;   // float4 per slab
   constexpr int NST = (SLAB + NT - 1) / NT;                                      // staged per thread
   __shared__ float4 sA[2 * SLAB];                   // [buf][mat * 4 + ti][lane]
@@ -46,24 +46,26 @@ __global__ __launch_bounds__(D / 16 * WAVE) void bwd_state_kernel(BwdStateArgs a
   float* tr = sTr + kt * 16 * TRP;
 
   // staging item f of a slab: mat = f / 256 (0: s dO, 1: -dv_new, 2: v_new), ti = f / 64 % 4,
-  // lane f % 64 of the operand block (ti, kb)
-  float4 st[NST];
-  auto fetch = [&](int kb) {
+  // lane f % 64 of the operand block (ti, kb).  Slabs and B operands are fetched two value
+  // blocks ahead (register sets by kb parity; the kb loop is unrolled by two so that every
+  // index is static): one block's 48 MFMAs per wave are too short to cover a load.
+  float4 st[2][NST];
+  auto fetch = [&](int kb, float4 (&dst)[NST]) {
 #pragma unroll
     for (int j = 0; j < NST; ++j) {
       const int f = tid + j * NT;
       if (f < SLAB) {
         const int mat = f >> 8, ti = (f >> 6) & 3, ln = f & 63;
         if (mat == 0)
-          st[j] = ld4(a.dout + tb + (16 * ti + (ln & 15)) * D + 16 * kb + 4 * (ln >> 4));
+          dst[j] = ld4(a.dout + tb + (16 * ti + (ln & 15)) * D + 16 * kb + 4 * (ln >> 4));
         else if (mat == 1)
-          st[j] = ld4(a.dv_new_f + tb + frag_blk(ti, kb, D) + 4 * ln);
+          dst[j] = ld4(a.dv_new_f + tb + frag_blk(ti, kb, D) + 4 * ln);
         else
-          st[j] = ld4(a.v_new_f + tb + frag_blk(kb, ti, T) + 4 * ln);
+          dst[j] = ld4(a.v_new_f + tb + frag_blk(kb, ti, T) + 4 * ln);
       }
     }
   };
-  auto put = [&](int buf) {
+  auto put = [&](int buf, const float4 (&src)[NST]) {
 #pragma unroll
     for (int j = 0; j < NST; ++j) {
       const int f = tid + j * NT;
@@ -71,18 +73,18 @@ __global__ __launch_bounds__(D / 16 * WAVE) void bwd_state_kernel(BwdStateArgs a
         const int mat = f >> 8, ti = (f >> 6) & 3, ln = f & 63;
         float4* dst = sA + buf * SLAB + (mat * 4 + ti) * WAVE;
         if (mat == 0) {
-          dst[ln] = scale4(st[j], sc);
+          dst[ln] = scale4(src[j], sc);
         } else if (mat == 1) {
-          dst[ln] = scale4(st[j], -1.f);
+          dst[ln] = scale4(src[j], -1.f);
         } else {
           // lane ln = (rr, gg) holds v_new[16 ti + 4 gg + e][16 kb + rr]: operand lane
           // (4 gg + e) + 16 (rr / 4), component rr % 4
           float* df = reinterpret_cast<float*>(dst);
           const int rr = ln & 15, gg = ln >> 4, base = 4 * (4 * gg + 16 * (rr >> 2)) + (rr & 3);
-          df[base] = st[j].x;
-          df[base + 4] = st[j].y;
-          df[base + 8] = st[j].z;
-          df[base + 12] = st[j].w;
+          df[base] = src[j].x;
+          df[base + 4] = src[j].y;
+          df[base + 8] = src[j].z;
+          df[base + 12] = src[j].w;
         }
       }
     }
@@ -94,21 +96,27 @@ __global__ __launch_bounds__(D / 16 * WAVE) void bwd_state_kernel(BwdStateArgs a
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) acc[m][ti] = f4{0.f, 0.f, 0.f, 0.f};
   float part = 0.f;
-  fetch(0);
-  put(0);
-  float4 hpT = ld4(a.h_pre_f + hb + frag_blk(0, kt, D) + 4 * l);
-  float4 dh = ld4(a.dh_next_f + hb + frag_blk(kt, 0, D) + 4 * l);
+  float4 hpT[2], dh[2];
+  fetch(0, st[0]);
+  hpT[0] = ld4(a.h_pre_f + hb + frag_blk(0, kt, D) + 4 * l);
+  dh[0] = ld4(a.dh_next_f + hb + frag_blk(kt, 0, D) + 4 * l);
+  fetch(1, st[1]);
+  hpT[1] = ld4(a.h_pre_f + hb + frag_blk(1, kt, D) + 4 * l);
+  dh[1] = ld4(a.dh_next_f + hb + frag_blk(kt, 1, D) + 4 * l);
+  put(0, st[0]);
   __syncthreads();
-#pragma unroll 1
+#pragma unroll 2
   for (int kb = 0; kb < NKB; ++kb) {
-    const int nk = kb + 1 < NKB ? kb + 1 : kb;       // last step re-fetches (unused)
-    fetch(nk);
+    const int pb = kb & 1;
     // h_pre block (kt, kb) from FA(h_pre^T) block (kb, kt), its MFMA result layout
-    const float4 hp = wave_transpose16(tr, hpT, r, g);
-    const float4 dhc = dh;
-    hpT = ld4(a.h_pre_f + hb + frag_blk(nk, kt, D) + 4 * l);
-    dh = ld4(a.dh_next_f + hb + frag_blk(kt, nk, D) + 4 * l);
-    const float4* cur = sA + (kb & 1) * SLAB;
+    const float4 hp = wave_transpose16(tr, hpT[pb], r, g);
+    const float4 dhc = dh[pb];
+    if (kb + 2 < NKB) {
+      fetch(kb + 2, st[pb]);
+      hpT[pb] = ld4(a.h_pre_f + hb + frag_blk(kb + 2, kt, D) + 4 * l);
+      dh[pb] = ld4(a.dh_next_f + hb + frag_blk(kt, kb + 2, D) + 4 * l);
+    }
+    const float4* cur = sA + pb * SLAB;
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) {
       mma16<B3>(acc[0][ti], cur[ti * WAVE + l], hp);
@@ -120,7 +128,7 @@ __global__ __launch_bounds__(D / 16 * WAVE) void bwd_state_kernel(BwdStateArgs a
     part = fmaf(dhc.y, hp.y, part);
     part = fmaf(dhc.z, hp.z, part);
     part = fmaf(dhc.w, hp.w, part);
-    if (kb + 1 < NKB) put((kb + 1) & 1);
+    if (kb + 1 < NKB) put(pb ^ 1, st[pb ^ 1]);
     __syncthreads();
   }
   drain(acc[0][0], acc[0][1], acc[0][2], acc[0][3]);

@@ -8,9 +8,10 @@
 //                   of 16 and up), then Wp = A (b k e^gc) and U = A (w v) on MFMA.
 //                   Semantics: fwd/scores.py:42-87, fwd/solve.py:9-48, fwd/cd_slim.py:14-21.
 //                   The raw inputs are fp32 or bfloat16 (template TIn), widened to fp32 on load.
-//   out_fwd_kernel  one workgroup per chunk after the state scan:
+//   out_fwd_kernel  one workgroup per chunk after the state scan, when the backward needs
+//                   h_pre and v_new anyway (training):
 //                   o = san(s Qg h_pre + Aqk v_new)                   (fwd/cd_slim.py:24-27)
-//   (the forward state scan is in gdn2_scan.hip)
+//   (the forward state scan is in gdn2_scan.hip; without a residual it computes o itself)
 //
 // Every tile the scans read is written in fragment layout (gdn2_common.hpp), so the scans
 // load each operand block with one coalesced float4 access per lane.
@@ -579,6 +580,8 @@ hipError_t launch_wy_fwd(int D, const WyFwdArgs& a, hipStream_t s, bool bf16_inp
   });
   return hipGetLastError();
 }
+
+
 
 hipError_t launch_out_fwd(int D, const OutFwdArgs& a, hipStream_t s) {
   dispatch_mode(a.cfg.dot_mode, [&](auto m) {

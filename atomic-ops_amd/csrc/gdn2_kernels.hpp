@@ -40,12 +40,13 @@ struct WyFwdArgs {
   Cfg cfg;
 };
 
-// Forward state scan: reads FA(Wp), FA(Kg^T), FA(U^T), gl; writes per chunk the entering state
-// h_pre as FA(h_pre^T) (D x D) and v_new as FA(v_new^T) (D x T), and the final state hf
-// (row-major D x D).
+// Forward state scan: reads FA(Wp), FA(Kg^T), FA(U^T), gl; writes the final state hf
+// (row-major D x D) and, when h_pre_f / v_new_f are set, per chunk the entering state h_pre as
+// FA(h_pre^T) (D x D) and v_new as FA(v_new^T) (D x T).  With o set it also reads FA(Qg),
+// FA(Aqk) and writes o (row-major T x D per chunk); otherwise out_fwd computes o.
 struct ScanFwdArgs {
-  const float *wp_f, *kgT_f, *uT_f, *gl, *h0;
-  float *hf, *h_pre_f, *v_new_f;
+  const float *wp_f, *kgT_f, *uT_f, *gl, *h0, *qg_f, *aqk_f;
+  float *hf, *o, *h_pre_f, *v_new_f;    // o, h_pre_f, v_new_f may be null
   int nc, n_bh;
   Cfg cfg;
 };

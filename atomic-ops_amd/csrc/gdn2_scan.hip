@@ -19,12 +19,13 @@
 // the sets never need copying, and all prefetch loads are unconditional so the compiler's
 // vmcnt waits stay exact.  Per chunk: two workgroup barriers.
 //
-// Each scan carries only its chain (h -> v_new -> h, dh -> dv_new -> dh).  The forward output
-// o, which needs h_pre and v_new but feeds nothing back, is computed chunk-parallel
-// afterwards (gdn2_fwd.hip); the reverse scan's dO terms are computed chunk-parallel before it
+// The chain is h -> v_new -> h (dh -> dv_new -> dh).  The forward output o, which needs
+// h_pre and v_new but feeds nothing back, is computed inside the forward scan by waves of
+// its own (below); the reverse scan's dO terms are computed chunk-parallel before it
 // (gdn2_bwd.hip).
 //
-// Forward (fwd/cd_slim.py:12-30):  v_new = U - Wp h;  h = san(e^gamma h + Kg^T v_new)
+// Forward (fwd/cd_slim.py:12-30):  v_new = U - Wp h;  h = san(e^gamma h + Kg^T v_new);
+//                                  o = san(s Qg h + Aqk v_new)
 // Reverse (bwd/mega.py:33-36):     dv_new = san(X + Kg dh);  dh = san(Y + e^gamma dh - Wp^T dv_new)
 //                                  with X = Aqk^T dO, Y = Qg^T (s dO)
 #include "gdn2_kernels.hpp"
@@ -38,11 +39,30 @@ __device__ __forceinline__ int xcd_remap(int nblk) {
   return (nblk % 8) ? b : (b % 8) * (nblk / 8) + b / 8;
 }
 
+// Forward scan with the output fused in.  Eight waves per workgroup (slice of 16 value
+// columns of one (batch, head)); per chunk two barriers:
+//   window A (after the state h_pre is in LDS):
+//     V waves 0-3   v_new tile i = U - Wp[tile i, :] h_pre  (full key contraction, no
+//                   cross-wave reduction), written to LDS (and, for the backward, global)
+//     O waves 4-7   read h_pre from LDS for their output tile
+//   window B (after v_new is in LDS):
+//     every wave w < D/16   h rows of key tile w: h = san(e^gamma h + Kg^T v_new), to LDS
+//     O wave j      o tile j = san(s Qg[tile j, :] h_pre + Aqk[tile j, :] v_new)
+//                   (fwd/cd_slim.py:24-27), at the default priority while the state work
+//                   runs at a raised one, so it takes the MFMA pipe when that work leaves it
+//                   idle.
+// h_pre in LDS is block kb = key tile in the MFMA result layout of the owning wave, which is
+// the B operand of Wp h and the A operand of h^T Qg^T; v_new tiles are in the B-operand
+// layout of Kg^T v_new, which is the A operand of v_new^T Aqk^T.  FA(Wp), FA(Qg), FA(Aqk),
+// FA(Kg^T), FA(U^T) blocks are loaded as stored (one float4 per lane), one chunk ahead into
+// the second of two register sets, interleaved with the MFMAs.
+template <int NH>
 struct FwdOps {
-  float4 wp[4];    // FA(Wp) block (ti, w):    Wp[16ti + r][16w + 4g .. +3]
-  float4 kg[4];    // FA(Kg^T) block (w, u):   Kg^T[16w + r][16u + 4g .. +3]
-  float4 uu;       // FA(U^T) block (slice, tp), lane lp (the v_new reduction pair)
-  float4 gm;       // gamma[16w + 4g .. +3]
+  float4 x[NH];    // V: FA(Wp) block (i, kb); O: FA(Qg) block (j, kb)
+  float4 aq[4];    // O: FA(Aqk) block (j, u), u <= j
+  float4 uu;       // V: FA(U^T) block (slice, i)
+  float4 kg[4];    // state rows: FA(Kg^T) block (w, u)
+  float4 gm;       // state rows: gamma[16w + 4g .. +3]
 };
 
 // Prefetch loads for the next chunk are issued in small groups between the MFMA groups of the
@@ -51,98 +71,154 @@ struct FwdOps {
 // stall overlaps the MFMAs already in flight.
 #define GDN2_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
 
-template <int D, int MODE>
-__global__ __launch_bounds__(D / 16 * WAVE) void scan_fwd_kernel(ScanFwdArgs a) {
-  constexpr int NW = D / 16, NVB = D / 16;
-  __shared__ float4 sPv[NW * 4 * WAVE];    // partial (Wp h) tiles, [wave][ti][lane]
-  __shared__ float4 sVB[4 * WAVE];         // v_new tiles in B-operand layout, [u][lane]
-  const float clip = a.cfg.clip;
+// ROLE < 0: V wave (v_new tile w); ROLE = j >= 0: O wave of output tile j (wave 4 + j).
+// OUT = false: no output (the O waves keep only their state rows and the barriers; the
+// output is then computed chunk-parallel from h_pre and v_new, gdn2_fwd.hip).
+template <int D, int MODE, bool OUT, int ROLE>
+__device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, float4* sV) {
+  constexpr int NH = D / 16, NVB = D / 16;
+  constexpr bool V = ROLE < 0, O = !V && OUT;
+  constexpr int J = V ? 0 : ROLE;
+  const float clip = a.cfg.clip, scale = a.cfg.scale;
   const int nc = a.nc;
   const int lin = xcd_remap(gridDim.x);
   const int vb = lin % NVB, bh = lin / NVB, c0 = 16 * vb;
-  const int tid = threadIdx.x, l = lane_id(), r = l & 15, g = l >> 4, w = wave_id();
-  // the reduction pair of this thread (threads < 256): output tile tp, lane lp
-  const int tp = (tid & 255) >> 6, lp = tid & 63;
-  const bool red = tid < 4 * WAVE;
-
-  f4 h;
-#pragma unroll
-  for (int e = 0; e < 4; ++e)
-    h[e] = a.h0 ? a.h0[(size_t)bh * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r] : 0.f;
-
+  const int l = lane_id(), r = l & 15, g = l >> 4, w = wave_id();
+  const int ti = w & 3;                        // v_new tile of a V wave
+  constexpr bool OWNS = V || NH == 8;           // keeps key tile w of the state (w < NH)
   auto base = [&](int c) { return (size_t)bh * nc + (c < nc ? c : nc - 1); };   // clamped chunk
-  auto load_all = [&](FwdOps& op, int c) {
-    const size_t tb = base(c) * T * D;
+
+  f4 h = {0.f, 0.f, 0.f, 0.f};
+  if (OWNS) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      op.wp[i] = ld4(a.wp_f + tb + frag_blk(i, w, D) + 4 * l);
-      op.kg[i] = ld4(a.kgT_f + tb + frag_blk(w, i, T) + 4 * l);
+    for (int e = 0; e < 4; ++e)
+      h[e] = a.h0 ? a.h0[(size_t)bh * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r] : 0.f;
+    sH[w * WAVE + l] = f4_to_float4(h);
+  }
+
+  auto load_all = [&](FwdOps<NH>& op, int c) {
+    const size_t tb = base(c) * T * D, sb = base(c) * T * T;
+    if constexpr (V) {
+#pragma unroll
+      for (int kb = 0; kb < NH; ++kb) op.x[kb] = ld4(a.wp_f + tb + frag_blk(ti, kb, D) + 4 * l);
+      op.uu = ld4(a.uT_f + tb + frag_blk(vb, ti, T) + 4 * l);
     }
-    op.uu = ld4(a.uT_f + tb + frag_blk(vb, tp, T) + 4 * lp);
-    op.gm = ld4(a.gl + base(c) * D + 16 * w + 4 * g);
+    if constexpr (O) {
+#pragma unroll
+      for (int kb = 0; kb < NH; ++kb) op.x[kb] = ld4(a.qg_f + tb + frag_blk(J, kb, D) + 4 * l);
+#pragma unroll
+      for (int u = 0; u <= J; ++u) op.aq[u] = ld4(a.aqk_f + sb + frag_blk(J, u, T) + 4 * l);
+    }
+    if constexpr (OWNS) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) op.kg[u] = ld4(a.kgT_f + tb + frag_blk(w, u, T) + 4 * l);
+      op.gm = ld4(a.gl + base(c) * D + 16 * w + 4 * g);
+    }
   };
 
-  // one chunk step on `op`; prefetches chunk cn into `nx`
-  auto step = [&](const FwdOps& op, int c, FwdOps& nx, int cn) {
+  auto step = [&](const FwdOps<NH>& op, int c, FwdOps<NH>& nx, int cn) {
     const size_t ch = (size_t)bh * nc + c, tb = ch * T * D;
-    const size_t tbn = base(cn) * T * D;
-    stg4(a.h_pre_f + ch * D * D + frag_blk(vb, w, D) + 4 * l, f4_to_float4(h));
-    // partial Wp h over this wave's 16 key rows
-    const float4 hb = f4_to_float4(h);
-    f4 pv[4];
+    const size_t tbn = base(cn) * T * D, sbn = base(cn) * T * T;
+    if (OWNS && a.h_pre_f) stg4(a.h_pre_f + ch * D * D + frag_blk(vb, w, D) + 4 * l, f4_to_float4(h));
+    // ---- window A ----
+    float4 hb[NH];
+    if constexpr (V || O) {
 #pragma unroll
-    for (int ti = 0; ti < 4; ++ti) {
-      pv[ti] = f4{0.f, 0.f, 0.f, 0.f};
-      mma16<MODE>(pv[ti], op.wp[ti], hb);
-      GDN2_SCHED_FENCE();
-      nx.wp[ti] = ld4(a.wp_f + tbn + frag_blk(ti, w, D) + 4 * l);
-      GDN2_SCHED_FENCE();
+      for (int kb = 0; kb < NH; ++kb) hb[kb] = sH[kb * WAVE + l];
     }
-    drain(pv[0], pv[1], pv[2], pv[3]);
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (V) {
+      __builtin_amdgcn_s_setprio(2);
 #pragma unroll
-    for (int ti = 0; ti < 4; ++ti) sPv[(w * 4 + ti) * WAVE + l] = f4_to_float4(pv[ti]);
+      for (int kb = 0; kb < NH; ++kb) {
+        mma16<MODE>(acc, op.x[kb], hb[kb]);
+        GDN2_SCHED_FENCE();
+        nx.x[kb] = ld4(a.wp_f + tbn + frag_blk(ti, kb, D) + 4 * l);
+        GDN2_SCHED_FENCE();
+      }
+      drain(acc);
+      const float4 vn = sub4(op.uu, f4_to_float4(acc));
+      sV[ti * WAVE + l] = vn;
+      if (a.v_new_f) stg4(a.v_new_f + tb + frag_blk(vb, ti, T) + 4 * l, vn);
+      nx.uu = ld4(a.uT_f + tbn + frag_blk(vb, ti, T) + 4 * l);
+    }
     __syncthreads();
-    // fixed-order reduction over waves: v_new = U - sum
-    if (red) {
-      float4 s = sPv[tid];
+    // ---- window B ----
+    float4 vv[4];
 #pragma unroll
-      for (int w2 = 1; w2 < NW; ++w2) s = add4(s, sPv[w2 * 4 * WAVE + tid]);
-      const float4 vn = sub4(op.uu, s);
-      sVB[tid] = vn;
-      stg4(a.v_new_f + tb + frag_blk(vb, tp, T) + 4 * lp, vn);
+    for (int u = 0; u < 4; ++u) vv[u] = sV[u * WAVE + l];
+    if constexpr (OWNS) {
+      __builtin_amdgcn_s_setprio(2);
+      f4 hn = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        mma16<MODE>(hn, op.kg[u], vv[u]);
+        GDN2_SCHED_FENCE();
+        nx.kg[u] = ld4(a.kgT_f + tbn + frag_blk(w, u, T) + 4 * l);
+        GDN2_SCHED_FENCE();
+      }
+      drain(hn);
+      const float gmv[4] = {op.gm.x, op.gm.y, op.gm.z, op.gm.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) h[e] = sanitize(h[e] * exp_nonpos(gmv[e]) + hn[e], clip);
+      nx.gm = ld4(a.gl + base(cn) * D + 16 * w + 4 * g);
     }
-    nx.uu = ld4(a.uT_f + tbn + frag_blk(vb, tp, T) + 4 * lp);
-    nx.gm = ld4(a.gl + base(cn) * D + 16 * w + 4 * g);
+    if constexpr (O) {
+      __builtin_amdgcn_s_setprio(0);
+#pragma unroll
+      for (int kb = 0; kb < NH; ++kb) {
+        mma16<MODE>(acc, hb[kb], op.x[kb]);
+        GDN2_SCHED_FENCE();
+        nx.x[kb] = ld4(a.qg_f + tbn + frag_blk(J, kb, D) + 4 * l);
+        GDN2_SCHED_FENCE();
+      }
+      f4 acc2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u <= J; ++u) {
+        mma16<MODE>(acc2, vv[u], op.aq[u]);
+        GDN2_SCHED_FENCE();
+        nx.aq[u] = ld4(a.aqk_f + sbn + frag_blk(J, u, T) + 4 * l);
+        GDN2_SCHED_FENCE();
+      }
+      drain(acc, acc2);
+      // lane (r, g): o[16 J + r][c0 + 4 g .. + 3]
+      stg4(a.o + tb + (size_t)(16 * J + r) * D + c0 + 4 * g,
+           make_float4(sanitize(scale * acc[0] + acc2[0], clip), sanitize(scale * acc[1] + acc2[1], clip),
+                       sanitize(scale * acc[2] + acc2[2], clip), sanitize(scale * acc[3] + acc2[3], clip)));
+    }
+    // every wave has read h_pre (window A) before the first barrier, so the new state may
+    // overwrite it here
+    if (OWNS) sH[w * WAVE + l] = f4_to_float4(h);
     __syncthreads();
-    // the B operands are read before the chain: the fences below would otherwise hold each
-    // LDS read back until the previous MFMA has issued
-    float4 vb4[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) vb4[u] = sVB[u * WAVE + l];
-    f4 hn = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      mma16<MODE>(hn, op.kg[u], vb4[u]);
-      GDN2_SCHED_FENCE();
-      nx.kg[u] = ld4(a.kgT_f + tbn + frag_blk(w, u, T) + 4 * l);
-      GDN2_SCHED_FENCE();
-    }
-    drain(hn);
-    const float gmv[4] = {op.gm.x, op.gm.y, op.gm.z, op.gm.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) h[e] = sanitize(h[e] * exp_nonpos(gmv[e]) + hn[e], clip);
   };
 
-  FwdOps A, B;
+  FwdOps<NH> A, B;
   load_all(A, 0);
+  __syncthreads();
   int c = 0;
   for (; c + 1 < nc; c += 2) {
     step(A, c, B, c + 1);
     step(B, c + 1, A, c + 2);
   }
   if (c < nc) step(A, c, B, c + 1);
+  if (OWNS) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) a.hf[(size_t)bh * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r] = h[e];
+    for (int e = 0; e < 4; ++e) a.hf[(size_t)bh * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r] = h[e];
+  }
+}
+
+template <int D, int MODE, bool OUT>
+__global__ __launch_bounds__(8 * WAVE) void scan_fwd_kernel(ScanFwdArgs a) {
+  constexpr int NH = D / 16;
+  __shared__ float4 sH[NH * WAVE];     // h_pre of the current chunk, [key tile][lane]
+  __shared__ float4 sV[4 * WAVE];      // v_new tiles, [token tile][lane]
+  switch (wave_id()) {
+    case 4: scan_fwd_role<D, MODE, OUT, 0>(a, sH, sV); break;
+    case 5: scan_fwd_role<D, MODE, OUT, 1>(a, sH, sV); break;
+    case 6: scan_fwd_role<D, MODE, OUT, 2>(a, sH, sV); break;
+    case 7: scan_fwd_role<D, MODE, OUT, 3>(a, sH, sV); break;
+    default: scan_fwd_role<D, MODE, OUT, -1>(a, sH, sV); break;
+  }
 }
 
 // Lane lt of block u of a FA(X^T) tile set in LDS (xs[u][lane], X of T x 16 columns) ->
@@ -266,8 +342,13 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
 hipError_t launch_scan_fwd(int D, const ScanFwdArgs& a, hipStream_t s) {
   dispatch_mode(a.cfg.dot_mode, [&](auto m) {
     constexpr int M = decltype(m)::value;
-    if (D == 128) hipLaunchKernelGGL((scan_fwd_kernel<128, M>), dim3(a.n_bh * 8), dim3(512), 0, s, a);
-    else hipLaunchKernelGGL((scan_fwd_kernel<64, M>), dim3(a.n_bh * 4), dim3(256), 0, s, a);
+    if (a.o) {
+      if (D == 128) hipLaunchKernelGGL((scan_fwd_kernel<128, M, true>), dim3(a.n_bh * 8), dim3(512), 0, s, a);
+      else hipLaunchKernelGGL((scan_fwd_kernel<64, M, true>), dim3(a.n_bh * 4), dim3(512), 0, s, a);
+    } else {
+      if (D == 128) hipLaunchKernelGGL((scan_fwd_kernel<128, M, false>), dim3(a.n_bh * 8), dim3(512), 0, s, a);
+      else hipLaunchKernelGGL((scan_fwd_kernel<64, M, false>), dim3(a.n_bh * 4), dim3(512), 0, s, a);
+    }
     return 0;
   });
   return hipGetLastError();

@@ -117,7 +117,8 @@ int gdn2_debug_gemm(int mode, const float* A, const float* B, float* C, int M, i
  * gdn2_prof_begin(n) starts recording for up to n launches (process-wide, not re-entrant);
  * gdn2_prof_end synchronises on the recorded events and returns, per kernel id, the summed
  * duration in milliseconds and the launch count, then stops recording.
- * Kernel ids: 0 wy_fwd, 1 scan_fwd, 2 scan_bwd, 3 bwd_state, 4 bwd_wy, 5 out_fwd, 6 bwd_pre. */
+ * Kernel ids: 0 wy_fwd, 1 scan_fwd (without a residual also the output), 2 scan_bwd,
+ * 3 bwd_state, 4 bwd_wy, 5 out_fwd (training only), 6 bwd_pre. */
 #define GDN2_NUM_KERNELS 7
 int gdn2_prof_begin(int max_launches);
 int gdn2_prof_end(double ms_sum[GDN2_NUM_KERNELS], int counts[GDN2_NUM_KERNELS]);

@@ -82,9 +82,9 @@ def test_residual_layout_and_workspaces():
         assert nxt - o >= s
     L = _lib.lib()
     d = _desc()
-    # [Wp | U^T | Kg^T], without a residual also [Qg | Aqk | gl | h_pre | v_new]
+    # [Wp | U^T | Kg^T], without a residual also [Qg | Aqk | gl] (h_pre / v_new never leave the scan)
     assert L.gdn2_fwd_workspace_bytes(ctypes.byref(d), 1) == N * 3 * 64 * 128 * 4
-    assert L.gdn2_fwd_workspace_bytes(ctypes.byref(d), 0) == N * (5 * 64 * 128 + 64 * 64 + 128 + 128 * 128) * 4
+    assert L.gdn2_fwd_workspace_bytes(ctypes.byref(d), 0) == N * (4 * 64 * 128 + 64 * 64 + 128) * 4
     assert L.gdn2_bwd_workspace_bytes(ctypes.byref(d)) >= N * (4 * 64 * 128 + 128 * 128 + 128) * 4
 
 
