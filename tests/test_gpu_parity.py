@@ -403,6 +403,28 @@ def test_forward_only_equals_training_forward_bitwise():
 
 
 @pytest.mark.parametrize("D", [64, 128])
+def test_forward_only_odd_chunks_with_h0(D):
+    """Without a residual the state scan computes o itself (output waves beside the chain);
+    with one it leaves o to the chunk-parallel output kernel.  An odd chunk count (L=192, the
+    scan's tail step) and a nonzero h0: both paths equal bit for bit, and within 2e-3 of the
+    float64 oracle."""
+    from atomic_gdn2 import make_blr_trainable
+    from oracle import gdn2_oracle as O
+    banner(f"forward-only odd chunks D={D}")
+    cfg = base_cfg()
+    scale = D ** -0.5
+    arrs = mk_inputs(2, 192, 2, D, 8, layout="bhld")
+    h0 = torch.randn(2, 2, D, D, device="cuda", generator=torch.Generator("cuda").manual_seed(9)) * 0.1
+    xs = [t.requires_grad_(True) for t in to_dev(arrs)]
+    o1, h1 = make_blr_trainable(cfg, scale)(*xs, h0)
+    o2, h2 = _fwd(cfg, scale, [t.detach() for t in xs], h0)
+    assert torch.equal(o1.detach(), o2) and torch.equal(h1.detach(), h2)
+    t = [torch.from_numpy(a).double() for a in arrs]
+    ro, rh = O.forward_ref(*t, scale, h0.double().cpu(), O.OracleCfg.from_cfg(cfg))
+    assert rel_l2(o2, ro) < GATE and rel_l2(h2, rh) < GATE
+
+
+@pytest.mark.parametrize("D", [64, 128])
 def test_bf16_inputs_forward(D):
     """bf16 inputs are widened on load: bit-equal to the fp32 path on the same (bf16-rounded)
     values, and within 2e-3 of the float64 oracle on those values."""
