@@ -298,18 +298,22 @@ def main():
     tflops = (ff + fb) / (ms * 1e-3) / 1e12
     kf = kernel_flops_per_token()
     ntok = B_ * H_ * L_
+    # HBM bytes per launch measured by rocprof counters (FETCH_SIZE / WRITE_SIZE, scaled by a
+    # copy kernel) at this workload; with this launch's own time they give each kernel's
+    # achieved HBM bandwidth (the bound the sequential scans are reported against).
+    tf = ROOT / "profiles" / "traffic.json"
+    tmeas = json.loads(tf.read_text()) if tf.exists() else {}
     kern = {}
     for name, (tot_ms, cnt) in prof.items():
         if cnt:
             avg = tot_ms / cnt
             kern[name] = {"avg_ms": round(avg, 5), "launches": cnt,
                           "tflops": round(kf[name] * ntok / (avg * 1e-3) / 1e12, 2)}
+            if isinstance(tmeas.get(name), int):
+                kern[name]["hbm_gb_per_s"] = round(tmeas[name] / (avg * 1e-3) / 1e9, 1)
     dom = max(kern, key=lambda n: kern[n]["avg_ms"])
     ach = kern[dom]["tflops"]
-    traffic = None
-    tf = ROOT / "profiles" / "traffic.json"
-    if tf.exists():
-        traffic = json.loads(tf.read_text()).get(dom)
+    traffic = tmeas.get(dom)
 
     out = {
         "metric": "fwd+bwd ms, TFLOP/s and MFMA % at B4 H6 L2048 D128 fp32; fwd tokens/s",
