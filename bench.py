@@ -248,11 +248,14 @@ def main():
 
     import torch
     from atomic_gdn2 import make_cfg, make_blr_trainable, _lib
-    from atomic_gdn2.synthetic import make_inputs
+    from atomic_gdn2.synthetic import make_inputs_np, inputs_sha256
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    (q, k, v, w, b, g), scale = make_inputs(B_, H_, L_, D_, seed=args.seed, device=dev)
+    arrs, scale = make_inputs_np(B_, H_, L_, D_, seed=args.seed)
+    sha = inputs_sha256(arrs)                      # recorded as the reference harness does
+    q, k, v, w, b, g = (torch.from_numpy(x).to(dev) for x in arrs)
+    del arrs
     xs = [t.requires_grad_(True) for t in (q, k, v, w, b, g)]
     cfg = make_cfg(bt=64, bc=32, score_bs=64, bs2=32, mb=8, wy_eps=0.0, dot_mode="highest",
                    solve_dot_mode="highest", b3_dot_mode="highest")
@@ -321,7 +324,8 @@ def main():
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
         "config": {"workload": "gdn2 grad-eval (fwd+bwd of sum(o^2)+sum(h_final^2)) B4 H6 L2048 D128 "
-                               "chunk64 wy_eps0 dot=highest", "B": B_, "H": H_, "L": L_, "D": D_, "bt": 64},
+                               "chunk64 wy_eps0 dot=highest", "B": B_, "H": H_, "L": L_, "D": D_, "bt": 64,
+                   "seed": args.seed, "inputs_sha256": sha},
         "fwd_ms": round(fwd_ms, 4), "fwd_tokens_per_s": round(B_ * L_ / (fwd_ms * 1e-3), 1),
         "canonical_gflop": round((ff + fb) / 1e9, 3),
         "canonical_gb_per_s": round(canonical_bytes(B_, H_, L_, D_) / (ms * 1e-3) / 1e9, 1),
