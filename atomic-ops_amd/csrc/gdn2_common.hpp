@@ -306,23 +306,6 @@ __device__ __forceinline__ int frag_off(int i, int j, int C) {
   return frag_blk(i >> 4, j >> 4, C) + (((i & 15) + ((j & 15) >> 2) * 16) << 2) + (j & 3);
 }
 
-// dst[m - m0][n] (row stride LD) = M[m][n] for m in [m0, m0 + nm), n in [0, NR), read from
-// src = M^T (NR x NC) in fragment layout.  nm and m0 are multiples of 16.
-template <int LD>
-__device__ __forceinline__ void load_fragT(float* dst, const float* __restrict__ src, int NR, int NC,
-                                           int m0, int nm, int tid, int nt) {
-  const int nbm = nm >> 4, nbc = NC >> 4, total = (NR >> 4) * nbm * 64;
-  for (int f = tid; f < total; f += nt) {
-    const int lane = f & 63, blk = f >> 6, bn = blk / nbm, bm = (m0 >> 4) + blk % nbm;
-    const float4 x = ld4(src + ((bn * nbc + bm) << 8) + 4 * lane);
-    const int n = 16 * bn + (lane & 15), m = 16 * bm + 4 * (lane >> 4) - m0;
-    dst[(m + 0) * LD + n] = x.x;
-    dst[(m + 1) * LD + n] = x.y;
-    dst[(m + 2) * LD + n] = x.z;
-    dst[(m + 3) * LD + n] = x.w;
-  }
-}
-
 // 16x16 tile held in the MFMA result layout (lane l = r + 16 g: column r, rows 4 g .. 4 g + 3)
 // -> the same tile in the A-operand layout (lane l: row r, columns 4 g .. 4 g + 3), through a
 // per-wave LDS tile with row stride TRP (conflict-free column reads).  Only the issuing wave
