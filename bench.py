@@ -81,10 +81,17 @@ def cpu_baseline(threads: int):
             break
     sec = sorted(times)[len(times) // 2]
     f, b = canonical_flops(1, 1, 2048, 128)
+    model = None
+    try:
+        with open("/proc/cpuinfo") as fh:
+            model = next((ln.split(":", 1)[1].strip() for ln in fh if ln.startswith("model name")), None)
+    except OSError:
+        pass
     return {"value": (f + b) / sec / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"B1 H1 L2048 D128 fp32 grad-eval (1/24 of the workload), median of {len(times)}: "
                       f"{sec * 1e3:.1f} ms", "ms_per_sample": sec * 1e3,
-            "ms_scaled_to_workload": sec * 1e3 * 24}
+            "ms_scaled_to_workload": sec * 1e3 * 24,
+            "host": {"cpu_model": model, "os_cpu_count": os.cpu_count()}}
 
 
 # Published grad-eval latencies of the reference on TPU v5e at B4 D128 (README.md:23-30 of the
