@@ -39,7 +39,8 @@ __device__ __forceinline__ int xcd_remap(int nblk) {
   return (nblk % 8) ? b : (b % 8) * (nblk / 8) + b / 8;
 }
 
-// Forward scan with the output fused in.  Eight waves per workgroup (slice of 16 value
+// Forward scan, with the output fused in when no residual is kept (OUT; in training the
+// output waves only carry their state rows).  Eight waves per workgroup (slice of 16 value
 // columns of one (batch, head)); per chunk two barriers:
 //   window A (after the state h_pre is in LDS):
 //     V waves 0-3   v_new tile i = U - Wp[tile i, :] h_pre  (full key contraction, no
