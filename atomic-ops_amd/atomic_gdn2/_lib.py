@@ -25,6 +25,7 @@ RES_STORAGE = {"aqk": ("T", "T", True, False), "A": ("T", "T", False, False),
                "wpT": ("D", "T", True, True), "kg": ("T", "D", True, False),
                "qg": ("T", "D", True, False), "gl": (None, "D", False, False)}
 KERNEL_NAMES = ("wy_fwd", "scan_fwd", "scan_bwd", "bwd_state", "bwd_wy", "out_fwd", "bwd_pre")
+ABI_VERSION = 2
 STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported configuration", 3: "HIP error"}
 
 _c_int, _c_dbl, _c_size, _vp = ctypes.c_int32, ctypes.c_double, ctypes.c_size_t, ctypes.c_void_p
@@ -35,7 +36,7 @@ class Gdn2Desc(ctypes.Structure):
     _fields_ = [("B", _c_int), ("H", _c_int), ("L", _c_int), ("D", _c_int),
                 ("bt", _c_int), ("score_bs", _c_int), ("bs2", _c_int), ("mb", _c_int),
                 ("diag", _c_int), ("dot_mode", _c_int), ("solve_dot_mode", _c_int),
-                ("b3_dot_mode", _c_int),
+                ("b3_dot_mode", _c_int), ("seq_ld", _c_int), ("state_ckpt", _c_int),
                 ("scale", _c_dbl), ("wy_eps", _c_dbl), ("clip", _c_dbl), ("diff_clip", _c_dbl)]
 
 
@@ -71,7 +72,7 @@ def lib():
         for fn in ("gdn2_residual_layout", "gdn2_fwd", "gdn2_fwd_bf16", "gdn2_bwd", "gdn2_wy_stage",
                    "gdn2_debug_gemm", "gdn2_prof_begin", "gdn2_prof_end"):
             getattr(L, fn).restype = _c_int
-        if L.gdn2_abi_version() != 1:
+        if L.gdn2_abi_version() != ABI_VERSION:
             raise Gdn2Error("libgdn2_hip.so ABI version mismatch")
         _LIB = L
     return _LIB
@@ -84,11 +85,13 @@ def check(status: int, what: str):
         raise err(f"{what}: {STATUS.get(status, status)}: {msg}")
 
 
-def make_desc(cfg, B, H, L, D, scale) -> Gdn2Desc:
+def make_desc(cfg, B, H, L, D, scale, seq_ld=0, state_ckpt=0) -> Gdn2Desc:
+    """Descriptor of one segment of L tokens; seq_ld = the full sequence length of the raw
+    tensors the segment lies in (0 = L)."""
     return Gdn2Desc(B, H, L, D, cfg.bt, cfg.score_bs, cfg.bs2, cfg.mb,
                     DIAG_IDS[cfg.diag], DOT_IDS[cfg.dot_mode], DOT_IDS[cfg.solve_dot_mode],
-                    DOT_IDS[cfg.b3_dot_mode], float(scale), float(cfg.wy_eps), float(cfg.clip),
-                    float(cfg.diff_clip))
+                    DOT_IDS[cfg.b3_dot_mode], int(seq_ld), int(state_ckpt), float(scale),
+                    float(cfg.wy_eps), float(cfg.clip), float(cfg.diff_clip))
 
 
 def residual_layout(desc: Gdn2Desc):
@@ -112,8 +115,9 @@ def decode_residual(name, flat, B, H, nc, T, D):
     return t.transpose(-1, -2) if transposed else t
 
 
-def ptr(t):
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+def ptr(t, offset=0):
+    """Device address of t (plus ``offset`` elements), or None."""
+    return None if t is None else ctypes.c_void_p(t.data_ptr() + offset * t.element_size())
 
 
 def stream_handle(device=None):

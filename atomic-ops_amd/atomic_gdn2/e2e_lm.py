@@ -51,12 +51,15 @@ class LMConfig:
 
 
 def operator_cfg(**kw):
-    """Operator configuration of the LM: the reference's production E2E profile (wy_eps 1e-3,
-    BTL diagonal) at this build's chunk of 64 tokens, with every product in fp32 ('highest').
-    The production profile's bf16x3 solve / backward products exist to avoid the cost of
-    full-precision products on the TPU; on MI355X fp32 MFMA is the native and faster path,
-    and it is at least as accurate."""
-    base = dict(bt=64, bc=32, score_bs=64, bs2=32, mb=8, diag="btl", wy_eps=1e-3, dot_mode="highest",
+    """Operator configuration of the LM: the profile of the reference's published speed runs,
+    'no_damping' (all_paths_speed_worker.py / isolated E2E: ``c.paths(profile='no_damping')``,
+    candidate_common.py ``paths``: bt 128, bs2 64, BTL diagonal, wy_eps = 0).  With wy_eps = 0 the
+    chunked WY form equals the token recurrence for every chunk size, so this build's chunk of
+    64 computes the same operator; only the rounding differs.  Every product is fp32
+    ('highest'): the profile's bf16x3 solve / backward products exist to avoid the cost of
+    full-precision products on the TPU; on MI355X fp32 MFMA is the native path, and it is at
+    least as accurate."""
+    base = dict(bt=64, bc=32, score_bs=64, bs2=32, mb=8, diag="btl", wy_eps=0.0, dot_mode="highest",
                 solve_dot_mode="highest", b3_dot_mode="highest")
     base.update(kw)
     return make_cfg(**base)

@@ -6,10 +6,12 @@ Drop-in for the reference's ``atomic_gdn2/pipeline.py:17-66``:
 * ``o`` (B,H,L,D) and ``h_final`` (B,H,D,D) are float32 whatever the input dtype;
 * sequences longer than ``cfg.max_chunks_per_call`` chunks are split into segments with the
   state carried through ``h0``/``h_final`` (pipeline.py:57-64);
-* each segment is one custom autograd node (the analogue of the reference's
-  ``jax.custom_vjp``): the forward runs the HIP forward (``gdn2_fwd``) and keeps its residual
-  buffer, the backward runs ``gdn2_bwd`` and returns gradients through ``_fin``
-  (pipeline.py:11-14): sanitized at 1e4 and cast back to each input's dtype.
+* the call is one custom autograd node (the analogue of the reference's per-segment
+  ``jax.custom_vjp``): its forward runs the HIP forward (``gdn2_fwd``) segment by segment and
+  keeps each segment's residual buffer, its backward runs ``gdn2_bwd`` over the segments in
+  reverse and returns each segment's gradients through ``_fin`` (pipeline.py:11-14): sanitized
+  at 1e4 and cast back to each input's dtype.  Segments are views into the full tensors
+  (``gdn2_desc.seq_ld``): no slice copies, gradient scatters or concatenation.
 
 Every call goes to the HIP kernels in ``libgdn2_hip.so``; there is no other backend.  Tensors
 must live on a ROCm device.
@@ -24,6 +26,8 @@ from . import _lib
 from .precision import sanitize
 
 _FINAL_CLIP = 1e4
+# chunk sizes (cfg.bt) the HIP kernels run
+SUPPORTED_BT = (64,)
 
 
 def _fin(x, dt, cfg):
@@ -56,59 +60,82 @@ def _check_device(q):
                            f"device (got {q.device})")
 
 
+def _segments(L, cfg):
+    """Token ranges of the reference's segment loop: at most max_chunks_per_call chunks each
+    (pipeline.py:57-64)."""
+    step = cfg.max_chunks_per_call * cfg.bt
+    return [(t0, min(L, t0 + step)) for t0 in range(0, L, step)]
+
+
 def make_blr_trainable(cfg, scale):
     scale = float(scale)
 
-    class _Segment(torch.autograd.Function):
+    class _Sequence(torch.autograd.Function):
+        """The whole call as one autograd node.  Forward and backward run the reference's
+        segment loop (pipeline.py:57-64) over views of the full tensors: each segment's kernels
+        read its inputs and write its o and gradients in place (gdn2_desc.seq_ld), the state
+        is carried through h0 / h_final forward and through dh0 / dh_final backward, and each
+        segment's gradients pass through ``_fin`` as the reference's per-segment custom_vjp
+        returns them (so the dh handed to the previous segment is _fin(dh0, float32))."""
+
         @staticmethod
         def forward(ctx, q, k, v, w, b, g, h0):
             # h0 None = zero initial state (the kernel takes a null pointer; no zero fill)
             dts = tuple(t.dtype for t in (q, k, v, w, b, g)) + ((h0.dtype,) if h0 is not None else (torch.float32,))
             xs = [_f32(t) for t in (q, k, v, w, b, g)]
-            h0c = None if h0 is None else _f32(h0)
+            h = None if h0 is None else _f32(h0)
             B, H, L, D = xs[0].shape
-            desc = _lib.make_desc(cfg, B, H, L, D, scale)
             dev = xs[0].device
             need_res = any(ctx.needs_input_grad)
             o = torch.empty((B, H, L, D), dtype=torch.float32, device=dev)
-            hf = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
             L_ = _lib.lib()
+            segs, res_list = [], []
             with torch.cuda.device(dev):
-                _, tot = _lib.residual_layout(desc)      # validates the descriptor
-                res = torch.empty(tot, dtype=torch.uint8, device=dev) if need_res else None
-                wsb = L_.gdn2_fwd_workspace_bytes(ctypes.byref(desc), int(need_res))
-                ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
-                _lib.check(L_.gdn2_fwd(ctypes.byref(desc), *map(_lib.ptr, xs), _lib.ptr(h0c),
-                                       _lib.ptr(o), _lib.ptr(hf), _lib.ptr(res), _lib.ptr(ws),
-                                       _lib.stream_handle(dev)), "gdn2_fwd")
+                stream = _lib.stream_handle(dev)
+                for t0, t1 in _segments(L, cfg):
+                    desc = _lib.make_desc(cfg, B, H, t1 - t0, D, scale, seq_ld=L)
+                    _, tot = _lib.residual_layout(desc)      # validates the descriptor
+                    res = torch.empty(tot, dtype=torch.uint8, device=dev) if need_res else None
+                    ws = torch.empty(L_.gdn2_fwd_workspace_bytes(ctypes.byref(desc), int(need_res)),
+                                     dtype=torch.uint8, device=dev)
+                    hf = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
+                    off = t0 * D
+                    _lib.check(L_.gdn2_fwd(ctypes.byref(desc), *(_lib.ptr(x, off) for x in xs), _lib.ptr(h),
+                                           _lib.ptr(o, off), _lib.ptr(hf), _lib.ptr(res), _lib.ptr(ws), stream),
+                               "gdn2_fwd")
+                    segs.append((t0, desc))
+                    res_list.append(res)
+                    h = hf
             if need_res:
-                ctx.save_for_backward(*xs, res)
-                ctx.desc = desc
+                ctx.save_for_backward(*xs, *res_list)
+                ctx.segs = segs
                 ctx.dts = dts
-            return o, hf
+            return o, h
 
         @staticmethod
         def backward(ctx, do, dhf):
-            *xs, res = ctx.saved_tensors
+            saved = ctx.saved_tensors
+            xs, res_list = saved[:6], saved[6:]
             q = xs[0]
             B, H, L, D = q.shape
             dev = q.device
             do = torch.zeros_like(q) if do is None else _f32(do)
-            dhf = q.new_zeros((B, H, D, D)) if dhf is None else _f32(dhf)
+            dh = q.new_zeros((B, H, D, D)) if dhf is None else _f32(dhf)
             grads = [torch.empty_like(q) for _ in range(6)]
-            dh0 = q.new_empty((B, H, D, D))
             L_ = _lib.lib()
             with torch.cuda.device(dev):
-                ws = torch.empty(L_.gdn2_bwd_workspace_bytes(ctypes.byref(ctx.desc)), dtype=torch.uint8,
-                                 device=dev)
-                dq, dk, dv, dw, db, dg = grads
-                _lib.check(L_.gdn2_bwd(ctypes.byref(ctx.desc), *map(_lib.ptr, xs), _lib.ptr(res),
-                                       _lib.ptr(do), _lib.ptr(dhf), _lib.ptr(dq), _lib.ptr(dk),
-                                       _lib.ptr(dv), _lib.ptr(dw), _lib.ptr(db), _lib.ptr(dg),
-                                       _lib.ptr(dh0), _lib.ptr(ws), _lib.stream_handle(dev)), "gdn2_bwd")
-            outs = (dq, dk, dv, dw, db, dg, dh0)
-            grads = tuple(_fin(x, dt, cfg) for x, dt in zip(outs, ctx.dts))
-            return grads if ctx.needs_input_grad[6] else grads[:6] + (None,)
+                stream = _lib.stream_handle(dev)
+                for (t0, desc), res in reversed(list(zip(ctx.segs, res_list))):
+                    ws = torch.empty(L_.gdn2_bwd_workspace_bytes(ctypes.byref(desc)), dtype=torch.uint8, device=dev)
+                    dh0 = q.new_empty((B, H, D, D))
+                    off = t0 * D
+                    _lib.check(L_.gdn2_bwd(ctypes.byref(desc), *(_lib.ptr(x, off) for x in xs), _lib.ptr(res),
+                                           _lib.ptr(do, off), _lib.ptr(dh), *(_lib.ptr(x, off) for x in grads),
+                                           _lib.ptr(dh0), _lib.ptr(ws), stream), "gdn2_bwd")
+                    # cotangent of the previous segment's h_final (float32), or of the caller's h0
+                    dh = dh0 if t0 == 0 else _fin(dh0, torch.float32, cfg)
+            out = tuple(_fin(x, dt, cfg) for x, dt in zip(grads, ctx.dts[:6]))
+            return out + ((_fin(dh, ctx.dts[6], cfg),) if ctx.needs_input_grad[6] else (None,))
 
     def forward_only(xs, h0):
         """No gradient needed: one kernel sequence over all L (no residual kept).  Equal bit for
@@ -140,7 +167,6 @@ def make_blr_trainable(cfg, scale):
         bsz, H, L, D = q.shape
         if L % cfg.bt:
             raise ValueError(f"L={L} must be divisible by bt={cfg.bt}")
-        nc = L // cfg.bt
         h = h0
         if h is not None and h.shape != (bsz, H, D, D):
             raise ValueError(f"h0.shape={tuple(h.shape)} must be {(bsz, H, D, D)}")
@@ -148,13 +174,6 @@ def make_blr_trainable(cfg, scale):
         xs = (q, k, v, w, b, g)
         if not (torch.is_grad_enabled() and any(t.requires_grad for t in xs + ((h,) if h is not None else ()))):
             return forward_only(xs, h)
-        outs = []
-        for s in range(0, nc, cfg.max_chunks_per_call):
-            e = min(nc, s + cfg.max_chunks_per_call)
-            a, c = s * cfg.bt, e * cfg.bt
-            seg = (q, k, v, w, b, g) if (a == 0 and c == L) else tuple(t[:, :, a:c] for t in (q, k, v, w, b, g))
-            o_seg, h = _Segment.apply(*seg, h)
-            outs.append(o_seg)
-        return (outs[0] if len(outs) == 1 else torch.cat(outs, dim=2)), h
+        return _Sequence.apply(q, k, v, w, b, g, h)
 
     return call

@@ -2,16 +2,25 @@
 ``gdn2_fwd.py:340-361``, ``gdn2_pipeline.py:145-152``) over the GDN-2 operator.
 
 Inputs are (batch, seq_len, heads, d_head) with d_head = 128; ``config`` is a legacy
-``KernelConfig`` whose chunk size ``bt`` the legacy validation still requires to divide seq_len.
-The operator itself always runs at this build's chunk of 64 tokens (the chunked WY form is exact
-for any chunk size; only rounding differs), with the legacy ``clip``, ``wy_eps`` and leaf size
-``mb`` and fp32 products everywhere (the legacy kernels use Precision.HIGHEST).  Returns
+``KernelConfig`` (chunk ``bt``, leaf ``mb``, ``clip``, ``wy_eps``).  Returns
 (o (batch, seq_len, heads, d_head) float32, h_final (batch, heads, d_head, d_head) float32).
+
+Which operator runs.  The reference dispatches on the device (fallback.py:9-22): its Pallas
+path runs chunk ``config.bt`` with ``config.wy_eps``; everywhere else it runs
+``gdn2_chunked_wy_reference(..., chunk_size=config.bt)`` with that function's default
+``wy_eps = 0`` (reference.py:109).  The (1 - wy_eps) damping acts on the coupling inside a
+chunk only, so with wy_eps > 0 the chunk size is part of the operator; with wy_eps = 0 the
+chunked WY form equals the token recurrence for every chunk size and only the rounding
+depends on it.  This shim therefore runs chunk ``config.bt`` with ``config.wy_eps`` when the
+HIP kernels support that chunk size, and otherwise (the bt = 128 / 256 presets) the
+reference's off-TPU operator: wy_eps = 0, at the kernels' chunk of 64.  Products are fp32
+everywhere (the legacy kernels use Precision.HIGHEST).
 """
 from __future__ import annotations
 
 
 from atomic_gdn2 import make_cfg, make_blr_trainable
+from atomic_gdn2.pipeline import SUPPORTED_BT
 
 from .configs import DEFAULT_CONFIG, KernelConfig, validate_inputs
 
@@ -22,12 +31,17 @@ def _operator(config: KernelConfig, scale: float):
     key = (config, float(scale))
     fn = _OPS.get(key)
     if fn is None:
-        mb = min(config.mb, 64)
-        cfg = make_cfg(bt=64, bc=32, score_bs=64, bs2=32, mb=mb, diag="btl", clip=config.clip,
-                       wy_eps=config.wy_eps, dot_mode="highest", solve_dot_mode="highest",
-                       b3_dot_mode="highest")
-        fn = _OPS[key] = make_blr_trainable(cfg, scale)
+        fn = _OPS[key] = make_blr_trainable(operator_cfg(config), scale)
     return fn
+
+
+def operator_cfg(config: KernelConfig):
+    """The operator configuration that stands in for ``config`` (see the module docstring)."""
+    bt = config.bt if config.bt in SUPPORTED_BT else 64
+    eps = config.wy_eps if bt == config.bt else 0.0
+    return make_cfg(bt=bt, bc=bt // 2, score_bs=bt, bs2=32, mb=min(config.mb, bt), diag="btl",
+                    clip=config.clip, wy_eps=eps, dot_mode="highest", solve_dot_mode="highest",
+                    b3_dot_mode="highest")
 
 
 def _run(q, k, v, w, b, g, scale, h0, config):

@@ -38,6 +38,8 @@ int validate(const gdn2_desc* d) {
   if (d->bt != gdn2::T) return fail(GDN2_ERR_UNSUPPORTED, "this build supports bt == 64 only");
   if (d->D != 64 && d->D != 128) return fail(GDN2_ERR_UNSUPPORTED, "this build supports D in {64, 128}");
   if (d->bs2 < 16) return fail(GDN2_ERR_UNSUPPORTED, "this build supports bs2 >= 16");
+  if (d->seq_ld != 0 && d->seq_ld < d->L) return fail(GDN2_ERR_INVALID, "seq_ld must be 0 or >= L");
+  if (d->state_ckpt != 0) return fail(GDN2_ERR_UNSUPPORTED, "this build supports state_ckpt == 0 only");
   return GDN2_OK;
 }
 
@@ -76,6 +78,8 @@ gdn2::Cfg make_cfg(const gdn2_desc* d) {
   c.solve_mode = d->solve_dot_mode;
   c.b3_mode = d->b3_dot_mode;
   c.mb = d->mb;
+  c.nc = d->L / d->bt;
+  c.seq_ld = d->seq_ld ? d->seq_ld : d->L;
   make_pieces(d->bt, d->score_bs, d->bs2, &c.pieces);
   return c;
 }
@@ -266,6 +270,7 @@ int gdn2_fwd_bf16(const gdn2_desc* d, const uint16_t* q, const uint16_t* k, cons
                   float* h_final, void* residual, void* workspace, void* stream) {
   return fwd_impl(d, q, k, v, w, b, g, true, h0, o, h_final, residual, workspace, stream);
 }
+
 
 int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v, const float* w,
              const float* b, const float* g, const void* residual, const float* d_o, const float* d_hf,

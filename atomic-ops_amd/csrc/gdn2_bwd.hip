@@ -41,7 +41,7 @@ __global__ __launch_bounds__(D / 16 * WAVE) __attribute__((amdgpu_waves_per_eu(D
   __shared__ __attribute__((aligned(16))) float sTr[NW * 16 * TRP];
   const Cfg& cf = a.cfg;
   const int chunk = blockIdx.x, tid = threadIdx.x, kt = wave_id(), l = lane_id(), r = l & 15, g = l >> 4;
-  const size_t tb = (size_t)chunk * T * D, hb = (size_t)chunk * D * D;
+  const size_t tb = (size_t)chunk * T * D, hb = (size_t)chunk * D * D, tio = io_off<D>(cf, chunk);
   const float sc = cf.scale;
   float* tr = sTr + kt * 16 * TRP;
 
@@ -57,7 +57,7 @@ __global__ __launch_bounds__(D / 16 * WAVE) __attribute__((amdgpu_waves_per_eu(D
       if (f < SLAB) {
         const int mat = f >> 8, ti = (f >> 6) & 3, ln = f & 63;
         if (mat == 0)
-          dst[j] = ld4(a.dout + tb + (16 * ti + (ln & 15)) * D + 16 * kb + 4 * (ln >> 4));
+          dst[j] = ld4(a.dout + tio + (16 * ti + (ln & 15)) * D + 16 * kb + 4 * (ln >> 4));
         else if (mat == 1)
           dst[j] = ld4(a.dv_new_f + tb + frag_blk(ti, kb, D) + 4 * ln);
         else
@@ -211,13 +211,13 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   const Cfg& cf = a.cfg;
   const float clip = cf.clip, scale = cf.scale;
   const int chunk = blockIdx.x, tid = threadIdx.x, wv = wave_id(), l = lane_id(), r = l & 15, g = l >> 4;
-  const size_t tb = (size_t)chunk * T * D, sb = (size_t)chunk * T * T;
-  const float* __restrict__ q = a.q + tb;
-  const float* __restrict__ k = a.k + tb;
-  const float* __restrict__ b = a.b + tb;
-  const float* __restrict__ w = a.w + tb;
-  const float* __restrict__ v = a.v + tb;
-  const float* __restrict__ dout = a.dout + tb;
+  const size_t tb = (size_t)chunk * T * D, sb = (size_t)chunk * T * T, tio = io_off<D>(cf, chunk);
+  const float* __restrict__ q = a.q + tio;
+  const float* __restrict__ k = a.k + tio;
+  const float* __restrict__ b = a.b + tio;
+  const float* __restrict__ w = a.w + tio;
+  const float* __restrict__ v = a.v + tio;
+  const float* __restrict__ dout = a.dout + tio;
   const float* __restrict__ dwp = a.dwp + tb;
   const int strip = St::strip(wv), dcol = 16 * strip + r;
   auto owned = [&](int t) { return t >= St::rtile(wv, 0) && (t - St::rtile(wv, 0)) % St::STEP == 0; };
@@ -257,7 +257,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     }
 #pragma unroll
     for (int it = 0; it < NIA; ++it) xa[it] = ldg4(a.A + sb + 4 * (tid + it * NT));
-    chunk_cumsum<D, LD, NT, true>(a.g + tb, sG);
+    chunk_cumsum<D, LD, NT, true>(a.g + tio, sG);
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
       const int f = tid + it * NT;
@@ -556,7 +556,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
             float sq = 0.f, sbk = 0.f;
             for (int jl = 0; jl < pc.P; ++jl) {
               const int j = pc.col0 + jl;
-              const float E = expf(fminf(fmaxf(gx - sG[j * LD + dcol], -dc), dc));
+              const float E = expf(clip_nan(gx - sG[j * LD + dcol], -dc, dc));
               const float ek = E * k[j * D + dcol];
               sq += sDAq[x * LT + j] * ek;
               sbk += sDA[x * LT + j] * ek;
@@ -570,7 +570,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
             float s2 = 0.f;
             for (int il = 0; il < pc.P; ++il) {
               const int i = pc.row0 + il;
-              const float E = expf(fminf(fmaxf(sG[i * LD + dcol] - gx, -dc), dc));
+              const float E = expf(clip_nan(sG[i * LD + dcol] - gx, -dc, dc));
               const float M = sDAq[i * LT + x] * (scale * q[i * D + dcol]) + sDA[i * LT + x] * (b[i * D + dcol] * k[i * D + dcol]);
               s2 += M * E;
             }
@@ -586,11 +586,11 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   // row tile rt only sees k blocks >= rt), then the gate gradients (mega.py:45-51) and the
   // combine with B4 (mega.py:52-59); dgc -> X1 for B5.  Row T-1 also needs the last-row decay
   // term (mega.py:50), a sum over all rows: its dgc is finished after the loop.
-  float* __restrict__ o_dq = a.dq + tb;
-  float* __restrict__ o_dk = a.dk + tb;
-  float* __restrict__ o_db = a.db + tb;
-  float* __restrict__ o_dw = a.dw + tb;
-  float* __restrict__ o_dv = a.dv + tb;
+  float* __restrict__ o_dq = a.dq + tio;
+  float* __restrict__ o_dk = a.dk + tio;
+  float* __restrict__ o_db = a.db + tio;
+  float* __restrict__ o_dw = a.dw + tio;
+  float* __restrict__ o_dv = a.dv + tio;
   float* sDgc = sX1;
   const float gl = sG[(T - 1) * LD + dcol];
   const float dlast = owned(3) && g == 3 ? a.dlast[(size_t)chunk * D + dcol] : 0.f;
@@ -702,7 +702,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     float4 off = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int s2 = NSEG - 1; s2 > sg; --s2) off = add4(off, ld4(sTot + s2 * LD + d));
 #pragma unroll
-    for (int i = 0; i < RUN; ++i) stg4(a.dg + tb + (sg * RUN + i) * D + d, san4(add4(x[i], off), clip));
+    for (int i = 0; i < RUN; ++i) stg4(a.dg + tio + (sg * RUN + i) * D + d, san4(add4(x[i], off), clip));
   }
 }
 
@@ -720,7 +720,7 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdPreArgs a) {
   __shared__ __attribute__((aligned(16))) float sOT[D * LT];      // dO^T: [value][token]
   const int chunk = blockIdx.x, tid = threadIdx.x, w = wave_id(), l = lane_id(), r = l & 15, g = l >> 4;
   const size_t tb = (size_t)chunk * T * D, sb = (size_t)chunk * T * T, hb = (size_t)chunk * D * D;
-  const float* __restrict__ dout = a.dout + tb;
+  const float* __restrict__ dout = a.dout + io_off<D>(a.cfg, chunk);
   // A operands, once per wave: X row block tp = w (all four k blocks: the blocks u < tp of
   // Aqk^T are exact zeros), Y row blocks kb = w + NW m.  Block (w, u) of Aqk^T in the operand
   // layout is block (u, w) of Aqk in the accumulator layout: FA(Aqk) block (u, w) transposed.

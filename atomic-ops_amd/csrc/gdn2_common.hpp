@@ -43,7 +43,16 @@ __device__ __forceinline__ float sanitize(float x, float c) {
 // legs and the element-wise gates.
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
-__device__ __forceinline__ float exp_nonpos(float x) { return fast_exp(fminf(x, 0.f)); }
+// min(x, 0) and clip(x, lo, hi) with NaN kept, as jnp.minimum / jnp.clip do (fminf / fmaxf
+// would return the other operand): IEEE 754-2019 minimum / maximum, one v_minimum3_f32 /
+// v_maximum3_f32 each on gfx950.  A NaN gate therefore gives a NaN factor, which the next
+// sanitize point turns into 0, exactly as in the reference.
+__device__ __forceinline__ float min0(float x) { return __builtin_elementwise_minimum(x, 0.f); }
+__device__ __forceinline__ float clip_nan(float x, float lo, float hi) {
+  return __builtin_elementwise_minimum(__builtin_elementwise_maximum(x, lo), hi);
+}
+
+__device__ __forceinline__ float exp_nonpos(float x) { return fast_exp(min0(x)); }
 
 // ---- bfloat16 helpers: round-to-nearest-even (NaN stays NaN) --------------------------
 // Two floats to two bfloat16, packed a | b << 16, by one v_cvt_pk_bf16_f32.

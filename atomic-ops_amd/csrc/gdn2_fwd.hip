@@ -63,10 +63,10 @@ __device__ __forceinline__ void score_pair(f4& accq, f4& acck, const TIn* __rest
     const float4 vi = ld4(gi + d), vj = ld4(gj + d), va = ld4(ga + d);
     float4 ra, cb;
     if constexpr (KIND == 0) {
-      ra = make_float4(fast_exp(fminf(vi.x - va.x, 0.f)), fast_exp(fminf(vi.y - va.y, 0.f)),
-                       fast_exp(fminf(vi.z - va.z, 0.f)), fast_exp(fminf(vi.w - va.w, 0.f)));
-      cb = make_float4(fast_exp(fminf(va.x - vj.x, 0.f)), fast_exp(fminf(va.y - vj.y, 0.f)),
-                       fast_exp(fminf(va.z - vj.z, 0.f)), fast_exp(fminf(va.w - vj.w, 0.f)));
+      ra = make_float4(fast_exp(min0(vi.x - va.x)), fast_exp(min0(vi.y - va.y)),
+                       fast_exp(min0(vi.z - va.z)), fast_exp(min0(vi.w - va.w)));
+      cb = make_float4(fast_exp(min0(va.x - vj.x)), fast_exp(min0(va.y - vj.y)),
+                       fast_exp(min0(va.z - vj.z)), fast_exp(min0(va.w - vj.w)));
     } else {
       const float4 h = scale4(sub4(va, ld4(gz + d)), 0.5f);
       ra = make_float4(fast_exp((vi.x - va.x) + h.x), fast_exp((vi.y - va.y) + h.y), fast_exp((vi.z - va.z) + h.z),
@@ -244,13 +244,13 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
   const Cfg& cf = a.cfg;
   const float clip = cf.clip;
   const int chunk = blockIdx.x;
-  const size_t tb = (size_t)chunk * T * D;
+  const size_t tb = (size_t)chunk * T * D, tio = io_off<D>(a.cfg, chunk);
   const size_t sb = (size_t)chunk * T * T;
-  const TIn* __restrict__ q = static_cast<const TIn*>(a.q) + tb;
-  const TIn* __restrict__ k = static_cast<const TIn*>(a.k) + tb;
-  const TIn* __restrict__ b = static_cast<const TIn*>(a.b) + tb;
-  const TIn* __restrict__ w = static_cast<const TIn*>(a.w) + tb;
-  const TIn* __restrict__ v = static_cast<const TIn*>(a.v) + tb;
+  const TIn* __restrict__ q = static_cast<const TIn*>(a.q) + tio;
+  const TIn* __restrict__ k = static_cast<const TIn*>(a.k) + tio;
+  const TIn* __restrict__ b = static_cast<const TIn*>(a.b) + tio;
+  const TIn* __restrict__ w = static_cast<const TIn*>(a.w) + tio;
+  const TIn* __restrict__ v = static_cast<const TIn*>(a.v) + tio;
   const int tid = threadIdx.x, wv = wave_id(), l = lane_id(), r = l & 15, g = l >> 4;
 
   // row-fragment items of this thread (item f is lane f%64 of 16x16 block f/64, so fragment
@@ -267,7 +267,7 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
   }
 
   // 1. gc = cumsum(g) inside the chunk
-  chunk_cumsum<D, LD, NT>(static_cast<const TIn*>(a.g) + tb, sG);
+  chunk_cumsum<D, LD, NT>(static_cast<const TIn*>(a.g) + tio, sG);
 
   // 2a. row fragments (cd_slim.py:17-21): FA(Kg) with kg = san(k e^{min(gl-gc,0)}),
   //     FA(Qg) with qg = san(q e^{min(gc,0)}); b*k and w*v into LDS.
@@ -336,7 +336,7 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
           const int row = pc.row0 + e / P, col = pc.col0 + e % P;
           float sq = 0.f, sk = 0.f;
           for (int d = 0; d < D; ++d) {
-            const float E = expf(fminf(fmaxf(sG[row * LD + d] - sG[col * LD + d], -dc), dc));
+            const float E = expf(clip_nan(sG[row * LD + d] - sG[col * LD + d], -dc, dc));
             const float kj = in_val(k + col * D + d);
             sq += (in_val(q + row * D + d) * E) * kj;
             sk += (sBK[row * LD + d] * E) * kj;
@@ -530,7 +530,7 @@ __global__ __launch_bounds__(256) void out_fwd_kernel(OutFwdArgs a) {
       drain(acc1, acc2);
       const float4 ov = make_float4(sanitize(scale * acc1[0] + acc2[0], clip), sanitize(scale * acc1[1] + acc2[1], clip),
                                     sanitize(scale * acc1[2] + acc2[2], clip), sanitize(scale * acc1[3] + acc2[3], clip));
-      stg4(a.o + tb + (size_t)(16 * tq + r) * D + 16 * cb + 4 * g, ov);
+      stg4(a.o + io_off<D>(a.cfg, chunk) + (size_t)(16 * tq + r) * D + 16 * cb + 4 * g, ov);
     }
   }
 }

@@ -22,8 +22,19 @@ struct PieceList {
 struct Cfg {
   float scale, wy_eps, ome, clip, diff_clip;   // ome = 1 - wy_eps, rounded once on the host
   int diag, dot_mode, solve_mode, b3_mode, mb;
+  int nc;        // chunks per (batch, head) sequence of this segment
+  int seq_ld;    // tokens between consecutive (batch, head) sequences of the raw operator tensors
   PieceList pieces;
 };
+
+// Offset in floats of a chunk (index (b, h) * nc + chunk of the segment) in a raw operator
+// tensor -- q..g, o, dO and the input gradients, (B, H, seq_ld, D) with the segment starting at
+// the pointer passed in.  Per-segment buffers (residual, workspace) are chunk-contiguous.
+template <int D>
+__device__ __forceinline__ size_t io_off(const Cfg& c, int chunk) {
+  const int bh = chunk / c.nc, cc = chunk - bh * c.nc;
+  return ((size_t)bh * c.seq_ld + (size_t)cc * T) * D;
+}
 
 // Per-chunk outputs of the WY build.  "_f" outputs are in fragment layout (gdn2_common.hpp):
 //   wp_f FA(Wp) (T x D), wpT_f FA(Wp^T) (D x T), uT_f FA(U^T) (D x T), kg_f FA(Kg) (T x D),
@@ -111,14 +122,14 @@ hipError_t launch_gemm_probe(int mode, const float* A, const float* B, float* C,
 // Device-side leg factors of a score piece (B4; the forward scores inline the same formulas).
 __device__ __forceinline__ float piece_row_leg(const Piece& pc, const float* sG, int LD, int i, int d) {
   const float gi = sG[i * LD + d];
-  if (pc.kind == 0) return fast_exp(fminf(gi - sG[pc.anchor * LD + d], 0.f));
+  if (pc.kind == 0) return fast_exp(min0(gi - sG[pc.anchor * LD + d]));
   const float r = sG[pc.s0 * LD + d];
   const float half = 0.5f * (r - sG[(pc.s1 - 1) * LD + d]);
   return fast_exp((gi - r) + half);
 }
 __device__ __forceinline__ float piece_col_leg(const Piece& pc, const float* sG, int LD, int j, int d) {
   const float gj = sG[j * LD + d];
-  if (pc.kind == 0) return fast_exp(fminf(sG[pc.anchor * LD + d] - gj, 0.f));
+  if (pc.kind == 0) return fast_exp(min0(sG[pc.anchor * LD + d] - gj));
   const float r = sG[pc.s0 * LD + d];
   const float half = 0.5f * (r - sG[(pc.s1 - 1) * LD + d]);
   return fast_exp((r - gj) - half);

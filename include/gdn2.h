@@ -2,8 +2,9 @@
  * gdn2.h -- C ABI of the MI355X (gfx950) GDN-2 operator library `libgdn2_hip.so`.
  *
  * This is the drop-in boundary under the Python API `make_blr_trainable(cfg, scale)`.
- * Plain pointers and sizes only: every tensor argument is a device pointer to a contiguous
- * float32 buffer, and `stream` is a `hipStream_t` (NULL = the default stream).  Kernels are
+ * Plain pointers and sizes only: every tensor argument is a device pointer to a float32
+ * buffer (contiguous, except that the raw operator tensors of a segment may lie inside longer
+ * sequences, see gdn2_desc.seq_ld), and `stream` is a `hipStream_t` (NULL = the default stream).  Kernels are
  * enqueued on `stream`; no call synchronises the device, allocates memory or keeps a
  * pointer after it returns (except the profiling calls, see below).  Every entry point
  * returns a gdn2_status; on failure gdn2_last_error() describes the problem.
@@ -32,7 +33,7 @@
 extern "C" {
 #endif
 
-#define GDN2_ABI_VERSION 1
+#define GDN2_ABI_VERSION 2
 
 /* Matmul precision modes (atomic_gdn2/precision.py:27-31; config.py:51-53). */
 enum { GDN2_DOT_HIGHEST = 0, GDN2_DOT_BF16X3 = 1, GDN2_DOT_DEFAULT = 2 };
@@ -43,11 +44,22 @@ enum { GDN2_OK = 0, GDN2_ERR_INVALID = 1, GDN2_ERR_UNSUPPORTED = 2, GDN2_ERR_HIP
 
 /* One segment call.  Field meaning follows BLRConfig (atomic_gdn2/config.py:38-60).
  * Supported by this build: bt == 64, D in {64, 128}, L % bt == 0, bs2 in {16, 32, 64},
- * bs2 | score_bs | bt, mb a power of two dividing bt. */
+ * bs2 | score_bs | bt, mb a power of two dividing bt.
+ *   L        tokens of this segment (a multiple of bt).
+ *   seq_ld   tokens between the starts of consecutive (b, h) sequences in the raw operator
+ *            tensors q..g, o, d_o, dq..dg (0 = L, i.e. contiguous (B, H, L, D)).  A segment
+ *            [t0, t0 + L) of a (B, H, L_full, D) tensor is passed as the pointer advanced by
+ *            t0 * D floats with seq_ld = L_full: the kernels read and write it in place, the way
+ *            the reference's segment loop slices and concatenates (pipeline.py:57-64).
+ *   state_ckpt  how the residual keeps the state for the backward (no counterpart in the
+ *            reference, whose residual keeps the state entering every chunk, pipeline.py:25):
+ *            0 = the state entering every chunk; K >= 1 = only every K-th chunk's, the backward
+ *            recomputes the others. */
 typedef struct gdn2_desc {
   int32_t B, H, L, D;
   int32_t bt, score_bs, bs2, mb;
   int32_t diag, dot_mode, solve_dot_mode, b3_dot_mode;
+  int32_t seq_ld, state_ckpt;
   double scale, wy_eps, clip, diff_clip;
 } gdn2_desc;
 

@@ -14,7 +14,7 @@ kernel, every instruction within ``window`` wait states after a ``v_mfma*`` that
 Wait states: one per instruction, ``s_nop N`` counts N + 1.  Code is followed in program
 order (branches are not followed), which is how the straight-line MFMA chains are written.
 
-Usage: ``python atomic-ops_amd/mfma_hazards.py`` (exit status 1 if any hazard is found).
+Usage: ``python tests/mfma_hazards.py`` (exit status 1 if any hazard is found).
 """
 from __future__ import annotations
 
@@ -24,8 +24,8 @@ import sys
 import tempfile
 from pathlib import Path
 
-HERE = Path(__file__).resolve().parent
-sys.path.insert(0, str(HERE))
+PKG = Path(__file__).resolve().parents[1] / "atomic-ops_amd"
+sys.path.insert(0, str(PKG))
 from build_lib import HIPFLAGS, _hipcc  # noqa: E402
 
 _RANGE = re.compile(r"v\[(\d+):(\d+)\]")
@@ -89,7 +89,7 @@ def scan(asm: str, window: int = 24) -> dict:
 def check_all(window: int = 24, verbose: bool = True) -> dict:
     found = {}
     with tempfile.TemporaryDirectory() as td:
-        for src in sorted((HERE / "csrc").glob("*.hip")):
+        for src in sorted((PKG / "csrc").glob("*.hip")):
             out = Path(td) / (src.stem + ".s")
             cmd = [_hipcc(), *HIPFLAGS, "--cuda-device-only", "-S", str(src), "-o", str(out)]
             r = subprocess.run(cmd, capture_output=True, text=True)

@@ -1,5 +1,5 @@
 """CPU check that the compiled gfx950 kernels keep the MFMA issue discipline: no instruction
-touches an in-flight MFMA's registers (atomic-ops_amd/mfma_hazards.py)."""
+touches an in-flight MFMA's registers (tests/mfma_hazards.py)."""
 import shutil
 import sys
 from pathlib import Path
@@ -7,7 +7,7 @@ from pathlib import Path
 import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
-sys.path.insert(0, str(ROOT / "atomic-ops_amd"))
+sys.path.insert(0, str(ROOT / "tests"))
 
 
 def test_scanner_flags_a_planted_hazard():

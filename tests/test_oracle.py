@@ -10,6 +10,7 @@ Each oracle function is checked against something that does not share its formul
 Planted mistakes at the end show that each pin fails on a plausible slip.
 """
 import json
+import math
 from pathlib import Path
 
 import numpy as np
@@ -322,12 +323,19 @@ def test_planted_mistakes_are_caught(monkeypatch):
     assert fwd_err() > 1e-3
     monkeypatch.setattr(O, "recompute_wy_ref", orig_wy)
 
-    # a transposed leaf in the inverse is caught by the scipy pin
-    S = torch.tril(torch.randn(64, 64, generator=torch.Generator().manual_seed(0)) * 0.1, -1)
-    bad = O.ladder_inverse(S.T.tril(-1) + S.tril(-1) * 0, 0.0, 64, 8)
+    # slips in the ladder inverse are caught by the scipy pin (test_ladder_inverse_vs_scipy)
+    S = torch.tril(torch.randn(64, 64, generator=torch.Generator().manual_seed(0)) * 0.3, -1)
     ref = torch.as_tensor(scipy.linalg.solve_triangular((torch.eye(64) + S).numpy(), np.eye(64), lower=True,
                                                         unit_diagonal=True))
-    assert float((bad - ref).abs().max()) > 1e-3
+    assert float((O.ladder_inverse(S, 0.0, 64, 8) - ref).abs().max()) < 1e-12
+    orig_leaf, orig_dot = O.micro_inv, O.make_dot
+    monkeypatch.setattr(O, "micro_inv", lambda Tm: orig_leaf(Tm).transpose(-1, -2))    # transposed leaf
+    assert float((O.ladder_inverse(S, 0.0, 64, 8) - ref).abs().max()) > 1e-3
+    monkeypatch.setattr(O, "micro_inv", orig_leaf)
+    # operands of every merge product swapped: S21 X11 -> X11 S21, X22 M -> M X22
+    monkeypatch.setattr(O, "make_dot", lambda mode: (lambda a, b_: orig_dot(mode)(b_, a)))
+    assert float((O.ladder_inverse(S, 0.0, 64, 8) - ref).abs().max()) > 1e-3
+    monkeypatch.setattr(O, "make_dot", orig_dot)
 
     # a dropped (1-eps) factor in dAkk is caught by the analytic-vs-autograd pin
     cfg_e = O.OracleCfg(wy_eps=0.05)
@@ -337,3 +345,46 @@ def test_planted_mistakes_are_caught(monkeypatch):
     bw = O.backward_mega_ref(*map(ch, (q, k, v, w, b, g)), kf["A"], kf["Aqk"], kf["h_pre"], kf["v_new"],
                              ch(2 * kf["o"]), 2 * kf["h_final"], 0.25, cfg_e.with_(wy_eps=0.0))
     assert max(rel(O.from_chunks(bw[n]), gr[n]) for n in ("dq", "dk", "db", "dg")) > 1e-4
+
+
+# ---------------------------------------------------------------- numerics helpers out of range
+def test_numerics_helpers_outside_their_ranges():
+    """precision.py:41-52 with jnp semantics: jnp.minimum and jnp.clip keep a NaN, the masks
+    are False at NaN, nan_to_num maps NaN -> 0 and +-inf -> +-clip after the clip."""
+    nan, inf = float("nan"), float("inf")
+    c = 5e3
+    x = torch.tensor([nan, inf, -inf, 2 * c, -2 * c, 0.5 * c, 0.0, -0.0], dtype=torch.float64)
+    assert torch.equal(O.sanitize(x, c), torch.tensor([0.0, c, -c, c, -c, 0.5 * c, 0.0, 0.0], dtype=torch.float64))
+
+    e, m = O.exp_nonpos(torch.tensor([nan, inf, -inf, 3.0, 0.0, -2.0], dtype=torch.float64))
+    assert torch.isnan(e[0]) and e[1] == 1.0 and e[2] == 0.0 and e[3] == 1.0 and e[4] == 1.0
+    assert abs(float(e[5]) - math.exp(-2.0)) < 1e-15
+    assert m.tolist() == [0.0, 0.0, 1.0, 0.0, 0.0, 1.0]
+
+    lo, hi = -20.0, 20.0
+    e, m = O.exp_clipped(torch.tensor([nan, inf, -inf, 25.0, -25.0, 3.0, 20.0], dtype=torch.float64), lo, hi)
+    assert torch.isnan(e[0])
+    assert torch.allclose(e[1:], torch.tensor([math.exp(hi), math.exp(lo), math.exp(hi), math.exp(lo), math.exp(3.0),
+                                               math.exp(hi)], dtype=torch.float64), rtol=1e-15, atol=0.0)
+    assert m.tolist() == [0.0, 0.0, 0.0, 0.0, 0.0, 1.0, 1.0]
+
+
+def test_nan_gate_is_zeroed_not_ignored(monkeypatch):
+    """A NaN gate makes e^{min(gc,0)} NaN and the next sanitize point zero it: in the
+    reference a NaN in g at token p of a chunk zeroes q's gated copy from p on (qg = san(q e^gc)),
+    where a NaN-dropping min (fminf) would leave qg = q there.  The check fails on that slip."""
+    cfg = O.OracleCfg()
+    q, k, v, w, b, g, _ = rand_inputs(1, 1, 64, 8, 3)
+    p = 40
+    g = g.clone()
+    g[..., p, 2] = float("nan")
+    gc = torch.cumsum(g, -2)
+    A = torch.eye(64, dtype=torch.float64)
+    _, _, _, qg, _ = O.recompute_wy_ref(q, k, v, w, b, gc, A, cfg)
+    assert torch.all(qg[..., p:, 2] == 0.0) and torch.all(qg[..., :p, 2] != 0.0)
+    orig = O.exp_nonpos
+    monkeypatch.setattr(O, "exp_nonpos", lambda x: (torch.exp(torch.nan_to_num(x, nan=0.0).clamp(max=0.0)),
+                                                   (x < 0).to(x.dtype)))
+    _, _, _, qg_bad, _ = O.recompute_wy_ref(q, k, v, w, b, gc, A, cfg)
+    assert not torch.all(qg_bad[..., p:, 2] == 0.0)
+    monkeypatch.setattr(O, "exp_nonpos", orig)

@@ -53,13 +53,14 @@ def test_library_exports_every_header_symbol():
     assert len(names) >= 10, names
     missing = [n for n in names if not hasattr(L, n)]
     assert not missing, missing
-    assert L.gdn2_abi_version() == 1
+    assert L.gdn2_abi_version() == 2
 
 
 def test_descriptor_struct_matches_header():
     from atomic_gdn2 import _lib
-    assert ctypes.sizeof(_lib.Gdn2Desc) == 12 * 4 + 4 * 8
-    assert _lib.Gdn2Desc.scale.offset == 48
+    assert ctypes.sizeof(_lib.Gdn2Desc) == 14 * 4 + 4 * 8
+    assert _lib.Gdn2Desc.seq_ld.offset == 48 and _lib.Gdn2Desc.state_ckpt.offset == 52
+    assert _lib.Gdn2Desc.scale.offset == 56
 
 
 def _desc(**kw):
@@ -98,6 +99,16 @@ def test_descriptor_validation(kw, msg):
     from atomic_gdn2 import _lib
     with pytest.raises(ValueError, match=msg):
         _lib.residual_layout(_desc(**kw))
+
+
+def test_segment_stride_validation():
+    from atomic_gdn2 import _lib
+    d = _desc(L=1024)
+    d.seq_ld = 512
+    with pytest.raises(ValueError, match="seq_ld"):
+        _lib.residual_layout(d)
+    d.seq_ld = 4096
+    _lib.residual_layout(d)
 
 
 def test_null_pointers_rejected_without_gpu_work():
