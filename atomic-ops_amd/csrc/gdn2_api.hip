@@ -1,5 +1,6 @@
 // C ABI of the GDN-2 library: descriptor validation, residual / workspace layout, kernel
 // sequencing per segment, and optional per-kernel HIP-event timing.
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -271,6 +272,54 @@ int gdn2_fwd_bf16(const gdn2_desc* d, const uint16_t* q, const uint16_t* k, cons
   return fwd_impl(d, q, k, v, w, b, g, true, h0, o, h_final, residual, workspace, stream);
 }
 
+}  // extern "C"
+
+namespace {
+// Workspace of the allocation-free forward: a file-scope device array, which the code object
+// loader places in every GPU the library is loaded on, at that GPU's own address, for the
+// life of the process.  Host code never passes `scratch` itself to a kernel (on the host the
+// name is only a stand-in for the symbol); it uses the per-device address that
+// hipGetSymbolAddress reports, looked up once per device with that device current.
+constexpr size_t kScratchBytes = size_t(64) << 20;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_ptr;     // per device ordinal; null = not looked up yet
+
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if ((int)g_scratch_ptr.size() <= dev) g_scratch_ptr.resize(dev + 1, nullptr);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(GDN2_ERR_HIP, "hipGetSymbolAddress(scratch) returned null");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return GDN2_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int gdn2_fwd_noalloc(const gdn2_desc* d, const float* q, const float* k, const float* v, const float* w,
+                     const float* b, const float* g, const float* h0, float* o, float* h_final, void* stream) {
+  const int st = validate(d);
+  if (st) return st;
+  const size_t need = gdn2_fwd_workspace_bytes(d, 0);
+  if (need > kScratchBytes)
+    return fail(GDN2_ERR_UNSUPPORTED, "gdn2_fwd_noalloc: this call needs " + std::to_string(need) +
+                                          " bytes of workspace, above the library's fixed " +
+                                          std::to_string(kScratchBytes) + "-byte device scratch");
+  void* ws = nullptr;
+  const int sa = scratch_address(&ws);
+  if (sa) return sa;
+  return fwd_impl(d, q, k, v, w, b, g, false, h0, o, h_final, nullptr, ws, stream);
+}
 
 int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v, const float* w,
              const float* b, const float* g, const void* residual, const float* d_o, const float* d_hf,

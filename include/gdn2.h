@@ -106,6 +106,19 @@ int gdn2_fwd_bf16(const gdn2_desc* d, const uint16_t* q, const uint16_t* k, cons
                   const uint16_t* w, const uint16_t* b, const uint16_t* g, const float* h0, float* o,
                   float* h_final, void* residual, void* workspace, void* stream);
 
+/* Forward of one segment without a residual, like gdn2_fwd(d, ..., residual = NULL, ...), with
+ * the workspace in a fixed 64 MiB (67108864-byte) device array inside the library instead of
+ * a caller buffer.  No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  It calls no allocating routine.  Calls whose gdn2_fwd_workspace_bytes(d, 0)
+ * exceeds 64 MiB (e.g. more than 453 chunks of B*H*L/bt at D = 128) fail with
+ * GDN2_ERR_UNSUPPORTED.  Every call on one GPU shares that GPU's array: calls that overlap in
+ * time on one GPU (different streams or host threads) race; serialise them.  Nothing in the
+ * array needs clearing: each call writes every byte it reads. */
+int gdn2_fwd_noalloc(const gdn2_desc* d, const float* q, const float* k, const float* v,
+                     const float* w, const float* b, const float* g, const float* h0, float* o,
+                     float* h_final, void* stream);
+
 /* Backward of one segment: cotangents d_o (B,H,L,D) and d_hf (B,H,D,D) -> the raw
  * (sanitized at cfg.clip) gradients of q, k, v, w, b, g and h0, all float32. */
 int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v, const float* w,
