@@ -24,7 +24,7 @@ RES_STORAGE = {"aqk": ("T", "T", True, False), "A": ("T", "T", False, False),
                "h_pre": ("D", "D", True, True), "v_new": ("D", "T", True, True),
                "wpT": ("D", "T", True, True), "kg": ("T", "D", True, False),
                "qg": ("T", "D", True, False), "gl": (None, "D", False, False)}
-KERNEL_NAMES = ("wy_fwd", "scan_fwd", "scan_bwd", "bwd_state", "bwd_wy", "out_fwd", "bwd_pre")
+KERNEL_NAMES = ("wy_fwd", "scan_fwd", "scan_bwd", "bwd_state", "bwd_wy", "out_fwd", "bwd_pre", "bwd_state_rc")
 ABI_VERSION = 2
 STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported configuration", 3: "HIP error"}
 

@@ -28,6 +28,13 @@ from .precision import sanitize
 _FINAL_CLIP = 1e4
 # chunk sizes (cfg.bt) the HIP kernels run
 SUPPORTED_BT = (64,)
+# How the residual keeps the state for the backward (gdn2_desc.state_ckpt): K >= 1 keeps the
+# state entering every K-th chunk and the backward recomputes the others inside its state
+# reductions; 0 keeps every chunk's (as the reference's residual does, pipeline.py:25).
+# K = 3 keeps a third of the states at the stored form's speed (MI355X, B4 H6 D128, rounds
+# interleaved: 0.5124 vs 0.5128 ms at L = 2048, 1.0218 vs 1.0209 ms at L = 4096); K = 4 keeps a
+# quarter for 2 % more time, K = 8 an eighth for 6 %.
+DEFAULT_STATE_CKPT = 3
 
 
 def _fin(x, dt, cfg):
@@ -67,8 +74,14 @@ def _segments(L, cfg):
     return [(t0, min(L, t0 + step)) for t0 in range(0, L, step)]
 
 
-def make_blr_trainable(cfg, scale):
+def make_blr_trainable(cfg, scale, state_ckpt=None):
+    """``state_ckpt``: this build's residual knob (no counterpart in the reference), see
+    DEFAULT_STATE_CKPT; it changes memory and time, not results (the recomputed states equal
+    the stored ones bit for bit)."""
     scale = float(scale)
+    ckpt = DEFAULT_STATE_CKPT if state_ckpt is None else int(state_ckpt)
+    if ckpt < 0:
+        raise ValueError(f"state_ckpt={ckpt} must be >= 0")
 
     class _Sequence(torch.autograd.Function):
         """The whole call as one autograd node.  Forward and backward run the reference's
@@ -93,7 +106,7 @@ def make_blr_trainable(cfg, scale):
             with torch.cuda.device(dev):
                 stream = _lib.stream_handle(dev)
                 for t0, t1 in _segments(L, cfg):
-                    desc = _lib.make_desc(cfg, B, H, t1 - t0, D, scale, seq_ld=L)
+                    desc = _lib.make_desc(cfg, B, H, t1 - t0, D, scale, seq_ld=L, state_ckpt=ckpt)
                     _, tot = _lib.residual_layout(desc)      # validates the descriptor
                     res = torch.empty(tot, dtype=torch.uint8, device=dev) if need_res else None
                     ws = torch.empty(L_.gdn2_fwd_workspace_bytes(ctypes.byref(desc), int(need_res)),

@@ -40,7 +40,7 @@ int validate(const gdn2_desc* d) {
   if (d->D != 64 && d->D != 128) return fail(GDN2_ERR_UNSUPPORTED, "this build supports D in {64, 128}");
   if (d->bs2 < 16) return fail(GDN2_ERR_UNSUPPORTED, "this build supports bs2 >= 16");
   if (d->seq_ld != 0 && d->seq_ld < d->L) return fail(GDN2_ERR_INVALID, "seq_ld must be 0 or >= L");
-  if (d->state_ckpt != 0) return fail(GDN2_ERR_UNSUPPORTED, "this build supports state_ckpt == 0 only");
+  if (d->state_ckpt < 0) return fail(GDN2_ERR_INVALID, "state_ckpt must be >= 0");
   return GDN2_OK;
 }
 
@@ -104,7 +104,8 @@ void residual_sizes(const gdn2_desc* d, size_t sz[GDN2_RES_COUNT]) {
   const Dims x = dims(d);
   sz[GDN2_RES_AQK] = x.n_chunks * x.tT * 4;
   sz[GDN2_RES_A] = x.n_chunks * x.tT * 4;
-  sz[GDN2_RES_HPRE] = x.n_chunks * x.DD * 4;
+  const size_t nck = d->state_ckpt > 0 ? (x.nc + d->state_ckpt - 1) / d->state_ckpt : x.nc;
+  sz[GDN2_RES_HPRE] = x.n_bh * nck * x.DD * 4;
   sz[GDN2_RES_VNEW] = x.n_chunks * x.tD * 4;
   sz[GDN2_RES_WPT] = x.n_chunks * x.tD * 4;
   sz[GDN2_RES_KG] = x.n_chunks * x.tD * 4;
@@ -242,14 +243,18 @@ int fwd_impl(const gdn2_desc* d, const void* q, const void* k, const void* v, co
   hipError_t e = timed(0, s, [&] { return gdn2::launch_wy_fwd(d->D, wa, s, bf16); });
   if (e != hipSuccess) return hip_fail(e, "wy_fwd launch");
 
-  // Training keeps h_pre and v_new for the backward: the scan carries only the state and the
-  // output follows chunk-parallel.  Without a residual the scan computes the output itself and
-  // h_pre / v_new never leave it.
-  gdn2::ScanFwdArgs sa{wp, kgT, uT, gl, h0, qg, aqk, h_final, residual ? nullptr : o, hpre, vnew,
-                       (int)x.nc, (int)x.n_bh, cfg};
+  // Without a residual the scan computes the output itself and h_pre / v_new never leave it.
+  // Training with state_ckpt = K >= 1 likewise, keeping v_new and every K-th chunk's entering
+  // state (the backward recomputes the others).  Training with state_ckpt = 0 keeps every
+  // chunk's h_pre and v_new: the scan carries only the state and the output follows
+  // chunk-parallel from them.
+  const int ck = d->state_ckpt;
+  const bool fused_out = !residual || ck > 0;
+  gdn2::ScanFwdArgs sa{wp, kgT, uT, gl, h0, qg, aqk, h_final, fused_out ? o : nullptr, hpre, vnew,
+                       (int)x.nc, (int)x.n_bh, ck, cfg};
   e = timed(1, s, [&] { return gdn2::launch_scan_fwd(d->D, sa, s); });
   if (e != hipSuccess) return hip_fail(e, "scan_fwd launch");
-  if (residual) {
+  if (!fused_out) {
     gdn2::OutFwdArgs oa{qg, aqk, hpre, vnew, o, (int)x.n_chunks, cfg};
     e = timed(5, s, [&] { return gdn2::launch_out_fwd(d->D, oa, s); });
     if (e != hipSuccess) return hip_fail(e, "out_fwd launch");
@@ -363,9 +368,17 @@ int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v,
   e = timed(2, s, [&] { return gdn2::launch_scan_bwd(d->D, sa, s); });
   if (e != hipSuccess) return hip_fail(e, "scan_bwd launch");
 
-  gdn2::BwdStateArgs ba{d_o, dvn, vnew, hpre, dhn, dqg, dwp, dkg, dlast, (int)x.n_chunks, cfg};
-  e = timed(3, s, [&] { return gdn2::launch_bwd_state(d->D, ba, s); });
-  if (e != hipSuccess) return hip_fail(e, "bwd_state launch");
+  if (d->state_ckpt > 0) {
+    // the states entering the chunks are recomputed from the checkpoints inside the reductions
+    gdn2::BwdStateRcArgs ba{d_o, dvn, vnew, hpre, dhn, kg, gl, dqg, dwp, dkg, dlast,
+                            (int)x.nc, (int)x.n_bh, d->state_ckpt, cfg};
+    e = timed(7, s, [&] { return gdn2::launch_bwd_state_rc(d->D, ba, s); });
+    if (e != hipSuccess) return hip_fail(e, "bwd_state_rc launch");
+  } else {
+    gdn2::BwdStateArgs ba{d_o, dvn, vnew, hpre, dhn, dqg, dwp, dkg, dlast, (int)x.n_chunks, cfg};
+    e = timed(3, s, [&] { return gdn2::launch_bwd_state(d->D, ba, s); });
+    if (e != hipSuccess) return hip_fail(e, "bwd_state launch");
+  }
 
   gdn2::BwdWyArgs wa{q, k, v, w, b, g, A, d_o, vnew, dvn, dqg, dwp, dkg, dlast,
                      dq, dk, dv, dw, db, dg, (int)x.n_chunks, cfg};

@@ -148,6 +148,171 @@ __global__ __launch_bounds__(D / 16 * WAVE) __attribute__((amdgpu_waves_per_eu(D
 }
 
 // ------------------------------------------------------------------------------------
+// bwd_state_rc: the reductions of bwd_state with the states recomputed from checkpoints.
+// One workgroup of NWW waves per (batch, head, block of K = ckpt chunks, group of NWW key
+// tiles); wave w owns key tile kt = grp NWW + w (key rows 16 kt .. 16 kt + 15) over all value
+// columns, with that slice of the state in registers in the MFMA result layout (lane (r, g) of
+// block kb holds h[16 kt + 4 g + e][16 kb + r], which is lane l of FA(h^T) block (kb, kt), the
+// checkpoint's layout).  Per chunk c of the block and value block kb:
+//   reductions   as bwd_state (dQg^T, dWp^T, dKg^T tiles (kt, ti) over kb; sum_v dh_next h)
+//                with h_pre block (kt, kb) = the register block, turned into the B-operand
+//                layout by a per-wave LDS transpose;
+//   state step   (all chunks of the block but the last) h[kt, kb] = state_update(h, gamma,
+//                sum_u Kg^T[kt, u] v_new[u, kb]): the forward scan's update with the same
+//                operands in the same MFMA order, so the recomputed state is the forward's bit
+//                for bit.  Given v_new (stored), each key tile's rows step on their own: no
+//                exchange between waves.
+// A operands of one kb are staged once per workgroup in LDS (double-buffered, one barrier per
+// kb; the staging pipeline runs across chunk boundaries): s dO, -dv_new, v_new in the A-operand
+// layout (transposed on the way in) and v_new as stored (FA(v_new^T) blocks, which are the
+// B operands of Kg^T v_new).
+// ------------------------------------------------------------------------------------
+template <int D, int NWW, int B3, int DOT>
+__global__ __launch_bounds__(NWW * WAVE) __attribute__((amdgpu_waves_per_eu(2))) void bwd_state_rc_kernel(
+    BwdStateRcArgs a) {
+  constexpr int NKB = D / 16, NKT = D / 16, NG = NKT / NWW;
+  constexpr int SLAB = 16 * WAVE;                // float4 staged per value block
+  constexpr int NST = 3;                         // float4 loaded per thread per value block
+  static_assert(NWW == 4, "staging: wave w loads token tile w of each of the three operands");
+  static_assert(NKT % NWW == 0 && NKB % 2 == 0, "key tile groups, value block parity");
+  __shared__ float4 sA[2 * SLAB];                // [buf][mat * 4 + tile][lane]
+  __shared__ __attribute__((aligned(16))) float sTr[NWW * 16 * TRP];
+  const Cfg& cf = a.cfg;
+  const int K = a.ckpt, nc = a.nc, nblk = (nc + K - 1) / K;
+  const int lin = xcd_remap(gridDim.x);
+  const int grp = lin % NG, blk = (lin / NG) % nblk, bh = lin / (NG * nblk);
+  const int c0 = blk * K, c1 = min(nc, c0 + K);
+  const int w = wave_id(), kt = grp * NWW + w, l = lane_id(), r = l & 15, g = l >> 4;
+  const float sc = cf.scale, clip = cf.clip;
+  float* tr = sTr + w * 16 * TRP;
+  auto chunk_idx = [&](int c) { return (size_t)bh * nc + c; };
+
+  // staging: wave w loads and stages token tile ti = w of the value block's three A operands
+  // (s dO, -dv_new, v_new), one float4 per lane each
+  // wave-uniform base pointers plus unsigned 32-bit lane offsets, so that the loads take the
+  // scalar-base form and no 64-bit per-lane address is kept live across the loop
+  const unsigned lo_do = (unsigned)((r * D) + 4 * g), lo4 = 4u * (unsigned)l;
+  auto fetch = [&](int c, int kb, float4 (&dst)[NST]) {
+    const size_t tb = chunk_idx(c) * T * D, tio = ((size_t)bh * cf.seq_ld + (size_t)c * T) * D;
+    dst[0] = ld4(sbase(a.dout + tio + (16 * w * D + 16 * kb)) + lo_do);
+    dst[1] = ld4(sbase(a.dv_new_f + tb + frag_blk(w, kb, D)) + lo4);
+    dst[2] = ld4(sbase(a.v_new_f + tb + frag_blk(kb, w, T)) + lo4);
+  };
+  auto put = [&](int buf, const float4 (&src)[NST]) {
+    float4* base = sA + buf * SLAB;
+    base[w * WAVE + l] = scale4(src[0], sc);
+    base[(4 + w) * WAVE + l] = scale4(src[1], -1.f);
+    // lane (r, g) holds v_new[16 w + 4 g + e][16 kb + r]: A-operand lane (4 g + e) + 16 (r / 4),
+    // component r % 4; and as stored for the state step
+    float* df = reinterpret_cast<float*>(base + (8 + w) * WAVE);
+    const int o = 4 * (4 * g + 16 * (r >> 2)) + (r & 3);
+    df[o] = src[2].x;
+    df[o + 4] = src[2].y;
+    df[o + 8] = src[2].z;
+    df[o + 12] = src[2].w;
+    base[(12 + w) * WAVE + l] = src[2];
+  };
+  auto dh_at = [&](int c, int kb) { return ld4(sbase(a.dh_next_f + chunk_idx(c) * D * D + frag_blk(kt, kb, D)) + lo4); };
+
+  f4 h[NKB];
+  {
+    const size_t hcb = ((size_t)bh * nblk + blk) * D * D;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      const float4 x = ld4(sbase(a.hck_f + hcb + frag_blk(kb, kt, D)) + lo4);
+      h[kb] = f4{x.x, x.y, x.z, x.w};
+    }
+  }
+  float4 st[2][NST], dhb[2];
+  fetch(c0, 0, st[0]);
+  dhb[0] = dh_at(c0, 0);
+  fetch(c0, 1, st[1]);
+  dhb[1] = dh_at(c0, 1);
+  put(0, st[0]);
+  __syncthreads();
+
+  for (int c = c0; c < c1; ++c) {
+    const size_t ch = chunk_idx(c), tb = ch * T * D;
+    const bool step = c + 1 < c1;
+    float4 kga[4] = {}, gm = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (step) {
+      // Kg^T block (kt, u) in the A-operand layout = FA(Kg) block (u, kt) transposed
+#pragma unroll
+      for (int u = 0; u < 4; ++u) kga[u] = wave_transpose16(tr, ld4(sbase(a.kg_f + tb + frag_blk(u, kt, D)) + lo4), r, g);
+      gm = ld4(sbase(a.gl + ch * D + 16 * kt) + 4 * g);
+    }
+    f4 acc[3][4];
+#pragma unroll
+    for (int m = 0; m < 3; ++m)
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) acc[m][ti] = f4{0.f, 0.f, 0.f, 0.f};
+    float part = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      const int pb = kb & 1;
+      const float4 hp = wave_transpose16(tr, f4_to_float4(h[kb]), r, g);
+      const float4 dhc = dhb[pb];
+      {
+        // two value blocks ahead, across the chunk boundary
+        const int kn = kb + 2 < NKB ? kb + 2 : kb + 2 - NKB, cn = kb + 2 < NKB ? c : c + 1;
+        if (cn < c1) {
+          fetch(cn, kn, st[pb]);
+          dhb[pb] = dh_at(cn, kn);
+        }
+      }
+      const float4* cur = sA + pb * SLAB;
+      // operands of token tile ti + 1 are read while tile ti's MFMAs issue; the fences keep
+      // the compiler from hoisting every read of the block (64 VGPRs) above the first MFMA
+      float4 o0 = cur[l], o1 = cur[4 * WAVE + l], o2 = cur[8 * WAVE + l];
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) {
+        float4 n0 = o0, n1 = o1, n2 = o2;
+        if (ti < 3) {
+          n0 = cur[(ti + 1) * WAVE + l];
+          n1 = cur[(5 + ti) * WAVE + l];
+          n2 = cur[(9 + ti) * WAVE + l];
+        }
+        mma16<B3>(acc[0][ti], o0, hp);
+        mma16<B3>(acc[1][ti], o1, hp);
+        mma16<B3>(acc[2][ti], o2, dhc);
+        __builtin_amdgcn_sched_barrier(0);
+        o0 = n0;
+        o1 = n1;
+        o2 = n2;
+      }
+      part = fmaf(dhc.x, hp.x, part);
+      part = fmaf(dhc.y, hp.y, part);
+      part = fmaf(dhc.z, hp.z, part);
+      part = fmaf(dhc.w, hp.w, part);
+      if (step) {
+        f4 hn = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) mma16<DOT>(hn, kga[u], cur[(12 + u) * WAVE + l]);
+        drain(hn);
+        const float gmv[4] = {gm.x, gm.y, gm.z, gm.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[kb][e] = state_update(h[kb][e], gmv[e], hn[e], clip);
+      }
+      if (kb + 1 < NKB || c + 1 < c1) put(pb ^ 1, st[pb ^ 1]);     // the next value block
+      __syncthreads();
+    }
+    drain(acc[0][0], acc[0][1], acc[0][2], acc[0][3]);
+    drain(acc[1][0], acc[1][1], acc[1][2], acc[1][3]);
+    drain(acc[2][0], acc[2][1], acc[2][2], acc[2][3]);
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) {
+      const size_t o = tb + frag_blk(kt, ti, T);
+      stg4(sbase(a.dqg + o) + lo4, f4_to_float4(acc[0][ti]));
+      stg4(sbase(a.dwp + o) + lo4, f4_to_float4(acc[1][ti]));
+      stg4(sbase(a.dkg + o) + lo4, f4_to_float4(acc[2][ti]));
+    }
+    part += __shfl_xor(part, 16);
+    part += __shfl_xor(part, 32);
+    if (g == 0) sbase(a.dlast + ch * D + 16 * kt)[r] = part;
+  }
+}
+
+// ------------------------------------------------------------------------------------
 // bwd_wy: one workgroup (8 waves) per chunk.
 //
 // Output ownership: wave w owns column strip s = w % (D/16) (columns 16 s .. 16 s + 15) and
@@ -795,6 +960,22 @@ hipError_t launch_bwd_state(int D, const BwdStateArgs& a, hipStream_t s) {
     constexpr int M = decltype(m)::value;
     if (D == 128) hipLaunchKernelGGL((bwd_state_kernel<128, M>), dim3(a.n_chunks), dim3(8 * WAVE), 0, s, a);
     else hipLaunchKernelGGL((bwd_state_kernel<64, M>), dim3(a.n_chunks), dim3(4 * WAVE), 0, s, a);
+    return 0;
+  });
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd_state_rc(int D, const BwdStateRcArgs& a, hipStream_t s) {
+  const int nblk = (a.nc + a.ckpt - 1) / a.ckpt;
+  dispatch_mode(a.cfg.b3_mode, [&](auto m3) {
+    dispatch_mode(a.cfg.dot_mode, [&](auto md) {
+      constexpr int M3 = decltype(m3)::value, MD = decltype(md)::value;
+      if (D == 128)
+        hipLaunchKernelGGL((bwd_state_rc_kernel<128, 4, M3, MD>), dim3(a.n_bh * nblk * 2), dim3(4 * WAVE), 0, s, a);
+      else
+        hipLaunchKernelGGL((bwd_state_rc_kernel<64, 4, M3, MD>), dim3(a.n_bh * nblk), dim3(4 * WAVE), 0, s, a);
+      return 0;
+    });
     return 0;
   });
   return hipGetLastError();

@@ -54,6 +54,13 @@ __device__ __forceinline__ float clip_nan(float x, float lo, float hi) {
 
 __device__ __forceinline__ float exp_nonpos(float x) { return fast_exp(min0(x)); }
 
+// One element of the inter-chunk state update h = san(h e^gamma + (Kg^T v_new)), gamma <= 0
+// (fwd/cd_slim.py:28-29).  The forward scan and the backward's state recompute both call this,
+// so a recomputed state equals the forward's bit for bit.
+__device__ __forceinline__ float state_update(float h, float gamma, float kv, float clip) {
+  return sanitize(fmaf(h, exp_nonpos(gamma), kv), clip);
+}
+
 // ---- bfloat16 helpers: round-to-nearest-even (NaN stays NaN) --------------------------
 // Two floats to two bfloat16, packed a | b << 16, by one v_cvt_pk_bf16_f32.
 typedef float f2v __attribute__((ext_vector_type(2)));
@@ -225,6 +232,31 @@ __device__ __forceinline__ float4 in_ldg4(const uint16_t* p) {
                      __uint_as_float(u[1] & 0xffff0000u));
 }
 __device__ __forceinline__ void st4(float* p, const float4& x) { *reinterpret_cast<float4*>(p) = x; }
+
+// A wave-uniform global address held in SGPRs, opaque to the optimiser: p + (32-bit lane
+// offset) then compiles to a scalar-base global load / store (saddr + 32-bit voffset), and
+// loop-invariant code motion cannot merge the lane offset into per-block 64-bit sums and keep
+// one such VGPR pair live for every block of a loop.  The argument must be wave-uniform.
+typedef __attribute__((address_space(1))) float gfloat;
+typedef __attribute__((address_space(1))) const float cgfloat;
+__device__ __forceinline__ cgfloat* sbase(const float* p) {
+  cgfloat* q = (cgfloat*)p;
+  asm volatile("" : "+s"(q));
+  return q;
+}
+__device__ __forceinline__ gfloat* sbase(float* p) {
+  gfloat* q = (gfloat*)p;
+  asm volatile("" : "+s"(q));
+  return q;
+}
+__device__ __forceinline__ float4 ld4(cgfloat* p) {
+  const f4 v = *reinterpret_cast<const __attribute__((address_space(1))) f4*>(p);
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void stg4(gfloat* p, const float4& x) {
+  const f4 v = {x.x, x.y, x.z, x.w};
+  __builtin_nontemporal_store(v, reinterpret_cast<__attribute__((address_space(1))) f4*>(p));
+}
 // Global store with the non-temporal (streaming) hint, for outputs that only a later kernel
 // reads: they then do not evict from L2 the inputs that the writing kernel reads again.
 __device__ __forceinline__ void stg4(float* p, const float4& x) {

@@ -55,10 +55,12 @@ struct WyFwdArgs {
 // (row-major D x D) and, when h_pre_f / v_new_f are set, per chunk the entering state h_pre as
 // FA(h_pre^T) (D x D) and v_new as FA(v_new^T) (D x T).  With o set it also reads FA(Qg),
 // FA(Aqk) and writes o (row-major T x D per chunk); otherwise out_fwd computes o.
+// ckpt = K >= 2: h_pre_f keeps only the state entering chunks c = 0, K, 2K, ... of each
+// (batch, head), as checkpoint c / K of ceil(nc / K); ckpt 0 or 1: every chunk's.
 struct ScanFwdArgs {
   const float *wp_f, *kgT_f, *uT_f, *gl, *h0, *qg_f, *aqk_f;
   float *hf, *o, *h_pre_f, *v_new_f;    // o, h_pre_f, v_new_f may be null
-  int nc, n_bh;
+  int nc, n_bh, ckpt;
   Cfg cfg;
 };
 
@@ -98,6 +100,18 @@ struct BwdStateArgs {
   Cfg cfg;
 };
 
+// bwd_state with the states recomputed from checkpoints: per (batch, head) block of ckpt = K
+// chunks the state entering the block (checkpoint FA(h^T), ceil(nc / K) per (batch, head)) is
+// stepped forward through the block, h <- san(e^gamma h + Kg^T v_new), from FA(Kg), gl and the
+// stored FA(v_new^T) -- the forward scan's own update, bit for bit -- and each chunk's
+// reductions use it as h_pre.  Outputs as BwdStateArgs.
+struct BwdStateRcArgs {
+  const float *dout, *dv_new_f, *v_new_f, *hck_f, *dh_next_f, *kg_f, *gl;
+  float *dqg, *dwp, *dkg, *dlast;
+  int nc, n_bh, ckpt;
+  Cfg cfg;
+};
+
 struct BwdWyArgs {
   const float *q, *k, *v, *w, *b, *g, *A, *dout, *v_new_f, *dv_new_f;
   const float *dqg, *dwp, *dkg, *dlast;
@@ -112,12 +126,21 @@ hipError_t launch_out_fwd(int D, const OutFwdArgs& a, hipStream_t s);
 hipError_t launch_bwd_pre(int D, const BwdPreArgs& a, hipStream_t s);
 hipError_t launch_scan_bwd(int D, const ScanBwdArgs& a, hipStream_t s);
 hipError_t launch_bwd_state(int D, const BwdStateArgs& a, hipStream_t s);
+hipError_t launch_bwd_state_rc(int D, const BwdStateRcArgs& a, hipStream_t s);
 hipError_t launch_bwd_wy(int D, const BwdWyArgs& a, hipStream_t s);
 
 // Diagnostics: C[M,N] = A[M,K] * B[K,N] (row-major, fp32 storage) through the MFMA tile
 // routine of the given dot mode.  M, N, K multiples of 16, at most 64 x 64 x 128.
 hipError_t launch_gemm_probe(int mode, const float* A, const float* B, float* C, int M, int N,
                              int K, hipStream_t s);
+
+// Linear work index of this workgroup such that consecutive indices (workgroups of one
+// (batch, head), which read the same chunk operands) land on the same XCD (blockIdx % 8 picks
+// the XCD) and are served from that XCD's L2.  Identity unless nblk % 8 == 0.
+__device__ __forceinline__ int xcd_remap(int nblk) {
+  const int b = blockIdx.x;
+  return (nblk % 8) ? b : (b % 8) * (nblk / 8) + b / 8;
+}
 
 // Device-side leg factors of a score piece (B4; the forward scores inline the same formulas).
 __device__ __forceinline__ float piece_row_leg(const Piece& pc, const float* sG, int LD, int i, int d) {

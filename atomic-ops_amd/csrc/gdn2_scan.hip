@@ -32,13 +32,6 @@
 
 namespace gdn2 {
 
-// Workgroups of one (batch, head) land on the same XCD (blockIdx % 8 picks the XCD), so
-// the chunk operands they all read are served from that XCD's L2.
-__device__ __forceinline__ int xcd_remap(int nblk) {
-  const int b = blockIdx.x;
-  return (nblk % 8) ? b : (b % 8) * (nblk / 8) + b / 8;
-}
-
 // Forward scan, with the output fused in when no residual is kept (OUT; in training the
 // output waves only carry their state rows).  Eight waves per workgroup (slice of 16 value
 // columns of one (batch, head)); per chunk two barriers:
@@ -120,7 +113,10 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
   auto step = [&](const FwdOps<NH>& op, int c, FwdOps<NH>& nx, int cn) {
     const size_t ch = (size_t)bh * nc + c, tb = ch * T * D;
     const size_t tbn = base(cn) * T * D, sbn = base(cn) * T * T;
-    if (OWNS && a.h_pre_f) stg4(a.h_pre_f + ch * D * D + frag_blk(vb, w, D) + 4 * l, f4_to_float4(h));
+    if (OWNS && a.h_pre_f && (a.ckpt <= 1 || c % a.ckpt == 0)) {
+      const size_t hi = a.ckpt <= 1 ? ch : (size_t)bh * ((nc + a.ckpt - 1) / a.ckpt) + c / a.ckpt;
+      stg4(a.h_pre_f + hi * D * D + frag_blk(vb, w, D) + 4 * l, f4_to_float4(h));
+    }
     // ---- window A ----
     float4 hb[NH];
     if constexpr (V || O) {
@@ -161,7 +157,7 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
       drain(hn);
       const float gmv[4] = {op.gm.x, op.gm.y, op.gm.z, op.gm.w};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) h[e] = sanitize(h[e] * exp_nonpos(gmv[e]) + hn[e], clip);
+      for (int e = 0; e < 4; ++e) h[e] = state_update(h[e], gmv[e], hn[e], clip);
       nx.gm = ld4(a.gl + base(cn) * D + 16 * w + 4 * g);
     }
     if constexpr (O) {

@@ -38,14 +38,18 @@ B_, H_, L_, D_, T_ = 4, 6, 2048, 128, 64
 # Algorithmic FLOPs per (batch, head, token) of the work each kernel does, in the dense
 # convention of the canonical count (every T x T operand dense).  Their sum is the canonical
 # F_grad minus the W recompute (2*T*D) that this implementation keeps as a residual instead.
-def kernel_flops_per_token(T=T_, D=D_):
+# With state checkpoints (state_ckpt >= 1) the training forward scan also computes o (the
+# output kernel does not run), and bwd_state_rc does bwd_state's reductions; the 2 D^2 per
+# token of its state recompute ((K-1)/K of the chunks) is extra work, not counted.
+def kernel_flops_per_token(T=T_, D=D_, fused_out=False):
     return {
         "wy_fwd": 8 * T * D,                      # Aqk, Akk, Wp, U
-        "scan_fwd": 4 * D * D,                    # Wp h, Kg^T v_new
+        "scan_fwd": 4 * D * D + (2 * T * D + 2 * D * D if fused_out else 0),   # Wp h, Kg^T v_new (+ o)
         "out_fwd": 2 * T * D + 2 * D * D,         # Aqk v_new, Qg h_pre
         "bwd_pre": 2 * T * D + 2 * D * D,         # Aqk^T dO, Qg^T dO
         "scan_bwd": 4 * D * D,                    # Kg dh, Wp^T dv_new
         "bwd_state": 6 * D * D,                   # dQg, dWp, dKg
+        "bwd_state_rc": 6 * D * D,                # dQg, dWp, dKg (+ uncounted state recompute)
         "bwd_wy": 18 * T * D + 4 * T * T,         # dAqk, dA, dkb, dwv, B4; dA A^T, A^T tmp
     }
 
@@ -195,6 +199,62 @@ def sweep_config3(cfg, seed):
     return out
 
 
+def state_ckpt_table(cfg, seed, ks=(0, 1, 2, 3, 4, 8, 32)):
+    """Stored vs recomputed states: per state_ckpt K (0 = every chunk's state kept) the
+    grad-eval latency under the median protocol, the residual size and the per-kernel HIP-event
+    durations, at config 2 and at B4 H6 L4096."""
+    import ctypes
+    import torch
+    from atomic_gdn2 import make_blr_trainable, _lib
+    from atomic_gdn2.synthetic import make_inputs
+    rows = []
+    for (B, H, L) in ((4, 6, 2048), (4, 6, 4096)):
+        (q, k, v, w, b, g), scale = make_inputs(B, H, L, 128, seed=seed)
+        xs = [t.requires_grad_(True) for t in (q, k, v, w, b, g)]
+
+        def make_step(K):
+            fn = make_blr_trainable(cfg, scale, state_ckpt=K)
+
+            def step():
+                o, hf = fn(*xs)
+                return torch.autograd.grad((o, hf), xs, grad_outputs=(2.0 * o, 2.0 * hf))
+            return step
+
+        steps = {K: make_step(K) for K in ks}
+        # every K warmed up first, then 5 rounds that each time every K in turn (the mean of 4
+        # calls), so clock and cache state are shared fairly; the median round per K
+        for K in ks:
+            for _ in range(3):
+                steps[K]()
+        torch.cuda.synchronize()
+        per = {K: [] for K in ks}
+        for _ in range(5):
+            for K in ks:
+                t0 = time.perf_counter()
+                for _ in range(4):
+                    steps[K]()
+                torch.cuda.synchronize()
+                per[K].append((time.perf_counter() - t0) * 1e3 / 4)
+        for K in ks:
+            step = steps[K]
+            ms = sorted(per[K])[len(per[K]) // 2]
+            _lib.prof_begin(4 * 16)
+            for _ in range(4):
+                step()
+            torch.cuda.synchronize()
+            prof = _lib.prof_end()
+            seg = min(L, cfg.max_chunks_per_call * cfg.bt)
+            desc = _lib.make_desc(cfg, B, H, seg, 128, scale, seq_ld=L, state_ckpt=K)
+            offs, tot = _lib.residual_layout(desc)
+            nseg = L // seg
+            rows.append({"B": B, "H": H, "L": L, "state_ckpt": K, "ms": round(ms, 4),
+                         "residual_mb": round(tot * nseg / 1e6, 1),
+                         "state_mb": round((offs[3] - offs[2]) * nseg / 1e6, 1),
+                         "kernel_us": {n: round(t / c * 1e3, 1) for n, (t, c) in prof.items() if c}})
+        del xs, q, k, v, w, b, g
+    return rows
+
+
 def bench_config4(cfg, seed):
     """Config 4: forward-only long context, B8 H16 D128, bf16 inputs, fp32
     state; L = 32768 as 8 calls of 4096 tokens, each call's h0 = the previous h_final.  Inputs
@@ -260,6 +320,15 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--state-ckpt", type=int, default=None,
+                    help="residual state checkpoint interval K (0 = every chunk's state kept); "
+                         "default: the library's DEFAULT_STATE_CKPT")
+    ap.add_argument("--ckpt-table", action="store_true", help="only print the state_ckpt table and exit")
+    ap.add_argument("--profile-only", action="store_true",
+                    help="for rocprofv3: run --warmup then --steps gradient evaluations of the workload "
+                         "(no timing loops, no forward-only pass, no other configs) and print nothing else")
+    ap.add_argument("--seq-len", type=int, default=L_,
+                    help="sequence length of the workload for --profile-only (default 2048, config 2)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sweep", action="store_true", help="skip the config-3 sweep and the config-4 run")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end LM training step")
@@ -284,7 +353,7 @@ def main():
 
     import torch
     from atomic_gdn2 import make_cfg, make_blr_trainable, _lib
-    from atomic_gdn2.synthetic import make_inputs_np, inputs_sha256
+    from atomic_gdn2.synthetic import make_inputs, make_inputs_np, inputs_sha256
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -295,7 +364,26 @@ def main():
     xs = [t.requires_grad_(True) for t in (q, k, v, w, b, g)]
     cfg = make_cfg(bt=64, bc=32, score_bs=64, bs2=32, mb=8, wy_eps=0.0, dot_mode="highest",
                    solve_dot_mode="highest", b3_dot_mode="highest")
-    fn = make_blr_trainable(cfg, scale)
+    from atomic_gdn2.pipeline import DEFAULT_STATE_CKPT
+    ckpt = DEFAULT_STATE_CKPT if args.state_ckpt is None else args.state_ckpt
+    if args.ckpt_table:
+        print(json.dumps({"state_ckpt_table": state_ckpt_table(cfg, args.seed)}), flush=True)
+        return
+    if args.profile_only:
+        if args.seq_len == L_:
+            pxs, pscale = xs, scale
+        else:
+            pts, pscale = make_inputs(B_, H_, args.seq_len, D_, seed=args.seed)
+            pxs = [t.requires_grad_(True) for t in pts]
+        pfn = make_blr_trainable(cfg, pscale, state_ckpt=ckpt)
+        for _ in range(args.warmup + args.steps):
+            o, hf = pfn(*pxs)
+            torch.autograd.grad((o, hf), pxs, grad_outputs=(2.0 * o, 2.0 * hf))
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_only": True, "B": B_, "H": H_, "L": args.seq_len, "state_ckpt": ckpt,
+                          "grad_evals": args.warmup + args.steps}), flush=True)
+        return
+    fn = make_blr_trainable(cfg, scale, state_ckpt=ckpt)
 
     def step():
         # gradient of loss = sum(o^2) + sum(h_final^2): forward, the loss's cotangents
@@ -335,7 +423,7 @@ def main():
 
     ff, fb = canonical_flops(B_, H_, L_, D_)
     tflops = (ff + fb) / (ms * 1e-3) / 1e12
-    kf = kernel_flops_per_token()
+    kf = kernel_flops_per_token(fused_out=ckpt > 0)
     ntok = B_ * H_ * L_
     # HBM bytes per launch measured by rocprof counters (FETCH_SIZE / WRITE_SIZE, scaled by a
     # copy kernel) at this workload; with this launch's own time they give each kernel's
@@ -361,7 +449,7 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
         "config": {"workload": "gdn2 grad-eval (fwd+bwd of sum(o^2)+sum(h_final^2)) B4 H6 L2048 D128 "
                                "chunk64 wy_eps0 dot=highest", "B": B_, "H": H_, "L": L_, "D": D_, "bt": 64,
-                   "seed": args.seed, "inputs_sha256": sha},
+                   "seed": args.seed, "inputs_sha256": sha, "state_ckpt": ckpt},
         "fwd_ms": round(fwd_ms, 4), "fwd_tokens_per_s": round(B_ * L_ / (fwd_ms * 1e-3), 1),
         "canonical_gflop": round((ff + fb) / 1e9, 3),
         "canonical_gb_per_s": round(canonical_bytes(B_, H_, L_, D_) / (ms * 1e-3) / 1e9, 1),
@@ -373,6 +461,7 @@ def main():
     }
     if not args.no_sweep:
         out["config2_seeds"] = seeds_config2(cfg)
+        out["state_ckpt_table"] = state_ckpt_table(cfg, args.seed)
         out["config3_sweep"] = sweep_config3(cfg, args.seed)
         out["config4_long_context_fwd"] = bench_config4(cfg, args.seed)
     if not args.no_e2e:

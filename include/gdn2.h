@@ -67,7 +67,9 @@ typedef struct gdn2_desc {
  * reported by gdn2_residual_layout (bytes, 256-aligned), float32, per chunk:
  *   AQK   (B,H,nc, bt*bt)  gated q.k scores, FRAG(Aqk)                         (pipeline.py:25)
  *   A     (B,H,nc,bt,bt)   the WY inverse (I + (1-eps) Akk)^-1, row-major        (pipeline.py:25)
- *   HPRE  (B,H,nc, D*D)    state entering each chunk, FRAG(h_pre^T)              (cd_slim.py:22)
+ *   HPRE  (B,H,nck, D*D)   state entering each chunk (nck = nc, state_ckpt 0 or 1) or only
+ *                          chunks 0, K, 2K, .. (state_ckpt = K: nck = ceil(nc / K)),
+ *                          FRAG(h_pre^T)                                          (cd_slim.py:22)
  *   VNEW  (B,H,nc, D*bt)   v_new of each chunk, FRAG(v_new^T)                    (cd_slim.py:23)
  *   WPT   (B,H,nc, D*bt)   W = A (b k e^gc), FRAG(W^T)                           (cd_slim.py:17)
  *   KG    (B,H,nc, bt*D)   gated k, FRAG(Kg)                                     (cd_slim.py:20)
@@ -142,9 +144,10 @@ int gdn2_debug_gemm(int mode, const float* A, const float* B, float* C, int M, i
  * gdn2_prof_begin(n) starts recording for up to n launches (process-wide, not re-entrant);
  * gdn2_prof_end synchronises on the recorded events and returns, per kernel id, the summed
  * duration in milliseconds and the launch count, then stops recording.
- * Kernel ids: 0 wy_fwd, 1 scan_fwd (without a residual also the output), 2 scan_bwd,
- * 3 bwd_state, 4 bwd_wy, 5 out_fwd (training only), 6 bwd_pre. */
-#define GDN2_NUM_KERNELS 7
+ * Kernel ids: 0 wy_fwd, 1 scan_fwd (with the output unless state_ckpt == 0 in training),
+ * 2 scan_bwd, 3 bwd_state (state_ckpt == 0), 4 bwd_wy, 5 out_fwd (training, state_ckpt == 0),
+ * 6 bwd_pre, 7 bwd_state_rc (state_ckpt >= 1: bwd_state with the states recomputed). */
+#define GDN2_NUM_KERNELS 8
 int gdn2_prof_begin(int max_launches);
 int gdn2_prof_end(double ms_sum[GDN2_NUM_KERNELS], int counts[GDN2_NUM_KERNELS]);
 

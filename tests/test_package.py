@@ -101,6 +101,24 @@ def test_descriptor_validation(kw, msg):
         _lib.residual_layout(_desc(**kw))
 
 
+def test_state_checkpoint_residual_layout():
+    """state_ckpt = K keeps ceil(nc / K) states per (batch, head) instead of nc; negative K is
+    rejected."""
+    from atomic_gdn2 import _lib
+    d0 = _desc()
+    offs0, tot0 = _lib.residual_layout(d0)
+    for K, nck in ((1, 32), (2, 16), (3, 11), (32, 1), (100, 1)):
+        d = _desc()
+        d.state_ckpt = K
+        offs, tot = _lib.residual_layout(d)
+        assert offs[3] - offs[2] == 4 * 6 * nck * 128 * 128 * 4
+        assert tot0 - tot == 4 * 6 * (32 - nck) * 128 * 128 * 4
+    d = _desc()
+    d.state_ckpt = -1
+    with pytest.raises(ValueError, match="state_ckpt"):
+        _lib.residual_layout(d)
+
+
 def test_segment_stride_validation():
     from atomic_gdn2 import _lib
     d = _desc(L=1024)
