@@ -26,8 +26,8 @@ from . import _lib
 from .precision import sanitize
 
 _FINAL_CLIP = 1e4
-# chunk sizes (cfg.bt) the HIP kernels run
-SUPPORTED_BT = (64,)
+# chunk sizes (cfg.bt) the HIP kernels run (bt = 128 as pairs of 64-token half chunks, exactly)
+SUPPORTED_BT = (64, 128)
 # How the residual keeps the state for the backward (gdn2_desc.state_ckpt): K >= 1 keeps the
 # state entering every K-th chunk and the backward recomputes the others inside its state
 # reductions; 0 keeps every chunk's (as the reference's residual does, pipeline.py:25).
@@ -166,7 +166,7 @@ def make_blr_trainable(cfg, scale, state_ckpt=None):
         hf = torch.empty((B, H, D, D), dtype=torch.float32, device=dev)
         L_ = _lib.lib()
         with torch.cuda.device(dev):
-            _lib.residual_layout(desc)                   # validates the descriptor
+            # (an invalid descriptor gives 0 bytes here and a ValueError from the call below)
             ws = torch.empty(L_.gdn2_fwd_workspace_bytes(ctypes.byref(desc), 0), dtype=torch.uint8, device=dev)
             entry = L_.gdn2_fwd_bf16 if bf16 else L_.gdn2_fwd
             _lib.check(entry(ctypes.byref(desc), *map(_lib.ptr, xs), _lib.ptr(h0c), _lib.ptr(o), _lib.ptr(hf),

@@ -36,12 +36,33 @@ int validate(const gdn2_desc* d) {
     if (m < GDN2_DOT_HIGHEST || m > GDN2_DOT_DEFAULT) return fail(GDN2_ERR_INVALID, "unknown dot mode");
   if (d->diag != GDN2_DIAG_BTL && d->diag != GDN2_DIAG_LEAN) return fail(GDN2_ERR_INVALID, "unknown diag");
   if (!(d->clip > 0.0)) return fail(GDN2_ERR_INVALID, "clip must be positive");
-  if (d->bt != gdn2::T) return fail(GDN2_ERR_UNSUPPORTED, "this build supports bt == 64 only");
+  if (d->bt != gdn2::T && d->bt != 2 * gdn2::T)
+    return fail(GDN2_ERR_UNSUPPORTED, "this build supports bt in {64, 128}");
+  if (d->bt == 2 * gdn2::T && d->bs2 > gdn2::T)
+    return fail(GDN2_ERR_UNSUPPORTED, "this build supports bs2 <= 64 at bt == 128");
   if (d->D != 64 && d->D != 128) return fail(GDN2_ERR_UNSUPPORTED, "this build supports D in {64, 128}");
   if (d->bs2 < 16) return fail(GDN2_ERR_UNSUPPORTED, "this build supports bs2 >= 16");
   if (d->seq_ld != 0 && d->seq_ld < d->L) return fail(GDN2_ERR_INVALID, "seq_ld must be 0 or >= L");
   if (d->state_ckpt < 0) return fail(GDN2_ERR_INVALID, "state_ckpt must be >= 0");
   return GDN2_OK;
+}
+
+// Calls that keep or use a residual: validate() plus the residual's own constraint.
+int validate_residual(const gdn2_desc* d) {
+  const int st = validate(d);
+  if (st) return st;
+  if (d->bt == 2 * gdn2::T && d->wy_eps > 0.0 && d->state_ckpt == 0)
+    return fail(GDN2_ERR_UNSUPPORTED, "bt == 128 with wy_eps > 0 needs state_ckpt >= 1");
+  return GDN2_OK;
+}
+
+// bt = 128 runs as pairs of 64-token half chunks (gdn2_kernels.hpp, Cfg::pair).  With
+// wy_eps > 0 the backward's state recompute needs both halves of a pair in one block, so the
+// checkpoint interval (in half chunks) is rounded up to an even number.
+bool damped_pairs(const gdn2_desc* d) { return d->bt == 2 * gdn2::T && d->wy_eps > 0.0; }
+int eff_ckpt(const gdn2_desc* d) {
+  const int k = d->state_ckpt;
+  return (damped_pairs(d) && (k & 1)) ? k + 1 : k;
 }
 
 // Pieces of the two-level block-local rescaling (fwd/scores.py:42-75): for each row block
@@ -78,10 +99,14 @@ gdn2::Cfg make_cfg(const gdn2_desc* d) {
   c.dot_mode = d->dot_mode;
   c.solve_mode = d->solve_dot_mode;
   c.b3_mode = d->b3_dot_mode;
-  c.mb = d->mb;
-  c.nc = d->L / d->bt;
+  c.mb = d->mb < gdn2::T ? d->mb : gdn2::T;    // leaves inside a 64-token (half) chunk
+  c.nc = d->L / gdn2::T;
   c.seq_ld = d->seq_ld ? d->seq_ld : d->L;
-  make_pieces(d->bt, d->score_bs, d->bs2, &c.pieces);
+  c.pair = damped_pairs(d) ? 1 : 0;
+  // the score pieces inside one 64-token (half) chunk: at bt = 128 the pieces of the 128
+  // geometry that lie inside a half are the 64 geometry's with the outer block capped at 64
+  // (the pieces crossing the halves are carried by the state, see Cfg::pair)
+  make_pieces(gdn2::T, d->score_bs < gdn2::T ? d->score_bs : gdn2::T, d->bs2, &c.pieces);
   return c;
 }
 
@@ -90,12 +115,12 @@ struct Dims {
 };
 Dims dims(const gdn2_desc* d) {
   Dims x;
-  x.nc = (size_t)(d->L / d->bt);
+  x.nc = (size_t)(d->L / gdn2::T);
   x.n_bh = (size_t)d->B * d->H;
   x.n_chunks = x.n_bh * x.nc;
   x.D = (size_t)d->D;
-  x.tD = (size_t)d->bt * d->D;
-  x.tT = (size_t)d->bt * d->bt;
+  x.tD = (size_t)gdn2::T * d->D;
+  x.tT = (size_t)gdn2::T * gdn2::T;
   x.DD = (size_t)d->D * d->D;
   return x;
 }
@@ -104,7 +129,8 @@ void residual_sizes(const gdn2_desc* d, size_t sz[GDN2_RES_COUNT]) {
   const Dims x = dims(d);
   sz[GDN2_RES_AQK] = x.n_chunks * x.tT * 4;
   sz[GDN2_RES_A] = x.n_chunks * x.tT * 4;
-  const size_t nck = d->state_ckpt > 0 ? (x.nc + d->state_ckpt - 1) / d->state_ckpt : x.nc;
+  const size_t K = (size_t)eff_ckpt(d);
+  const size_t nck = K > 0 ? (x.nc + K - 1) / K : x.nc;
   sz[GDN2_RES_HPRE] = x.n_bh * nck * x.DD * 4;
   sz[GDN2_RES_VNEW] = x.n_chunks * x.tD * 4;
   sz[GDN2_RES_WPT] = x.n_chunks * x.tD * 4;
@@ -167,7 +193,7 @@ int gdn2_abi_version(void) { return GDN2_ABI_VERSION; }
 const char* gdn2_last_error(void) { return g_err.c_str(); }
 
 int gdn2_residual_layout(const gdn2_desc* d, size_t offsets[GDN2_RES_COUNT], size_t* total_bytes) {
-  const int st = validate(d);
+  const int st = validate_residual(d);
   if (st) return st;
   if (!offsets || !total_bytes) return fail(GDN2_ERR_INVALID, "null output pointer");
   residual_offsets(d, offsets, total_bytes);
@@ -177,7 +203,7 @@ int gdn2_residual_layout(const gdn2_desc* d, size_t offsets[GDN2_RES_COUNT], siz
 // forward workspace (fragment layouts): [Wp | U^T | Kg^T], and without a residual also
 // [Qg | Aqk | gl] (with a residual those live in it).
 size_t gdn2_fwd_workspace_bytes(const gdn2_desc* d, int with_residual) {
-  if (validate(d)) return 0;
+  if (with_residual ? validate_residual(d) : validate(d)) return 0;
   const Dims x = dims(d);
   size_t n = 3 * align_up(x.n_chunks * x.tD * 4);
   if (!with_residual)
@@ -187,10 +213,12 @@ size_t gdn2_fwd_workspace_bytes(const gdn2_desc* d, int with_residual) {
 
 // backward workspace: [dv_new | dh_next | dqg | dwp | dkg | dlast | X | Y]
 size_t gdn2_bwd_workspace_bytes(const gdn2_desc* d) {
-  if (validate(d)) return 0;
+  if (validate_residual(d)) return 0;
   const Dims x = dims(d);
-  return 5 * align_up(x.n_chunks * x.tD * 4) + 2 * align_up(x.n_chunks * x.DD * 4) +
-         align_up(x.n_chunks * x.D * 4);
+  size_t n = 5 * align_up(x.n_chunks * x.tD * 4) + 2 * align_up(x.n_chunks * x.DD * 4) +
+             align_up(x.n_chunks * x.D * 4);
+  if (damped_pairs(d)) n += align_up(x.n_chunks / 2 * x.DD * 4);     // eps Wp_b^T dv_new_b per pair
+  return n;
 }
 
 }  // extern "C"
@@ -200,7 +228,7 @@ namespace {
 int fwd_impl(const gdn2_desc* d, const void* q, const void* k, const void* v, const void* w, const void* b,
              const void* g, bool bf16, const float* h0, float* o, float* h_final, void* residual,
              void* workspace, void* stream) {
-  int st = validate(d);
+  int st = residual ? validate_residual(d) : validate(d);
   if (st) return st;
   if (!q || !k || !v || !w || !b || !g || !o || !h_final || !workspace)
     return fail(GDN2_ERR_INVALID, "null tensor pointer");
@@ -248,7 +276,7 @@ int fwd_impl(const gdn2_desc* d, const void* q, const void* k, const void* v, co
   // state (the backward recomputes the others).  Training with state_ckpt = 0 keeps every
   // chunk's h_pre and v_new: the scan carries only the state and the output follows
   // chunk-parallel from them.
-  const int ck = d->state_ckpt;
+  const int ck = eff_ckpt(d);
   const bool fused_out = !residual || ck > 0;
   gdn2::ScanFwdArgs sa{wp, kgT, uT, gl, h0, qg, aqk, h_final, fused_out ? o : nullptr, hpre, vnew,
                        (int)x.nc, (int)x.n_bh, ck, cfg};
@@ -330,7 +358,7 @@ int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v,
              const float* b, const float* g, const void* residual, const float* d_o, const float* d_hf,
              float* dq, float* dk, float* dv, float* dw, float* db, float* dg, float* dh0, void* workspace,
              void* stream) {
-  int st = validate(d);
+  int st = validate_residual(d);
   if (st) return st;
   if (!q || !k || !v || !w || !b || !g || !residual || !d_o || !d_hf || !dq || !dk || !dv || !dw || !db ||
       !dg || !dh0 || !workspace)
@@ -358,20 +386,21 @@ int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v,
   float* dkg = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
   float* dlast = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.D * 4);
   float* xo = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
-  float* yo = at<float>(workspace, o2);
+  float* yo = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.DD * 4);
+  float* ez = damped_pairs(d) ? at<float>(workspace, o2) : nullptr;
 
   gdn2::BwdPreArgs pa{aqk, qg, d_o, xo, yo, (int)x.n_chunks, cfg};
   hipError_t e = timed(6, s, [&] { return gdn2::launch_bwd_pre(d->D, pa, s); });
   if (e != hipSuccess) return hip_fail(e, "bwd_pre launch");
 
-  gdn2::ScanBwdArgs sa{wpT, kg, gl, xo, yo, d_hf, dvn, dhn, dh0, (int)x.nc, (int)x.n_bh, cfg};
+  gdn2::ScanBwdArgs sa{wpT, kg, gl, xo, yo, d_hf, dvn, dhn, dh0, ez, (int)x.nc, (int)x.n_bh, cfg};
   e = timed(2, s, [&] { return gdn2::launch_scan_bwd(d->D, sa, s); });
   if (e != hipSuccess) return hip_fail(e, "scan_bwd launch");
 
   if (d->state_ckpt > 0) {
     // the states entering the chunks are recomputed from the checkpoints inside the reductions
-    gdn2::BwdStateRcArgs ba{d_o, dvn, vnew, hpre, dhn, kg, gl, dqg, dwp, dkg, dlast,
-                            (int)x.nc, (int)x.n_bh, d->state_ckpt, cfg};
+    gdn2::BwdStateRcArgs ba{d_o, dvn, vnew, hpre, dhn, kg, gl, ez, dqg, dwp, dkg, dlast,
+                            (int)x.nc, (int)x.n_bh, eff_ckpt(d), cfg};
     e = timed(7, s, [&] { return gdn2::launch_bwd_state_rc(d->D, ba, s); });
     if (e != hipSuccess) return hip_fail(e, "bwd_state_rc launch");
   } else {
@@ -392,6 +421,8 @@ int gdn2_wy_stage(const gdn2_desc* d, const float* q, const float* k, const floa
                   float* kg, float* qg, float* gl, void* stream) {
   int st = validate(d);
   if (st) return st;
+  if (d->bt != gdn2::T)
+    return fail(GDN2_ERR_UNSUPPORTED, "gdn2_wy_stage reports chunks of 64 tokens: use bt == 64");
   if (!q || !k || !v || !w || !b || !g || !aqk || !wp || !u || !kg || !qg || !gl)
     return fail(GDN2_ERR_INVALID, "null tensor pointer");
   const Dims x = dims(d);

@@ -177,8 +177,12 @@ __global__ __launch_bounds__(NWW * WAVE) __attribute__((amdgpu_waves_per_eu(2)))
   static_assert(NKT % NWW == 0 && NKB % 2 == 0, "key tile groups, value block parity");
   __shared__ float4 sA[2 * SLAB];                // [buf][mat * 4 + tile][lane]
   __shared__ __attribute__((aligned(16))) float sTr[NWW * 16 * TRP];
+  // Cfg::pair: the damped state of a pair's second half (its dWp uses it), [wave][kb][lane],
+  // stored while stepping through the first half (K is even: a block holds whole pairs)
+  __shared__ float4 sHd[NWW * NKB * WAVE];
   const Cfg& cf = a.cfg;
   const int K = a.ckpt, nc = a.nc, nblk = (nc + K - 1) / K;
+  const bool damp = cf.pair != 0;
   const int lin = xcd_remap(gridDim.x);
   const int grp = lin % NG, blk = (lin / NG) % nblk, bh = lin / (NG * nblk);
   const int c0 = blk * K, c1 = min(nc, c0 + K);
@@ -213,6 +217,12 @@ __global__ __launch_bounds__(NWW * WAVE) __attribute__((amdgpu_waves_per_eu(2)))
     base[(12 + w) * WAVE + l] = src[2];
   };
   auto dh_at = [&](int c, int kb) { return ld4(sbase(a.dh_next_f + chunk_idx(c) * D * D + frag_blk(kt, kb, D)) + lo4); };
+  // eps Wp_b^T dv_new_b of the pair chunk c belongs to (scan_bwd), added to dh_next in the first
+  // half's dKg; zero where unused
+  auto ez_at = [&](int c, int kb) {
+    if (!damp || (c & 1)) return make_float4(0.f, 0.f, 0.f, 0.f);
+    return ld4(sbase(a.ez_f + ((size_t)bh * (nc / 2) + c / 2) * D * D + frag_blk(kt, kb, D)) + lo4);
+  };
 
   f4 h[NKB];
   {
@@ -223,17 +233,20 @@ __global__ __launch_bounds__(NWW * WAVE) __attribute__((amdgpu_waves_per_eu(2)))
       h[kb] = f4{x.x, x.y, x.z, x.w};
     }
   }
-  float4 st[2][NST], dhb[2];
+  float4 st[2][NST], dhb[2], ezb[2];
   fetch(c0, 0, st[0]);
   dhb[0] = dh_at(c0, 0);
+  ezb[0] = ez_at(c0, 0);
   fetch(c0, 1, st[1]);
   dhb[1] = dh_at(c0, 1);
+  ezb[1] = ez_at(c0, 1);
   put(0, st[0]);
   __syncthreads();
 
   for (int c = c0; c < c1; ++c) {
     const size_t ch = chunk_idx(c), tb = ch * T * D;
     const bool step = c + 1 < c1;
+    const bool second = damp && (c & 1);            // a pair's second half: dWp from h_d
     float4 kga[4] = {}, gm = make_float4(0.f, 0.f, 0.f, 0.f);
     if (step) {
       // Kg^T block (kt, u) in the A-operand layout = FA(Kg) block (u, kt) transposed
@@ -251,13 +264,16 @@ __global__ __launch_bounds__(NWW * WAVE) __attribute__((amdgpu_waves_per_eu(2)))
     for (int kb = 0; kb < NKB; ++kb) {
       const int pb = kb & 1;
       const float4 hp = wave_transpose16(tr, f4_to_float4(h[kb]), r, g);
+      const float4 hpw = second ? wave_transpose16(tr, sHd[(w * NKB + kb) * WAVE + l], r, g) : hp;
       const float4 dhc = dhb[pb];
+      const float4 dhk = add4(dhc, ezb[pb]);
       {
         // two value blocks ahead, across the chunk boundary
         const int kn = kb + 2 < NKB ? kb + 2 : kb + 2 - NKB, cn = kb + 2 < NKB ? c : c + 1;
         if (cn < c1) {
           fetch(cn, kn, st[pb]);
           dhb[pb] = dh_at(cn, kn);
+          ezb[pb] = ez_at(cn, kn);
         }
       }
       const float4* cur = sA + pb * SLAB;
@@ -273,8 +289,8 @@ __global__ __launch_bounds__(NWW * WAVE) __attribute__((amdgpu_waves_per_eu(2)))
           n2 = cur[(9 + ti) * WAVE + l];
         }
         mma16<B3>(acc[0][ti], o0, hp);
-        mma16<B3>(acc[1][ti], o1, hp);
-        mma16<B3>(acc[2][ti], o2, dhc);
+        mma16<B3>(acc[1][ti], o1, hpw);
+        mma16<B3>(acc[2][ti], o2, dhk);
         __builtin_amdgcn_sched_barrier(0);
         o0 = n0;
         o1 = n1;
@@ -290,6 +306,13 @@ __global__ __launch_bounds__(NWW * WAVE) __attribute__((amdgpu_waves_per_eu(2)))
         for (int u = 0; u < 4; ++u) mma16<DOT>(hn, kga[u], cur[(12 + u) * WAVE + l]);
         drain(hn);
         const float gmv[4] = {gm.x, gm.y, gm.z, gm.w};
+        if (damp && !(c & 1)) {
+          // the forward scan's damped state (gdn2_scan.hip), bit for bit
+          const float ome = cf.ome;
+          sHd[(w * NKB + kb) * WAVE + l] =
+              make_float4(state_update(h[kb][0], gmv[0], ome * hn[0], clip), state_update(h[kb][1], gmv[1], ome * hn[1], clip),
+                          state_update(h[kb][2], gmv[2], ome * hn[2], clip), state_update(h[kb][3], gmv[3], ome * hn[3], clip));
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) h[kb][e] = state_update(h[kb][e], gmv[e], hn[e], clip);
       }

@@ -24,6 +24,17 @@ struct Cfg {
   int diag, dot_mode, solve_mode, b3_mode, mb;
   int nc;        // chunks per (batch, head) sequence of this segment
   int seq_ld;    // tokens between consecutive (batch, head) sequences of the raw operator tensors
+  // pair = 1: the operator's chunk is bt = 128 with wy_eps > 0, run as pairs of 64-token half
+  // chunks (a = chunks 2m, b = 2m + 1).  The WY inverse of the 128 chunk is block lower
+  // triangular; its diagonal blocks are the halves' own inverses (I + (1-eps) Akk_hh)^-1 and
+  // its off-diagonal block A_ba = -A_bb (1-eps) Akk_ba A_aa.  Expanding v_new = A (wv - X h)
+  // with it, the first half is the 64-chunk form, and the second half is the 64-chunk form
+  // from the damped state h_d = e^gamma_a h + (1-eps) Kg_a^T v_new_a instead of the state
+  // h_mid = e^gamma_a h + Kg_a^T v_new_a entering it: the cross-half scores (Aqk_ba, Akk_ba)
+  // are carried by the state, exactly, and only the erase term sees the damping.  The output
+  // and the state update use h_mid.  With wy_eps = 0 (pair = 0) bt = 128 and bt = 64 are the
+  // same operator.
+  int pair;
   PieceList pieces;
 };
 
@@ -83,9 +94,12 @@ struct BwdPreArgs {
 
 // Reverse state scan: reads FA(Wp^T), FA(Kg), gl, X, Y; writes dv_new as FA(dv_new) (T x D),
 // dh_next as FA(dh_next) (D x D), dh0 row-major.
+// With Cfg::pair the cotangent of the damped state of each pair's second half reaches the
+// first half's Kg v_new term as eps Wp_b^T dv_new_b: added to dh there, and written per pair as
+// FA(ez) (D x D, the dh_next layout) for bwd_state_rc's dKg.
 struct ScanBwdArgs {
   const float *wpT_f, *kg_f, *gl, *x_f, *y_f, *dhf;
-  float *dv_new_f, *dh_next_f, *dh0;
+  float *dv_new_f, *dh_next_f, *dh0, *ez_f;
   int nc, n_bh;
   Cfg cfg;
 };
@@ -106,7 +120,7 @@ struct BwdStateArgs {
 // stored FA(v_new^T) -- the forward scan's own update, bit for bit -- and each chunk's
 // reductions use it as h_pre.  Outputs as BwdStateArgs.
 struct BwdStateRcArgs {
-  const float *dout, *dv_new_f, *v_new_f, *hck_f, *dh_next_f, *kg_f, *gl;
+  const float *dout, *dv_new_f, *v_new_f, *hck_f, *dh_next_f, *kg_f, *gl, *ez_f;
   float *dqg, *dwp, *dkg, *dlast;
   int nc, n_bh, ckpt;
   Cfg cfg;

@@ -68,8 +68,11 @@ struct FwdOps {
 // ROLE < 0: V wave (v_new tile w); ROLE = j >= 0: O wave of output tile j (wave 4 + j).
 // OUT = false: no output (the O waves keep only their state rows and the barriers; the
 // output is then computed chunk-parallel from h_pre and v_new, gdn2_fwd.hip).
+// With Cfg::pair (bt = 128, wy_eps > 0) the state rows also go to sHd after each pair's first
+// half as the damped state h_d = state_update(h, gamma, (1 - eps) Kg^T v_new), from which the
+// V waves compute the second half's v_new (the O waves and the state update keep h).
 template <int D, int MODE, bool OUT, int ROLE>
-__device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, float4* sV) {
+__device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, float4* sHd, float4* sV) {
   constexpr int NH = D / 16, NVB = D / 16;
   constexpr bool V = ROLE < 0, O = !V && OUT;
   constexpr int J = V ? 0 : ROLE;
@@ -110,7 +113,11 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
     }
   };
 
-  auto step = [&](const FwdOps<NH>& op, int c, FwdOps<NH>& nx, int cn) {
+  const bool damp = a.cfg.pair != 0;
+  const float ome = a.cfg.ome;
+  // ODD: c is odd (the loop below is unrolled by two from c = 0), i.e. a pair's second half
+  auto step = [&](const FwdOps<NH>& op, int c, FwdOps<NH>& nx, int cn, auto odd) {
+    constexpr bool ODD = decltype(odd)::value;
     const size_t ch = (size_t)bh * nc + c, tb = ch * T * D;
     const size_t tbn = base(cn) * T * D, sbn = base(cn) * T * T;
     if (OWNS && a.h_pre_f && (a.ckpt <= 1 || c % a.ckpt == 0)) {
@@ -120,8 +127,9 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
     // ---- window A ----
     float4 hb[NH];
     if constexpr (V || O) {
+      const float4* src = (V && ODD && damp) ? sHd : sH;
 #pragma unroll
-      for (int kb = 0; kb < NH; ++kb) hb[kb] = sH[kb * WAVE + l];
+      for (int kb = 0; kb < NH; ++kb) hb[kb] = src[kb * WAVE + l];
     }
     f4 acc = {0.f, 0.f, 0.f, 0.f};
     if constexpr (V) {
@@ -156,6 +164,14 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
       }
       drain(hn);
       const float gmv[4] = {op.gm.x, op.gm.y, op.gm.z, op.gm.w};
+      if (!ODD && damp) {
+        float4 hd;
+        hd.x = state_update(h[0], gmv[0], ome * hn[0], clip);
+        hd.y = state_update(h[1], gmv[1], ome * hn[1], clip);
+        hd.z = state_update(h[2], gmv[2], ome * hn[2], clip);
+        hd.w = state_update(h[3], gmv[3], ome * hn[3], clip);
+        sHd[w * WAVE + l] = hd;       // read in the next step's window A, after its barrier
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) h[e] = state_update(h[e], gmv[e], hn[e], clip);
       nx.gm = ld4(a.gl + base(cn) * D + 16 * w + 4 * g);
@@ -194,10 +210,10 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
   __syncthreads();
   int c = 0;
   for (; c + 1 < nc; c += 2) {
-    step(A, c, B, c + 1);
-    step(B, c + 1, A, c + 2);
+    step(A, c, B, c + 1, std::false_type{});
+    step(B, c + 1, A, c + 2, std::true_type{});
   }
-  if (c < nc) step(A, c, B, c + 1);
+  if (c < nc) step(A, c, B, c + 1, std::false_type{});
   if (OWNS) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) a.hf[(size_t)bh * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r] = h[e];
@@ -208,13 +224,14 @@ template <int D, int MODE, bool OUT>
 __global__ __launch_bounds__(8 * WAVE) void scan_fwd_kernel(ScanFwdArgs a) {
   constexpr int NH = D / 16;
   __shared__ float4 sH[NH * WAVE];     // h_pre of the current chunk, [key tile][lane]
+  __shared__ float4 sHd[NH * WAVE];    // the damped state of a pair's second half (Cfg::pair)
   __shared__ float4 sV[4 * WAVE];      // v_new tiles, [token tile][lane]
   switch (wave_id()) {
-    case 4: scan_fwd_role<D, MODE, OUT, 0>(a, sH, sV); break;
-    case 5: scan_fwd_role<D, MODE, OUT, 1>(a, sH, sV); break;
-    case 6: scan_fwd_role<D, MODE, OUT, 2>(a, sH, sV); break;
-    case 7: scan_fwd_role<D, MODE, OUT, 3>(a, sH, sV); break;
-    default: scan_fwd_role<D, MODE, OUT, -1>(a, sH, sV); break;
+    case 4: scan_fwd_role<D, MODE, OUT, 0>(a, sH, sHd, sV); break;
+    case 5: scan_fwd_role<D, MODE, OUT, 1>(a, sH, sHd, sV); break;
+    case 6: scan_fwd_role<D, MODE, OUT, 2>(a, sH, sHd, sV); break;
+    case 7: scan_fwd_role<D, MODE, OUT, 3>(a, sH, sHd, sV); break;
+    default: scan_fwd_role<D, MODE, OUT, -1>(a, sH, sHd, sV); break;
   }
 }
 
@@ -270,21 +287,35 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
     op.gm = ld4(a.gl + ch * D + 16 * w + 4 * g);
   };
 
-  auto step = [&](const BwdOps& op, int s, BwdOps& nx, int sn) {
+  // Cfg::pair: steps alternate between a pair's second half (s even, chunk nc - 1 - s odd) and
+  // its first half (s odd).  The second half's eps Wp^T dv_new (the cotangent its damped
+  // state passes to the first half's Kg^T v_new, beyond the state's own) is added to dh in the
+  // first half's Kg dh term and written out for bwd_state_rc; the carry itself is unchanged.
+  const bool damp = a.cfg.pair != 0;
+  const float eps = a.cfg.wy_eps;
+  float4 ez = make_float4(0.f, 0.f, 0.f, 0.f);
+  auto step = [&](const BwdOps& op, int s, BwdOps& nx, int sn, auto sodd) {
+    constexpr bool FIRST_HALF = decltype(sodd)::value;
     const size_t ch = chunk(s), tb = ch * T * D;
     const size_t chn = chunk(sn), tbn = chn * T * D;
     const float4 db = f4_to_float4(dh);
+    const float4 dbk = (FIRST_HALF && damp) ? add4(db, ez) : db;
     f4 p[4];
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) {
       p[ti] = f4{0.f, 0.f, 0.f, 0.f};
-      mma16<MODE>(p[ti], op.kg[ti], db);
+      mma16<MODE>(p[ti], op.kg[ti], dbk);
       GDN2_SCHED_FENCE();
       nx.kg[ti] = ld4(a.kg_f + tbn + frag_blk(ti, w, D) + 4 * l);
       GDN2_SCHED_FENCE();
     }
     // dh entering this chunk's step (mega.py:35) as FA(dh_next) block (w, slice)
     const float4 dhv = wave_transpose16(sTr + w * 16 * TRP, db, r, g);
+    if (FIRST_HALF && damp) {
+      const size_t c = ch - (size_t)bh * nc;
+      stg4(a.ez_f + ((size_t)bh * (nc / 2) + c / 2) * D * D + frag_blk(w, vb, D) + 4 * l,
+           wave_transpose16(sTr + w * 16 * TRP, ez, r, g));
+    }
     drain(p[0], p[1], p[2], p[3]);
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) sP[(w * 4 + ti) * WAVE + l] = f4_to_float4(p[ti]);
@@ -315,6 +346,7 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
     float4 dvv = db;
     if (red) dvv = frag_transpose_lds(sDB, tp, lp);     // FA(dv_new) block (tp, slice)
     drain(z);
+    if (!FIRST_HALF && damp) ez = scale4(f4_to_float4(z), eps);
     const float gmv[4] = {op.gm.x, op.gm.y, op.gm.z, op.gm.w};
     const float yv[4] = {op.yy.x, op.yy.y, op.yy.z, op.yy.w};
 #pragma unroll
@@ -328,10 +360,10 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
   load_all(A, 0);
   int s = 0;
   for (; s + 1 < nc; s += 2) {
-    step(A, s, B, s + 1);
-    step(B, s + 1, A, s + 2);
+    step(A, s, B, s + 1, std::false_type{});
+    step(B, s + 1, A, s + 2, std::true_type{});
   }
-  if (s < nc) step(A, s, B, s + 1);
+  if (s < nc) step(A, s, B, s + 1, std::false_type{});
 #pragma unroll
   for (int e = 0; e < 4; ++e) a.dh0[(size_t)bh * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r] = dh[e];
 }

@@ -1,0 +1,115 @@
+"""bt = 128 (the reference's default and PROD chunk) against the float64 oracle run at bt = 128.
+
+The kernels run a 128-token chunk as two 64-token halves; with wy_eps > 0 the second half
+erases from the damped state e^gamma_a h + (1 - eps) Kg_a^T v_new_a (gdn2_kernels.hpp,
+Cfg::pair), which is the block form of the 128 chunk's WY inverse.  The oracle computes the
+128 chunk directly (its own two-level scores, ladder inverse over 128 rows, scan), so these
+tests pin that algebra (measured ~4e-7 rel-L2); as a control, the chunk-64 operator with the
+same eps = 0.05 differs from the bt = 128 oracle by more than twice the gate (~5e-3).
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import mk_inputs, rel_l2
+from test_gpu_parity import GATE, NAMES, banner, base_cfg, compare, oracle_grad, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm GPU")
+
+
+def cfg128(**kw):
+    d = dict(bt=128, bc=64, score_bs=128, bs2=32, mb=8)
+    d.update(kw)
+    return base_cfg(**d)
+
+
+def grad(cfg, scale, arrs, h0, ckpt=None, dtype=torch.float32):
+    from atomic_gdn2 import make_blr_trainable
+    xs = [t.requires_grad_(True) for t in to_dev(arrs, dtype)]
+    h0t = torch.from_numpy(h0).cuda().requires_grad_(True)
+    o, hf = make_blr_trainable(cfg, scale, state_ckpt=ckpt)(*xs, h0t)
+    gr = torch.autograd.grad((o * o).sum() + (hf * hf).sum(), xs + [h0t])
+    torch.cuda.synchronize()
+    out = dict(o=o.detach(), h_final=hf.detach())
+    out.update(zip(NAMES + ("dh0",), gr))
+    return out
+
+
+CASES = [
+    dict(wy_eps=1e-3),                                   # the PROD geometry's damping
+    dict(wy_eps=0.05, bs2=64),                           # strong damping, whole-half BTL blocks
+    dict(wy_eps=0.05, score_bs=64, mb=16),
+    dict(wy_eps=0.0, bs2=64),                            # the reference's published speed profile
+    dict(wy_eps=0.02, score_bs=32, bs2=16, mb=4),
+    dict(wy_eps=0.05, diag="lean"),
+]
+
+
+@pytest.mark.parametrize("kw", CASES, ids=lambda kw: ",".join(f"{k}={v}" for k, v in kw.items()))
+@pytest.mark.parametrize("D", [64, 128])
+def test_bt128_matches_oracle(kw, D):
+    banner(f"bt=128 vs oracle {kw} D={D}")
+    cfg = cfg128(**kw)
+    scale = D ** -0.5
+    arrs = mk_inputs(1, 384, 2, D, 31, g=0.05, layout="bhld")       # three 128-token chunks
+    h0 = (np.random.default_rng(32).normal(size=(1, 2, D, D)) * 0.1).astype(np.float32)
+    hip = grad(cfg, scale, arrs, h0)
+    ref = oracle_grad(cfg, scale, arrs, h0)
+    errs = compare(hip, ref, GATE, names=("o", "h_final") + NAMES + ("dh0",))
+    banner(f"bt=128 max rel-L2 {max(errs.values()):.2e}")
+
+
+def test_damping_makes_bt128_a_different_operator():
+    """Control for the test above: with eps = 0.05 the chunk-64 operator is not the bt = 128
+    one, beyond the parity gate, so matching the bt = 128 oracle is not automatic."""
+    banner("bt=64 vs bt=128 operators under eps = 0.05")
+    scale = 128 ** -0.5
+    arrs = mk_inputs(1, 256, 1, 128, 33, g=0.05, layout="bhld")
+    h0 = np.zeros((1, 1, 128, 128), np.float32)
+    r128 = oracle_grad(cfg128(wy_eps=0.05), scale, arrs, h0)
+    hip64 = grad(base_cfg(wy_eps=0.05), scale, arrs, h0)
+    assert max(rel_l2(hip64[n], r128[n]) for n in ("o",) + NAMES) > 2 * GATE
+
+
+def test_prod_defaults_run_and_match_oracle():
+    """make_cfg() as the reference ships it (bt 128, score_bs 128, bs2 32, mb 8, wy_eps 1e-3,
+    solve / backward products bf16x3) runs and matches the oracle."""
+    from atomic_gdn2 import make_cfg
+    banner("PROD defaults")
+    cfg = make_cfg()
+    assert cfg.bt == 128 and cfg.wy_eps == 1e-3
+    scale = 128 ** -0.5
+    arrs = mk_inputs(2, 256, 2, 128, 34, g=0.05, layout="bhld")
+    h0 = (np.random.default_rng(35).normal(size=(2, 2, 128, 128)) * 0.1).astype(np.float32)
+    hip = grad(cfg, scale, arrs, h0)
+    compare(hip, oracle_grad(cfg, scale, arrs, h0), GATE, names=("o", "h_final") + NAMES + ("dh0",))
+
+
+def test_bt128_checkpoints_segments_and_forward_only():
+    """Every checkpoint interval gives the same bits (odd ones are rounded up to whole pairs);
+    keeping every chunk's state is rejected with wy_eps > 0; four 128-chunks as two segments
+    match the oracle; the no-grad forward equals the training forward bit for bit."""
+    from atomic_gdn2 import make_blr_trainable
+    banner("bt=128 checkpoints / segments / forward-only")
+    cfg = cfg128(wy_eps=0.03, max_chunks_per_call=2)
+    scale = 128 ** -0.5
+    arrs = mk_inputs(1, 512, 2, 128, 36, g=0.05, layout="bhld")
+    h0 = (np.random.default_rng(37).normal(size=(1, 2, 128, 128)) * 0.1).astype(np.float32)
+    ref = grad(cfg, scale, arrs, h0, ckpt=2)
+    for ck in (1, 3, 4, 8):
+        got = grad(cfg, scale, arrs, h0, ckpt=ck)
+        for n in ref:
+            assert torch.equal(got[n], ref[n]), (ck, n)
+    with pytest.raises(ValueError, match="state_ckpt"):
+        grad(cfg, scale, arrs, h0, ckpt=0)
+    compare(ref, oracle_grad(cfg, scale, arrs, h0), GATE, names=("o", "h_final") + NAMES + ("dh0",))
+    with torch.no_grad():
+        o, hf = make_blr_trainable(cfg, scale)(*to_dev(arrs), torch.from_numpy(h0).cuda())
+    torch.cuda.synchronize()
+    assert torch.equal(o, ref["o"]) and torch.equal(hf, ref["h_final"])

@@ -90,9 +90,10 @@ def test_legacy_entry_points_match_oracle():
     xs = [x.clone().requires_grad_(True) for x in dev]
     o2, hf2 = atomic_ops.gdn2_forward_trainable(*xs, scale, config=KAGGLE_SMALL)
     ((o2 * o2).sum() + (hf2 * hf2).sum()).backward()
-    # the reference's off-TPU operator for this preset: chunk config.bt = 128, wy_eps = 0
+    # the preset's own operator: chunk config.bt = 128 with its wy_eps (the kernels run bt = 128)
     ref = grad_ref(q, k, v, w, b, g, scale, None,
-                   OracleCfg(bt=KAGGLE_SMALL.bt, score_bs=KAGGLE_SMALL.bt, bs2=32, mb=KAGGLE_SMALL.mb, wy_eps=0.0))
+                   OracleCfg(bt=KAGGLE_SMALL.bt, score_bs=KAGGLE_SMALL.bt, bs2=32, mb=KAGGLE_SMALL.mb,
+                             wy_eps=KAGGLE_SMALL.wy_eps))
     for x, n in zip(xs, ("dq", "dk", "dv", "dw", "db", "dg")):
         assert rel_l2(x.grad, sw(ref[n])) < 2e-3, n
 
@@ -114,11 +115,13 @@ def test_legacy_pallas_shapes():
 
 
 def test_operator_cfg_follows_the_reference_dispatch():
-    """Presets whose chunk the kernels do not run get the reference's off-TPU operator
-    (wy_eps = 0, any chunk size); a supported chunk keeps its own wy_eps."""
+    """Presets whose chunk the kernels do not run (bt = 256) get the reference's off-TPU
+    operator (wy_eps = 0, any chunk size); a supported chunk (64, 128) keeps its own wy_eps."""
     from atomic_ops.fallback import operator_cfg
-    for preset in (KAGGLE_SMALL, KAGGLE_LARGE):
+    for preset in (KAGGLE_MEDIUM, KAGGLE_LARGE):
         c = operator_cfg(preset)
-        assert c.wy_eps == 0.0 and c.clip == preset.clip
+        assert c.wy_eps == 0.0 and c.clip == preset.clip and c.bt == 64
+    c = operator_cfg(KAGGLE_SMALL)
+    assert c.bt == 128 and c.wy_eps == KAGGLE_SMALL.wy_eps and c.mb == KAGGLE_SMALL.mb
     c = operator_cfg(KernelConfig(bt=64, bc=32, mb=8, clip=1e4, wy_eps=1e-3))
     assert c.bt == 64 and c.wy_eps == 1e-3 and c.mb == 8
