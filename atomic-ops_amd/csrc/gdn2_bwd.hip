@@ -301,9 +301,9 @@ __global__ __launch_bounds__(NWW * WAVE) __attribute__((amdgpu_waves_per_eu(2)))
       part = fmaf(dhc.z, hp.z, part);
       part = fmaf(dhc.w, hp.w, part);
       if (step) {
+        // the forward scan's Kg^T v_new chain (gdn2_scan.hip), the same MFMAs in the same order
         f4 hn = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int u = 0; u < 4; ++u) mma16<DOT>(hn, kga[u], cur[(12 + u) * WAVE + l]);
+        mma_chain<DOT, 4>(hn, 0, [&](int u) { return kga[u]; }, [&](int u) { return cur[(12 + u) * WAVE + l]; });
         drain(hn);
         const float gmv[4] = {gm.x, gm.y, gm.z, gm.w};
         if (damp && !(c & 1)) {
@@ -489,13 +489,16 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     const float* ar = sX2 + (16 * ti + r) * LD + 4 * g;
     const float* br = sX1 + (16 * tj + r) * LD + 4 * g;
     f4 acc = {0.f, 0.f, 0.f, 0.f};
+    constexpr int KSTEP = B3 == DOT_HIGHEST ? 1 : 2;      // bf16: two k blocks per MFMA
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
-      mma16<B3>(acc, ld4(ar + 16 * kb), ld4(br + 16 * kb));
+    for (int kb = 0; kb < NKB; kb += KSTEP) {
+      if constexpr (KSTEP == 1) mma16<B3>(acc, ld4(ar + 16 * kb), ld4(br + 16 * kb));
+      else mma32<B3>(acc, ld4(ar + 16 * kb), ld4(br + 16 * kb), ld4(ar + 16 * kb + 16), ld4(br + 16 * kb + 16));
       __builtin_amdgcn_sched_barrier(0);
-      const int sl = m2 * NKB + kb;
 #pragma unroll
-      for (int item = NITEMS * sl / NSLOT; item < NITEMS * (sl + 1) / NSLOT; ++item) prefetch(item);
+      for (int sl = m2 * NKB + kb; sl < m2 * NKB + kb + KSTEP; ++sl)
+#pragma unroll
+        for (int item = NITEMS * sl / NSLOT; item < NITEMS * (sl + 1) / NSLOT; ++item) prefetch(item);
       __builtin_amdgcn_sched_barrier(0);
     }
     drain(acc);
@@ -530,8 +533,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     const float* ar = sX2 + (16 * ti + r) * LD + 4 * g;
     const float* br = sX1 + (16 * tj + r) * LD + 4 * g;
     accA[m2] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) mma16<B3>(accA[m2], ld4(ar + 16 * kb), ld4(br + 16 * kb));
+    mma_chain<B3, NKB>(accA[m2], 0, [&](int kb) { return ld4(ar + 16 * kb); }, [&](int kb) { return ld4(br + 16 * kb); });
     drain(accA[m2]);
   }
   __syncthreads();
@@ -548,8 +550,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     const float* ar = sX2 + (16 * ti + r) * LD + 4 * g;
     const float* br = sX1 + (16 * tj + r) * LD + 4 * g;
     f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) mma16<B3>(acc, ld4(ar + 16 * kb), ld4(br + 16 * kb));
+    mma_chain<B3, NKB>(acc, 0, [&](int kb) { return ld4(ar + 16 * kb); }, [&](int kb) { return ld4(br + 16 * kb); });
     drain(acc);
 #pragma unroll
     for (int e = 0; e < 4; ++e)
@@ -568,9 +569,8 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   for (int t = wv; t < 16; t += NW) {
     const int ti = t >> 2, tj = t & 3;
     f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-      mma16<B3>(acc, ld4(sDA + (16 * ti + r) * LT + 16 * kb + 4 * g), ld4(sA + (16 * tj + r) * LT + 16 * kb + 4 * g));
+    mma_chain<B3, 4>(acc, 0, [&](int kb) { return ld4(sDA + (16 * ti + r) * LT + 16 * kb + 4 * g); },
+                     [&](int kb) { return ld4(sA + (16 * tj + r) * LT + 16 * kb + 4 * g); });
     drain(acc);
 #pragma unroll
     for (int e = 0; e < 4; ++e) sTmp[(16 * ti + 4 * g + e) * LT + 16 * tj + r] = sanitize(acc[e], clip);
@@ -584,13 +584,16 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     if (tj <= ti) {
       // full k range as one straight-line chain (the blocks kb < ti of A^T are exact zeros)
       f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        const float* ac = sA + (16 * kb + 4 * g) * LT + 16 * ti + r;
-        const float* tc = sTmp + (16 * kb + 4 * g) * LT + 16 * tj + r;
-        mma16<B3>(acc, make_float4(ac[0], ac[LT], ac[2 * LT], ac[3 * LT]),
-                  make_float4(tc[0], tc[LT], tc[2 * LT], tc[3 * LT]));
-      }
+      mma_chain<B3, 4>(
+          acc, 0,
+          [&](int kb) {
+            const float* ac = sA + (16 * kb + 4 * g) * LT + 16 * ti + r;
+            return make_float4(ac[0], ac[LT], ac[2 * LT], ac[3 * LT]);
+          },
+          [&](int kb) {
+            const float* tc = sTmp + (16 * kb + 4 * g) * LT + 16 * tj + r;
+            return make_float4(tc[0], tc[LT], tc[2 * LT], tc[3 * LT]);
+          });
       drain(acc);
 #pragma unroll
       for (int e = 0; e < 4; ++e)
@@ -804,13 +807,24 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     f4 dkb = {0.f, 0.f, 0.f, 0.f}, dwv = {0.f, 0.f, 0.f, 0.f};
     // straight-line MFMA chain: skip the zero k blocks only where rt is a compile-time value
     constexpr bool RT_STATIC = St::NS == NW;          // rt == m for every wave
-#pragma unroll
-    for (int kb = RT_STATIC ? m : 0; kb < 4; ++kb) {
+    auto acol = [&](int kb) {
       const float* ac = sA + (16 * kb + 4 * g) * LT + 16 * rt + r;
-      const float4 av = make_float4(ac[0], ac[LT], ac[2 * LT], ac[3 * LT]);
+      return make_float4(ac[0], ac[LT], ac[2 * LT], ac[3 * LT]);
+    };
+    auto pcol = [&](int kb) {
       const float* pv = sX2 + (16 * kb + 4 * g) * LD + dcol;
-      mma16<B3>(dkb, av, dwpc[kb]);
-      mma16<B3>(dwv, av, make_float4(pv[0], pv[LD], pv[2 * LD], pv[3 * LD]));
+      return make_float4(pv[0], pv[LD], pv[2 * LD], pv[3 * LD]);
+    };
+    if constexpr (B3 == DOT_HIGHEST) {
+#pragma unroll
+      for (int kb = RT_STATIC ? m : 0; kb < 4; ++kb) {
+        const float4 av = acol(kb);
+        mma16<B3>(dkb, av, dwpc[kb]);
+        mma16<B3>(dwv, av, pcol(kb));
+      }
+    } else {
+      mma_chain<B3, 4>(dkb, RT_STATIC ? m : 0, acol, [&](int kb) { return dwpc[kb]; });
+      mma_chain<B3, 4>(dwv, RT_STATIC ? m : 0, acol, pcol);
     }
     drain(dkb, dwv);
     const float4 q4 = pick4(qv, rt), k4 = pick4(kv, rt), b4 = pick4(bv, rt);
@@ -949,14 +963,12 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdPreArgs a) {
       bs[u] = scale4(bo[u], scale);
     }
     f4 accx = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int u = 0; u < 4; ++u) mma16<B3>(accx, ax[u], bo[u]);
+    mma_chain<B3, 4>(accx, 0, [&](int u) { return ax[u]; }, [&](int u) { return bo[u]; });
     f4 accy[NYW];
 #pragma unroll
     for (int m = 0; m < NYW; ++m) {
       accy[m] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int u = 0; u < 4; ++u) mma16<B3>(accy[m], ay[m][u], bs[u]);
+      mma_chain<B3, 4>(accy[m], 0, [&](int u) { return ay[m][u]; }, [&](int u) { return bs[u]; });
     }
     drain(accx);
     stg4(a.x_f + tb + frag_blk(vb, w, T) + 4 * l, f4_to_float4(accx));

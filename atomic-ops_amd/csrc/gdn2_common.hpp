@@ -125,6 +125,21 @@ __device__ __forceinline__ void mfma_bf16x3(f4& acc, const s4& ah, const s4& al,
       : "+v"(acc)
       : "v"(ah), "v"(al), "v"(bh), "v"(bl));
 }
+// gfx950's 32-deep bf16 MFMA: lane l supplies 8 k values of A's row l % 16 and of B's column
+// l % 16 (group l / 16); the pairing of A's and B's values is all that matters to the sum.
+typedef short s8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ void mfma_bf16x1_k32(f4& acc, const s8& a, const s8& b) {
+  asm volatile("s_nop 1\n\tv_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma_bf16x3_k32(f4& acc, const s8& ah, const s8& al, const s8& bh, const s8& bl) {
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_mfma_f32_16x16x32_bf16 %0, %1, %3, %0\n\t"
+      "v_mfma_f32_16x16x32_bf16 %0, %1, %4, %0\n\t"
+      "v_mfma_f32_16x16x32_bf16 %0, %2, %3, %0"
+      : "+v"(acc)
+      : "v"(ah), "v"(al), "v"(bh), "v"(bl));
+}
 __device__ __forceinline__ void drain(f4& a) {
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(a));
 }
@@ -160,24 +175,7 @@ __device__ __forceinline__ s4 round4(const float4& x) {
 }
 
 template <bool THREE>
-__device__ __forceinline__ void mma_tile_bf16(f4& acc, const View& A, const View& B, int K) {
-  const int l = lane_id(), r = l & 15, g = l >> 4;
-  for (int k0 = 0; k0 < K; k0 += 16) {
-    const int kk = k0 + 4 * g;
-    const float4 a = make_float4(A.at(r, kk), A.at(r, kk + 1), A.at(r, kk + 2), A.at(r, kk + 3));
-    const float4 b = make_float4(B.at(kk, r), B.at(kk + 1, r), B.at(kk + 2, r), B.at(kk + 3, r));
-    s4 ah, bh, al, bl;
-    if (THREE) {
-      split4(a, ah, al);
-      split4(b, bh, bl);
-    } else {
-      ah = round4(a);
-      bh = round4(b);
-    }
-    if (THREE) mfma_bf16x3(acc, ah, al, bh, bl);
-    else mfma_bf16x1(acc, ah, bh);
-  }
-}
+__device__ __forceinline__ void mma_tile_bf16(f4& acc, const View& A, const View& B, int K);
 
 // ---- one 16-wide k block with register operands ----------------------------------------
 // k-permuted mapping: within a 16-wide block, lane group g = l/16 owns k = 4g + e, e = 0..3,
@@ -203,7 +201,64 @@ __device__ __forceinline__ void mma16(f4& acc, const float4& a, const float4& b)
     mfma_bf16x1(acc, round4(a), round4(b));
   }
 }
+// Two consecutive 16-wide k blocks at once: (a0, b0) are the lane's operands of block kb,
+// (a1, b1) of block kb + 1.  highest: the same 8 fp32 MFMAs as two mma16 calls (identical
+// results); the bf16 modes: one 16x16x32 bf16 MFMA per pass on the two blocks' values
+// concatenated (lane group g: k = 4 g .. 4 g + 3 of both blocks), half the bf16 issues.
+__device__ __forceinline__ s8 cat8(const s4& x, const s4& y) {
+  return s8{x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+}
+template <int MODE>
+__device__ __forceinline__ void mma32(f4& acc, const float4& a0, const float4& b0, const float4& a1, const float4& b1) {
+  if constexpr (MODE == DOT_HIGHEST) {
+    mfma_f32x4(acc, a0, b0);
+    mfma_f32x4(acc, a1, b1);
+  } else if constexpr (MODE == DOT_BF16X3) {
+    s4 a0h, a0l, a1h, a1l, b0h, b0l, b1h, b1l;
+    split4(a0, a0h, a0l);
+    split4(a1, a1h, a1l);
+    split4(b0, b0h, b0l);
+    split4(b1, b1h, b1l);
+    mfma_bf16x3_k32(acc, cat8(a0h, a1h), cat8(a0l, a1l), cat8(b0h, b1h), cat8(b0l, b1l));
+  } else {
+    mfma_bf16x1_k32(acc, cat8(round4(a0), round4(a1)), cat8(round4(b0), round4(b1)));
+  }
+}
+// acc += sum over the k blocks kb in [k0, K1) of the lane operands a(kb), b(kb): fp32 one block
+// at a time (the instruction stream of a plain mma16 loop), the bf16 modes two blocks per
+// 32-deep MFMA and a last single block if the count is odd.  k0 must fold to a constant
+// (a template value or an unrolled loop index): no branch may sit inside a chain.
+template <int MODE, int K1, class FA, class FB>
+__device__ __forceinline__ void mma_chain(f4& acc, int k0, FA a, FB b) {
+  if constexpr (MODE == DOT_HIGHEST) {
+#pragma unroll
+    for (int kb = k0; kb < K1; ++kb) mma16<MODE>(acc, a(kb), b(kb));
+  } else {
+#pragma unroll
+    for (int kb = k0; kb + 1 < K1; kb += 2) mma32<MODE>(acc, a(kb), b(kb), a(kb + 1), b(kb + 1));
+    if ((K1 - k0) & 1) mma16<MODE>(acc, a(K1 - 1), b(K1 - 1));
+  }
+}
 __device__ __forceinline__ float4 f4_to_float4(const f4& x) { return make_float4(x[0], x[1], x[2], x[3]); }
+
+// bf16 tile product for the diagnostics: pairs of 16-wide k blocks on the 32-deep MFMA (the
+// operand mapping of mma32), a last single block on the 16-deep one
+template <bool THREE>
+__device__ __forceinline__ void mma_tile_bf16(f4& acc, const View& A, const View& B, int K) {
+  constexpr int MODE = THREE ? DOT_BF16X3 : DOT_DEFAULT;
+  const int l = lane_id(), r = l & 15, g = l >> 4;
+  auto opa = [&](int k0) {
+    const int kk = k0 + 4 * g;
+    return make_float4(A.at(r, kk), A.at(r, kk + 1), A.at(r, kk + 2), A.at(r, kk + 3));
+  };
+  auto opb = [&](int k0) {
+    const int kk = k0 + 4 * g;
+    return make_float4(B.at(kk, r), B.at(kk + 1, r), B.at(kk + 2, r), B.at(kk + 3, r));
+  };
+  int k0 = 0;
+  for (; k0 + 32 <= K; k0 += 32) mma32<MODE>(acc, opa(k0), opb(k0), opa(k0 + 16), opb(k0 + 16));
+  if (k0 < K) mma16<MODE>(acc, opa(k0), opb(k0));
+}
 __device__ __forceinline__ float4 scale4(const float4& x, float s) { return make_float4(s * x.x, s * x.y, s * x.z, s * x.w); }
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 

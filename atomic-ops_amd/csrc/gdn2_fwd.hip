@@ -57,8 +57,8 @@ __device__ __forceinline__ void score_pair(f4& accq, f4& acck, const TIn* __rest
     qa[kb] = in_ld4(qi + 16 * kb + 4 * g);
     ka[kb] = in_ld4(kj + 16 * kb + 4 * g);
   }
-#pragma unroll
-  for (int kb = 0; kb < D / 16; ++kb) {
+  // the operands of k block kb with the legs applied: q ra, (b k) ra, k cb
+  auto operands = [&](int kb, float4& aq, float4& ak, float4& bv) __attribute__((always_inline)) {
     const int d = 16 * kb + 4 * g;
     const float4 vi = ld4(gi + d), vj = ld4(gj + d), va = ld4(ga + d);
     float4 ra, cb;
@@ -74,9 +74,28 @@ __device__ __forceinline__ void score_pair(f4& accq, f4& acck, const TIn* __rest
       cb = make_float4(fast_exp((va.x - vj.x) - h.x), fast_exp((va.y - vj.y) - h.y), fast_exp((va.z - vj.z) - h.z),
                        fast_exp((va.w - vj.w) - h.w));
     }
-    const float4 bv = mul4(ka[kb], cb);
-    mma16<DOT>(accq, mul4(qa[kb], ra), bv);
-    mma16<DOT>(acck, mul4(ld4(bi + d), ra), bv);
+    bv = mul4(ka[kb], cb);
+    aq = mul4(qa[kb], ra);
+    ak = mul4(ld4(bi + d), ra);
+  };
+  if constexpr (DOT == DOT_HIGHEST) {
+#pragma unroll
+    for (int kb = 0; kb < D / 16; ++kb) {
+      float4 aq, ak, bv;
+      operands(kb, aq, ak, bv);
+      mma16<DOT>(accq, aq, bv);
+      mma16<DOT>(acck, ak, bv);
+    }
+  } else {
+    // bf16 modes: two k blocks per 32-deep MFMA
+#pragma unroll
+    for (int kb = 0; kb < D / 16; kb += 2) {
+      float4 aq0, ak0, bv0, aq1, ak1, bv1;
+      operands(kb, aq0, ak0, bv0);
+      operands(kb + 1, aq1, ak1, bv1);
+      mma32<DOT>(accq, aq0, bv0, aq1, bv1);
+      mma32<DOT>(acck, ak0, bv0, ak1, bv1);
+    }
   }
   drain(accq, acck);
 }
@@ -137,12 +156,12 @@ __device__ __forceinline__ void doubling_level_mfma(const float* sK, float* sI, 
 #pragma unroll
   for (int ti = 0; ti < NTL; ++ti) {
     mt[ti] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kb = 0; kb < NTL; ++kb) {
-      const float4 a = ld4(sK + (i0 + BB + 16 * ti + r) * LT + i0 + 16 * kb + 4 * g);
-      const float* bc = sI + (i0 + 16 * kb + 4 * g) * LT + i0 + 16 * tj + r;
-      mma16<MODE>(mt[ti], a, make_float4(bc[0], bc[LT], bc[2 * LT], bc[3 * LT]));
-    }
+    mma_chain<MODE, NTL>(
+        mt[ti], 0, [&](int kb) { return ld4(sK + (i0 + BB + 16 * ti + r) * LT + i0 + 16 * kb + 4 * g); },
+        [&](int kb) {
+          const float* bc = sI + (i0 + 16 * kb + 4 * g) * LT + i0 + 16 * tj + r;
+          return make_float4(bc[0], bc[LT], bc[2 * LT], bc[3 * LT]);
+        });
   }
   float4 mb4[NTL];
 #pragma unroll
@@ -153,9 +172,9 @@ __device__ __forceinline__ void doubling_level_mfma(const float* sK, float* sI, 
 #pragma unroll
   for (int ti = 0; ti < NTL; ++ti) {
     f4 x = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kb = 0; kb < NTL; ++kb)
-      mma16<MODE>(x, ld4(sI + (i0 + BB + 16 * ti + r) * LT + i0 + BB + 16 * kb + 4 * g), mb4[kb]);
+    mma_chain<MODE, NTL>(
+        x, 0, [&](int kb) { return ld4(sI + (i0 + BB + 16 * ti + r) * LT + i0 + BB + 16 * kb + 4 * g); },
+        [&](int kb) { return mb4[kb]; });
     drain(x);
 #pragma unroll
     for (int e = 0; e < 4; ++e) sI[(i0 + BB + 16 * ti + 4 * g + e) * LT + i0 + 16 * tj + r] = -x[e];
@@ -522,11 +541,18 @@ __global__ __launch_bounds__(256) void out_fwd_kernel(OutFwdArgs a) {
     if (ic + 1 < NCB) load_block(cb + NW);
 #pragma unroll
     for (int tq = 0; tq < 4; ++tq) {
+      // the same chains as the forward scan's output waves (gdn2_scan.hip), bit for bit
       f4 acc1 = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
+      mma_chain<DOT, NKB>(acc1, 0, [&](int kb) { return hc[kb]; }, [&](int kb) { return sQ[(tq * NKB + kb) * WAVE + l]; });
+      if constexpr (DOT == DOT_HIGHEST) {
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) mma16<DOT>(acc1, hc[kb], sQ[(tq * NKB + kb) * WAVE + l]);
+        for (int u = 0; u <= tq; ++u) mma16<DOT>(acc2, vc[u], sA[(tq * 4 + u) * WAVE + l]);
+      } else {
 #pragma unroll
-      for (int u = 0; u <= tq; ++u) mma16<DOT>(acc2, vc[u], sA[(tq * 4 + u) * WAVE + l]);
+        for (int u = 0; u + 1 <= tq; u += 2)
+          mma32<DOT>(acc2, vc[u], sA[(tq * 4 + u) * WAVE + l], vc[u + 1], sA[(tq * 4 + u + 1) * WAVE + l]);
+        if (!(tq & 1)) mma16<DOT>(acc2, vc[tq], sA[(tq * 4 + tq) * WAVE + l]);
+      }
       drain(acc1, acc2);
       const float4 ov = make_float4(sanitize(scale * acc1[0] + acc2[0], clip), sanitize(scale * acc1[1] + acc2[1], clip),
                                     sanitize(scale * acc1[2] + acc2[2], clip), sanitize(scale * acc1[3] + acc2[3], clip));

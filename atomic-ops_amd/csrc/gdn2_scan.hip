@@ -134,12 +134,23 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
     f4 acc = {0.f, 0.f, 0.f, 0.f};
     if constexpr (V) {
       __builtin_amdgcn_s_setprio(2);
+      if constexpr (MODE == DOT_HIGHEST) {
 #pragma unroll
-      for (int kb = 0; kb < NH; ++kb) {
-        mma16<MODE>(acc, op.x[kb], hb[kb]);
-        GDN2_SCHED_FENCE();
-        nx.x[kb] = ld4(a.wp_f + tbn + frag_blk(ti, kb, D) + 4 * l);
-        GDN2_SCHED_FENCE();
+        for (int kb = 0; kb < NH; ++kb) {
+          mma16<MODE>(acc, op.x[kb], hb[kb]);
+          GDN2_SCHED_FENCE();
+          nx.x[kb] = ld4(a.wp_f + tbn + frag_blk(ti, kb, D) + 4 * l);
+          GDN2_SCHED_FENCE();
+        }
+      } else {
+#pragma unroll
+        for (int kb = 0; kb < NH; kb += 2) {
+          mma32<MODE>(acc, op.x[kb], hb[kb], op.x[kb + 1], hb[kb + 1]);
+          GDN2_SCHED_FENCE();
+          nx.x[kb] = ld4(a.wp_f + tbn + frag_blk(ti, kb, D) + 4 * l);
+          nx.x[kb + 1] = ld4(a.wp_f + tbn + frag_blk(ti, kb + 1, D) + 4 * l);
+          GDN2_SCHED_FENCE();
+        }
       }
       drain(acc);
       const float4 vn = sub4(op.uu, f4_to_float4(acc));
@@ -154,13 +165,25 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
     for (int u = 0; u < 4; ++u) vv[u] = sV[u * WAVE + l];
     if constexpr (OWNS) {
       __builtin_amdgcn_s_setprio(2);
+      // Kg^T v_new: the same chain as the backward's state recompute (gdn2_bwd.hip)
       f4 hn = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (MODE == DOT_HIGHEST) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        mma16<MODE>(hn, op.kg[u], vv[u]);
-        GDN2_SCHED_FENCE();
-        nx.kg[u] = ld4(a.kgT_f + tbn + frag_blk(w, u, T) + 4 * l);
-        GDN2_SCHED_FENCE();
+        for (int u = 0; u < 4; ++u) {
+          mma16<MODE>(hn, op.kg[u], vv[u]);
+          GDN2_SCHED_FENCE();
+          nx.kg[u] = ld4(a.kgT_f + tbn + frag_blk(w, u, T) + 4 * l);
+          GDN2_SCHED_FENCE();
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; u += 2) {
+          mma32<MODE>(hn, op.kg[u], vv[u], op.kg[u + 1], vv[u + 1]);
+          GDN2_SCHED_FENCE();
+          nx.kg[u] = ld4(a.kgT_f + tbn + frag_blk(w, u, T) + 4 * l);
+          nx.kg[u + 1] = ld4(a.kgT_f + tbn + frag_blk(w, u + 1, T) + 4 * l);
+          GDN2_SCHED_FENCE();
+        }
       }
       drain(hn);
       const float gmv[4] = {op.gm.x, op.gm.y, op.gm.z, op.gm.w};
@@ -178,20 +201,40 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
     }
     if constexpr (O) {
       __builtin_amdgcn_s_setprio(0);
-#pragma unroll
-      for (int kb = 0; kb < NH; ++kb) {
-        mma16<MODE>(acc, hb[kb], op.x[kb]);
-        GDN2_SCHED_FENCE();
-        nx.x[kb] = ld4(a.qg_f + tbn + frag_blk(J, kb, D) + 4 * l);
-        GDN2_SCHED_FENCE();
-      }
       f4 acc2 = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (MODE == DOT_HIGHEST) {
 #pragma unroll
-      for (int u = 0; u <= J; ++u) {
-        mma16<MODE>(acc2, vv[u], op.aq[u]);
-        GDN2_SCHED_FENCE();
-        nx.aq[u] = ld4(a.aqk_f + sbn + frag_blk(J, u, T) + 4 * l);
-        GDN2_SCHED_FENCE();
+        for (int kb = 0; kb < NH; ++kb) {
+          mma16<MODE>(acc, hb[kb], op.x[kb]);
+          GDN2_SCHED_FENCE();
+          nx.x[kb] = ld4(a.qg_f + tbn + frag_blk(J, kb, D) + 4 * l);
+          GDN2_SCHED_FENCE();
+        }
+#pragma unroll
+        for (int u = 0; u <= J; ++u) {
+          mma16<MODE>(acc2, vv[u], op.aq[u]);
+          GDN2_SCHED_FENCE();
+          nx.aq[u] = ld4(a.aqk_f + sbn + frag_blk(J, u, T) + 4 * l);
+          GDN2_SCHED_FENCE();
+        }
+      } else {
+#pragma unroll
+        for (int kb = 0; kb < NH; kb += 2) {
+          mma32<MODE>(acc, hb[kb], op.x[kb], hb[kb + 1], op.x[kb + 1]);
+          GDN2_SCHED_FENCE();
+          nx.x[kb] = ld4(a.qg_f + tbn + frag_blk(J, kb, D) + 4 * l);
+          nx.x[kb + 1] = ld4(a.qg_f + tbn + frag_blk(J, kb + 1, D) + 4 * l);
+          GDN2_SCHED_FENCE();
+        }
+#pragma unroll
+        for (int u = 0; u <= J; u += 2) {
+          if (u + 1 <= J) mma32<MODE>(acc2, vv[u], op.aq[u], vv[u + 1], op.aq[u + 1]);
+          else mma16<MODE>(acc2, vv[u], op.aq[u]);
+          GDN2_SCHED_FENCE();
+          nx.aq[u] = ld4(a.aqk_f + sbn + frag_blk(J, u, T) + 4 * l);
+          if (u + 1 <= J) nx.aq[u + 1] = ld4(a.aqk_f + sbn + frag_blk(J, u + 1, T) + 4 * l);
+          GDN2_SCHED_FENCE();
+        }
       }
       drain(acc, acc2);
       // lane (r, g): o[16 J + r][c0 + 4 g .. + 3]
@@ -336,12 +379,23 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
 #pragma unroll
     for (int u = 0; u < 4; ++u) db4[u] = sDB[u * WAVE + l];
     f4 z = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (MODE == DOT_HIGHEST) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      mma16<MODE>(z, op.wpT[u], db4[u]);
-      GDN2_SCHED_FENCE();
-      nx.wpT[u] = ld4(a.wpT_f + tbn + frag_blk(w, u, T) + 4 * l);
-      GDN2_SCHED_FENCE();
+      for (int u = 0; u < 4; ++u) {
+        mma16<MODE>(z, op.wpT[u], db4[u]);
+        GDN2_SCHED_FENCE();
+        nx.wpT[u] = ld4(a.wpT_f + tbn + frag_blk(w, u, T) + 4 * l);
+        GDN2_SCHED_FENCE();
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; u += 2) {
+        mma32<MODE>(z, op.wpT[u], db4[u], op.wpT[u + 1], db4[u + 1]);
+        GDN2_SCHED_FENCE();
+        nx.wpT[u] = ld4(a.wpT_f + tbn + frag_blk(w, u, T) + 4 * l);
+        nx.wpT[u + 1] = ld4(a.wpT_f + tbn + frag_blk(w, u + 1, T) + 4 * l);
+        GDN2_SCHED_FENCE();
+      }
     }
     float4 dvv = db;
     if (red) dvv = frag_transpose_lds(sDB, tp, lp);     // FA(dv_new) block (tp, slice)

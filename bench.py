@@ -255,6 +255,38 @@ def state_ckpt_table(cfg, seed, ks=(0, 1, 2, 3, 4, 8, 32)):
     return rows
 
 
+def dot_mode_table(seed):
+    """Config 2's gradient evaluation under each dot mode (the three set alike), the PROD
+    precision mix (scores and scan fp32, solve and backward products bf16x3) at bt 64, and
+    make_cfg() as the reference ships it (bt 128, wy_eps 1e-3, that mix); median protocol."""
+    import torch
+    from atomic_gdn2 import make_cfg, make_blr_trainable, _lib
+    from atomic_gdn2.synthetic import make_inputs
+    (q, k, v, w, b, g), scale = make_inputs(B_, H_, L_, D_, seed=seed)
+    xs = [t.requires_grad_(True) for t in (q, k, v, w, b, g)]
+    base = dict(bt=64, bc=32, score_bs=64, bs2=32, mb=8, wy_eps=0.0)
+    rows = {}
+    for name, cfg in (("highest", make_cfg(**base, dot_mode="highest", solve_dot_mode="highest", b3_dot_mode="highest")),
+                      ("bf16x3", make_cfg(**base, dot_mode="bf16x3", solve_dot_mode="bf16x3", b3_dot_mode="bf16x3")),
+                      ("default", make_cfg(**base, dot_mode="default", solve_dot_mode="default", b3_dot_mode="default")),
+                      ("prod_mix_bt64", make_cfg(**base)),
+                      ("make_cfg_bt128", make_cfg())):
+        fn = make_blr_trainable(cfg, scale)
+
+        def step():
+            o, hf = fn(*xs)
+            return torch.autograd.grad((o, hf), xs, grad_outputs=(2.0 * o, 2.0 * hf))
+
+        ms = _median_ms(step)
+        _lib.prof_begin(4 * 16)
+        for _ in range(4):
+            step()
+        torch.cuda.synchronize()
+        prof = _lib.prof_end()
+        rows[name] = {"ms": round(ms, 4), "kernel_us": {n: round(t / c * 1e3, 1) for n, (t, c) in prof.items() if c}}
+    return rows
+
+
 def bench_config4(cfg, seed):
     """Config 4: forward-only long context, B8 H16 D128, bf16 inputs, fp32
     state; L = 32768 as 8 calls of 4096 tokens, each call's h0 = the previous h_final.  Inputs
@@ -324,6 +356,7 @@ def main():
                     help="residual state checkpoint interval K (0 = every chunk's state kept); "
                          "default: the library's DEFAULT_STATE_CKPT")
     ap.add_argument("--ckpt-table", action="store_true", help="only print the state_ckpt table and exit")
+    ap.add_argument("--dot-table", action="store_true", help="only print the dot-mode table and exit")
     ap.add_argument("--profile-only", action="store_true",
                     help="for rocprofv3: run --warmup then --steps gradient evaluations of the workload "
                          "(no timing loops, no forward-only pass, no other configs) and print nothing else")
@@ -368,6 +401,9 @@ def main():
     ckpt = DEFAULT_STATE_CKPT if args.state_ckpt is None else args.state_ckpt
     if args.ckpt_table:
         print(json.dumps({"state_ckpt_table": state_ckpt_table(cfg, args.seed)}), flush=True)
+        return
+    if args.dot_table:
+        print(json.dumps({"dot_mode_ms": dot_mode_table(args.seed)}), flush=True)
         return
     if args.profile_only:
         if args.seq_len == L_:
@@ -462,6 +498,7 @@ def main():
     if not args.no_sweep:
         out["config2_seeds"] = seeds_config2(cfg)
         out["state_ckpt_table"] = state_ckpt_table(cfg, args.seed)
+        out["dot_mode_ms"] = dot_mode_table(args.seed)
         out["config3_sweep"] = sweep_config3(cfg, args.seed)
         out["config4_long_context_fwd"] = bench_config4(cfg, args.seed)
     if not args.no_e2e:
