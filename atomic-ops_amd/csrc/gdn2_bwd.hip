@@ -347,10 +347,12 @@ __global__ __launch_bounds__(NWW * WAVE) __attribute__((amdgpu_waves_per_eu(2)))
 // Phases (LDS: gc | X1 | X2 | A | dAqk | dA/dAkk | column partial sums):
 //   P1 dAqk = (dO v_new^T) * causal                 X1 = v_new, X2 = dO              (mega.py:32)
 //   P2 dA = san(dWp kb^T + dv_new (w v)^T)           X1 = kb / w v, X2 = dWp / dv_new (mega.py:41)
-//   P3 tmp = san(dA A^T)                                      X1 = tmp              (mega.py:43)
+//      and per owned tile dwv = A^T dv_new                                          (mega.py:42)
+//   P3 tmp = san(dA A^T)                               X2 = tmp, X1 = dwv           (mega.py:43)
+//   dw = san(dwv v), dv = san(dwv w) as row-major items, stored here           (mega.py:57-58)
 //   P4 dAkk = san(-(1-eps) A^T tmp) * strict                                       (mega.py:44)
 //   B4 VJP of the two-level scores, piece by piece (owned tiles, registers)   (b4.py:45-97)
-//   per owned tile: dkb = A^T dWp, dwv = A^T dv_new (mega.py:42), the gate gradients
+//   per owned tile: dkb = A^T dWp (mega.py:42), the gate gradients
 //   dq3 / dk3 / db3 / dgc3 and the combine with B4                           (mega.py:45-59)
 //   B5 dg = reverse cumsum of dgc3 + dgc4                                            (mega.py:53)
 // ------------------------------------------------------------------------------------
@@ -382,9 +384,12 @@ __device__ __forceinline__ float4 pick4(const float4 (&x)[4], int t) {
                      sel4(x[0].z, x[1].z, x[2].z, x[3].z, t), sel4(x[0].w, x[1].w, x[2].w, x[3].w, t));
 }
 
-// STD: the pieces are the standard geometry's (bt = score_bs = 64, bs2 = 32), see std_pieces()
-template <int D, int B3, bool STD>
+// STD: the pieces are the standard geometry's (bt = score_bs = 64, bs2 = 32), see std_pieces().
+// LEAN: the lean diagonal (cfg.diag); a compile-time choice, so that the BTL kernels carry no
+// trace of the lean loops (whose live ranges otherwise push registers into scratch).
+template <int D, int B3, bool STD, bool LEAN>
 __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
+  static_assert(!(STD && LEAN), "the standard piece list is the BTL one");
   using Lay = BwdWyLayout<D>;
   using St = Strip<D>;
   constexpr int LD = Lay::LD, LT = Lay::LT, NT = 512, NW = 8, NTW = St::NTW, NKB = D / 16;
@@ -461,28 +466,29 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   __syncthreads();
 
   // The P2 operands' global loads are spread between P1's MFMAs (a burst of loads stalls the
-  // issuing wave while the CU's memory path is busy).  b and k arrive as this lane's column
-  // at the rows of the four row tiles (the layout B4 and the gates use, so they stay in
-  // registers to the end); w, v, dWp, dv_new as row-major / fragment items.
-  float4 kv[4], bv[4];
-  float4 xw[NIT], xv[NIT], xdw[NIT], xdv[NIT];
+  // issuing wave while the CU's memory path is busy).  b, k and dWp arrive as this lane's
+  // column at the rows of the four row tiles (the layout B4, the dkb chain and the gates use,
+  // so they stay in registers to the end); w, v, dv_new as row-major / fragment items, which
+  // also serve dw / dv after P2.  Every input is read once.
+  float4 kv[4], bv[4], dwpc[4];
+  float4 xw[NIT], xv[NIT], xdv[NIT];
   constexpr int NRT = T / 16;
   auto prefetch = [&](int item) {
-    if (item < 2 * NRT) {
+    if (item < 3 * NRT) {
       if (item < NRT) bv[item] = col4(b, item);
-      else kv[item - NRT] = col4(k, item - NRT);
+      else if (item < 2 * NRT) kv[item - NRT] = col4(k, item - NRT);
+      else dwpc[item - 2 * NRT] = fcol4(dwp, item - 2 * NRT);
       return;
     }
-    const int arr = (item - 2 * NRT) / NIT, it = (item - 2 * NRT) % NIT, f = tid + it * NT;
-    if (arr == 0) xw[it] = ld4(w + 4 * f);
-    else if (arr == 1) xv[it] = ld4(v + 4 * f);
-    else if (arr == 2) xdw[it] = ld4(dwp + 4 * f);
+    const int arr = (item - 3 * NRT) / NIT, it = (item - 3 * NRT) % NIT, f = tid + it * NT;
+    if (arr == 0) xw[it] = ldg4(w + 4 * f);
+    else if (arr == 1) xv[it] = ldg4(v + 4 * f);
     else xdv[it] = ldg4(a.dv_new_f + tb + 4 * f);
   };
 
   // P1: dAqk = (dO v_new^T) * causal; 16 tiles, two per wave
   static_assert(NW == 8, "P1 assumes two dAqk tiles per wave");
-  constexpr int NITEMS = 2 * NRT + 4 * NIT, NSLOT = 2 * NKB;
+  constexpr int NITEMS = 3 * NRT + 3 * NIT, NSLOT = 2 * NKB;
 #pragma unroll
   for (int m2 = 0; m2 < 2; ++m2) {
     const int t = wv + NW * m2, ti = t >> 2, tj = t & 3;
@@ -511,20 +517,21 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   __syncthreads();
 
   // P2: dA = san(dWp kb^T + dv_new (w v)^T), the two products with operands staged in turn:
-  //     X1 = kb = b k e^{min(gc,0)}, X2 = dWp; then X1 = w v, X2 = dv_new (kept for dwv)
-  // X1 = kb at this wave's column strip and owned row tiles (every element written once)
+  //     X1 = kb = b k e^{min(gc,0)}, X2 = dWp; then X1 = w v, X2 = dv_new (for dwv)
+  // X1 = kb and X2 = dWp at this wave's column strip and owned row tiles (every element
+  // written once)
 #pragma unroll
   for (int t = 0; t < NRT; ++t) {
     if (!owned(t)) continue;
     const float bb[4] = {bv[t].x, bv[t].y, bv[t].z, bv[t].w}, kk[4] = {kv[t].x, kv[t].y, kv[t].z, kv[t].w};
+    const float dd[4] = {dwpc[t].x, dwpc[t].y, dwpc[t].z, dwpc[t].w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int i = 16 * t + 4 * g + e;
       sX1[i * LD + dcol] = (bb[e] * kk[e]) * exp_nonpos(sG[i * LD + dcol]);
+      sX2[i * LD + dcol] = dd[e];
     }
   }
-#pragma unroll
-  for (int it = 0; it < NIT; ++it) put_fragT(sX2, xdw[it], tid + it * NT);
   __syncthreads();
   f4 accA[2];
 #pragma unroll
@@ -556,6 +563,31 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     for (int e = 0; e < 4; ++e)
       sDA[(16 * ti + 4 * g + e) * LT + 16 * tj + r] = sanitize(accA[m2][e] + acc[e], clip);
   }
+  // dwv = A^T dv_new on the owned tiles (mega.py:42; A^T is upper triangular, so row tile rt
+  // only sees k blocks >= rt).  It needs no B4 result, so dw and dv leave before B4 (their
+  // stores overlap P3 / P4 / B4) and the gate phase keeps only the dkb chain.
+  constexpr bool RT_STATIC = St::NS == NW;            // rt == m for every wave
+  f4 dwv[NTW];
+#pragma unroll
+  for (int m = 0; m < NTW; ++m) {
+    const int rt = St::rtile(wv, m);
+    auto acol = [&](int kb) {
+      const float* ac = sA + (16 * kb + 4 * g) * LT + 16 * rt + r;
+      return make_float4(ac[0], ac[LT], ac[2 * LT], ac[3 * LT]);
+    };
+    auto pcol = [&](int kb) {
+      const float* pv = sX2 + (16 * kb + 4 * g) * LD + dcol;
+      return make_float4(pv[0], pv[LD], pv[2 * LD], pv[3 * LD]);
+    };
+    dwv[m] = f4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (B3 == DOT_HIGHEST) {
+#pragma unroll
+      for (int kb = RT_STATIC ? m : 0; kb < 4; ++kb) mma16<B3>(dwv[m], acol(kb), pcol(kb));
+    } else {
+      mma_chain<B3, 4>(dwv[m], RT_STATIC ? m : 0, acol, pcol);
+    }
+    drain(dwv[m]);
+  }
   __syncthreads();
 
   // q of this lane's column at the rows of all four row tiles (B4 and the gates), loaded
@@ -564,8 +596,16 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
 #pragma unroll
   for (int t = 0; t < 4; ++t) qv[t] = col4(q, t);
 
-  // P3: tmp = san(dA A^T) into X1 (as T x LT)
-  float* sTmp = sX1;
+  // dwv -> X1 (row-major), read back below as the row-major items of w and v
+#pragma unroll
+  for (int m = 0; m < NTW; ++m) {
+    const int rt = St::rtile(wv, m);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sX1[(16 * rt + 4 * g + e) * LD + dcol] = dwv[m][e];
+  }
+
+  // P3: tmp = san(dA A^T) into X2 (as T x LT; dv_new is done with)
+  float* sTmp = sX2;
   for (int t = wv; t < 16; t += NW) {
     const int ti = t >> 2, tj = t & 3;
     f4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -576,6 +616,17 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     for (int e = 0; e < 4; ++e) sTmp[(16 * ti + 4 * g + e) * LT + 16 * tj + r] = sanitize(acc[e], clip);
   }
   __syncthreads();
+
+  // dw = san(dwv v), dv = san(dwv w) (mega.py:57-58), row-major items, one float4 store each
+  float* __restrict__ o_dw = a.dw + tio;
+  float* __restrict__ o_dv = a.dv + tio;
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int f = tid + it * NT, i = f / (D / 4), d = 4 * (f % (D / 4));
+    const float4 x = ld4(sX1 + i * LD + d);
+    st4(o_dw + i * D + d, san4(mul4(x, xv[it]), clip));
+    st4(o_dv + i * D + d, san4(mul4(x, xw[it]), clip));
+  }
 
   // P4: dAkk = san(-(1-eps) A^T tmp) * strict into sDA; tiles above the diagonal are zero
   for (int t = wv; t < 16; t += NW) {
@@ -610,10 +661,6 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   // stores would wait for them too).  The first ones are issued here, to arrive during B4.
   const float* __restrict__ dqgp = a.dqg + tb;
   const float* __restrict__ dkgp = a.dkg + tb;
-  float4 dwpc[4];
-#pragma unroll
-  for (int kb = 0; kb < 4; ++kb) dwpc[kb] = fcol4(dwp, kb);
-  float4 nw4 = col4(w, St::rtile(wv, 0)), nv4 = col4(v, St::rtile(wv, 0));
   float4 ndq4 = fcol4(dqgp, St::rtile(wv, 0)), ndk4 = fcol4(dkgp, St::rtile(wv, 0));
 
   // B4: VJP of the two-level scores on the owned tiles (b4.py:45-97)
@@ -625,7 +672,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     dk4[m] = dq4[m];
     dgc4[m] = dq4[m];
   }
-  const bool lean = cf.diag == DIAG_LEAN;
+  constexpr bool lean = LEAN;
   // One piece of the two-level score factorisation; with the standard geometry the three
   // pieces are compile-time constants, so every branch and index below folds away.
   auto b4_piece = [&](const Piece pc) __attribute__((always_inline)) {
@@ -731,7 +778,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   }
 
   // lean diagonal blocks (b4.py:20-30): exact E = exp(clip(gc_i - gc_j, +-diff_clip)) per element
-  if (lean) {
+  if constexpr (LEAN) {
     for (int pi = 0; pi < cf.pieces.n; ++pi) {
       const Piece pc = cf.pieces.p[pi];
       if (pc.kind != 1) continue;
@@ -773,20 +820,18 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     }
   }
 
-  // per owned tile: dkb = A^T dWp, dwv = A^T dv_new (mega.py:42; A^T is upper triangular, so
-  // row tile rt only sees k blocks >= rt), then the gate gradients (mega.py:45-51) and the
+  // per owned tile: dkb = A^T dWp (mega.py:42; A^T is upper triangular, so row tile rt only
+  // sees k blocks >= rt), then the gate gradients (mega.py:45-51) and the
   // combine with B4 (mega.py:52-59); dgc -> X1 for B5.  Row T-1 also needs the last-row decay
   // term (mega.py:50), a sum over all rows: its dgc is finished after the loop.
   float* __restrict__ o_dq = a.dq + tio;
   float* __restrict__ o_dk = a.dk + tio;
   float* __restrict__ o_db = a.db + tio;
-  float* __restrict__ o_dw = a.dw + tio;
-  float* __restrict__ o_dv = a.dv + tio;
   float* sDgc = sX1;
   const float gl = sG[(T - 1) * LD + dcol];
   const float dlast = owned(3) && g == 3 ? a.dlast[(size_t)chunk * D + dcol] : 0.f;
   float part = 0.f, fix3 = 0.f, fix4 = 0.f;
-  // The five gradient tiles leave through a per-wave 16x16 LDS transpose (in the dAqk buffer,
+  // The three gradient tiles leave through a per-wave 16x16 LDS transpose (in the dAqk buffer,
   // free once every wave has left B4) as one float4 row store per lane instead of four
   // scalar column stores.  Plain stores: streaming stores complete later, and the next
   // tile's load waits would cover them.
@@ -796,48 +841,33 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
 #pragma unroll
   for (int m = 0; m < NTW; ++m) {
     const int rt = St::rtile(wv, m), i0 = 16 * rt + 4 * g;
-    const float4 w4 = nw4, v4 = nv4, dqg4 = ndq4, dkg4 = ndk4;
+    const float4 dqg4 = ndq4, dkg4 = ndk4;
     if (m + 1 < NTW) {
       const int rn = St::rtile(wv, m + 1);
-      nw4 = col4(w, rn);
-      nv4 = col4(v, rn);
       ndq4 = fcol4(dqgp, rn);
       ndk4 = fcol4(dkgp, rn);
     }
-    f4 dkb = {0.f, 0.f, 0.f, 0.f}, dwv = {0.f, 0.f, 0.f, 0.f};
+    f4 dkb = {0.f, 0.f, 0.f, 0.f};
     // straight-line MFMA chain: skip the zero k blocks only where rt is a compile-time value
-    constexpr bool RT_STATIC = St::NS == NW;          // rt == m for every wave
     auto acol = [&](int kb) {
       const float* ac = sA + (16 * kb + 4 * g) * LT + 16 * rt + r;
       return make_float4(ac[0], ac[LT], ac[2 * LT], ac[3 * LT]);
     };
-    auto pcol = [&](int kb) {
-      const float* pv = sX2 + (16 * kb + 4 * g) * LD + dcol;
-      return make_float4(pv[0], pv[LD], pv[2 * LD], pv[3 * LD]);
-    };
     if constexpr (B3 == DOT_HIGHEST) {
 #pragma unroll
-      for (int kb = RT_STATIC ? m : 0; kb < 4; ++kb) {
-        const float4 av = acol(kb);
-        mma16<B3>(dkb, av, dwpc[kb]);
-        mma16<B3>(dwv, av, pcol(kb));
-      }
+      for (int kb = RT_STATIC ? m : 0; kb < 4; ++kb) mma16<B3>(dkb, acol(kb), dwpc[kb]);
     } else {
       mma_chain<B3, 4>(dkb, RT_STATIC ? m : 0, acol, [&](int kb) { return dwpc[kb]; });
-      mma_chain<B3, 4>(dwv, RT_STATIC ? m : 0, acol, pcol);
     }
-    drain(dkb, dwv);
+    drain(dkb);
     const float4 q4 = pick4(qv, rt), k4 = pick4(kv, rt), b4 = pick4(bv, rt);
     const float qa[4] = {q4.x, q4.y, q4.z, q4.w}, ka[4] = {k4.x, k4.y, k4.z, k4.w}, ba[4] = {b4.x, b4.y, b4.z, b4.w};
-    const float wa[4] = {w4.x, w4.y, w4.z, w4.w}, va[4] = {v4.x, v4.y, v4.z, v4.w};
     const float qga[4] = {dqg4.x, dqg4.y, dqg4.z, dqg4.w}, kga[4] = {dkg4.x, dkg4.y, dkg4.z, dkg4.w};
-    float ow[4], ov[4], oq[4], ok[4], ob[4];
+    float oq[4], ok[4], ob[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int i = i0 + e;
       const float be = ba[e], ke = ka[e], qe = qa[e];
-      ow[e] = sanitize(dwv[e] * va[e], clip);     // mega.py:57
-      ov[e] = sanitize(dwv[e] * wa[e], clip);     // mega.py:58
       const float gi = sG[i * LD + dcol];
       const float egc = exp_nonpos(gi), ekg = exp_nonpos(gl - gi);
       const float mgc = gi < 0.f ? 1.f : 0.f, mkg = (gl - gi) < 0.f ? 1.f : 0.f;
@@ -867,8 +897,6 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     }
     // lane (r, g) after the transpose: row 16 rt + r, columns 16 strip + 4 g .. + 3
     const int ro = (16 * rt + r) * D + 16 * strip + 4 * g;
-    st4(o_dw + ro, wave_transpose16(tr, make_float4(ow[0], ow[1], ow[2], ow[3]), r, g));
-    st4(o_dv + ro, wave_transpose16(tr, make_float4(ov[0], ov[1], ov[2], ov[3]), r, g));
     st4(o_dq + ro, wave_transpose16(tr, make_float4(oq[0], oq[1], oq[2], oq[3]), r, g));
     st4(o_dk + ro, wave_transpose16(tr, make_float4(ok[0], ok[1], ok[2], ok[3]), r, g));
     st4(o_db + ro, wave_transpose16(tr, make_float4(ob[0], ob[1], ob[2], ob[3]), r, g));
@@ -1031,15 +1059,18 @@ static bool std_pieces(const PieceList& pl) {
 }
 
 hipError_t launch_bwd_wy(int D, const BwdWyArgs& a, hipStream_t s) {
-  const bool std_geom = std_pieces(a.cfg.pieces);
+  const bool lean = a.cfg.diag == DIAG_LEAN, std_geom = !lean && std_pieces(a.cfg.pieces);
   dispatch_mode(a.cfg.b3_mode, [&](auto m) {
     constexpr int M = decltype(m)::value;
+    const dim3 grid(a.n_chunks), block(512);
     if (D == 128) {
-      if (std_geom) hipLaunchKernelGGL((bwd_wy_kernel<128, M, true>), dim3(a.n_chunks), dim3(512), 0, s, a);
-      else hipLaunchKernelGGL((bwd_wy_kernel<128, M, false>), dim3(a.n_chunks), dim3(512), 0, s, a);
+      if (lean) hipLaunchKernelGGL((bwd_wy_kernel<128, M, false, true>), grid, block, 0, s, a);
+      else if (std_geom) hipLaunchKernelGGL((bwd_wy_kernel<128, M, true, false>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((bwd_wy_kernel<128, M, false, false>), grid, block, 0, s, a);
     } else {
-      if (std_geom) hipLaunchKernelGGL((bwd_wy_kernel<64, M, true>), dim3(a.n_chunks), dim3(512), 0, s, a);
-      else hipLaunchKernelGGL((bwd_wy_kernel<64, M, false>), dim3(a.n_chunks), dim3(512), 0, s, a);
+      if (lean) hipLaunchKernelGGL((bwd_wy_kernel<64, M, false, true>), grid, block, 0, s, a);
+      else if (std_geom) hipLaunchKernelGGL((bwd_wy_kernel<64, M, true, false>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((bwd_wy_kernel<64, M, false, false>), grid, block, 0, s, a);
     }
     return 0;
   });
