@@ -822,8 +822,14 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
 
   // per owned tile: dkb = A^T dWp (mega.py:42; A^T is upper triangular, so row tile rt only
   // sees k blocks >= rt), then the gate gradients (mega.py:45-51) and the
-  // combine with B4 (mega.py:52-59); dgc -> X1 for B5.  Row T-1 also needs the last-row decay
-  // term (mega.py:50), a sum over all rows: its dgc is finished after the loop.
+  // combine with B4 (mega.py:52-59).  Row T-1 also needs the last-row decay term (mega.py:50),
+  // a sum over all rows: its dgc is finished after the loop.
+  // With RT_STATIC (D = 128) a wave owns whole columns: the gradient tiles are stored from the
+  // accumulator layout (four rows of 64 contiguous bytes per instruction), and the column sum
+  // and B5 stay inside the wave, so no barrier follows P4.  Otherwise two waves share a
+  // column: the tiles leave through a per-wave 16x16 LDS transpose (in the dAqk buffer, free
+  // once every wave has left B4), dgc goes to X1 and B5 runs over the workgroup.  Plain
+  // stores: streaming stores complete later, and the next tile's load waits would cover them.
   float* __restrict__ o_dq = a.dq + tio;
   float* __restrict__ o_dk = a.dk + tio;
   float* __restrict__ o_db = a.db + tio;
@@ -831,12 +837,9 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   const float gl = sG[(T - 1) * LD + dcol];
   const float dlast = owned(3) && g == 3 ? a.dlast[(size_t)chunk * D + dcol] : 0.f;
   float part = 0.f, fix3 = 0.f, fix4 = 0.f;
-  // The three gradient tiles leave through a per-wave 16x16 LDS transpose (in the dAqk buffer,
-  // free once every wave has left B4) as one float4 row store per lane instead of four
-  // scalar column stores.  Plain stores: streaming stores complete later, and the next
-  // tile's load waits would cover them.
+  float dgv[NTW][4];                                 // RT_STATIC: this lane's dgc3 + dgc4
   static_assert(NW * 16 * TRP <= T * LT, "transpose tiles fit in the dAqk buffer");
-  __syncthreads();
+  if constexpr (!RT_STATIC) __syncthreads();
   float* tr = sDAq + wv * 16 * TRP;
 #pragma unroll
   for (int m = 0; m < NTW; ++m) {
@@ -891,20 +894,57 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
       if (i == T - 1) {
         fix3 = dgc3;
         fix4 = dgc4v;
-      } else {
-        sDgc[i * LD + dcol] = sanitize(dgc3, clip) + dgc4v;
       }
+      const float dgcv = sanitize(dgc3, clip) + dgc4v;
+      if constexpr (RT_STATIC) dgv[m][e] = dgcv;
+      else if (i != T - 1) sDgc[i * LD + dcol] = dgcv;
     }
-    // lane (r, g) after the transpose: row 16 rt + r, columns 16 strip + 4 g .. + 3
-    const int ro = (16 * rt + r) * D + 16 * strip + 4 * g;
-    st4(o_dq + ro, wave_transpose16(tr, make_float4(oq[0], oq[1], oq[2], oq[3]), r, g));
-    st4(o_dk + ro, wave_transpose16(tr, make_float4(ok[0], ok[1], ok[2], ok[3]), r, g));
-    st4(o_db + ro, wave_transpose16(tr, make_float4(ob[0], ob[1], ob[2], ob[3]), r, g));
+    if constexpr (RT_STATIC) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        o_dq[(i0 + e) * D + dcol] = oq[e];
+        o_dk[(i0 + e) * D + dcol] = ok[e];
+        o_db[(i0 + e) * D + dcol] = ob[e];
+      }
+    } else {
+      // lane (r, g) after the transpose: row 16 rt + r, columns 16 strip + 4 g .. + 3
+      const int ro = (16 * rt + r) * D + 16 * strip + 4 * g;
+      st4(o_dq + ro, wave_transpose16(tr, make_float4(oq[0], oq[1], oq[2], oq[3]), r, g));
+      st4(o_dk + ro, wave_transpose16(tr, make_float4(ok[0], ok[1], ok[2], ok[3]), r, g));
+      st4(o_db + ro, wave_transpose16(tr, make_float4(ob[0], ob[1], ob[2], ob[3]), r, g));
+    }
   }
   // last-row decay gradient: sum over all rows of the column (lanes g, then the waves of the
   // strip in order) + e^gamma sum_v(dh_next h_pre) [gl < 0]
   part += __shfl_xor(part, 16);
   part += __shfl_xor(part, 32);
+  if constexpr (RT_STATIC) {
+    // the strip is this wave's alone; row T-1 is element 3 of row tile 3 on the lanes g = 3
+    const float dec = exp_nonpos(gl), mdec = gl < 0.f ? 1.f : 0.f;
+    const float colsum = part + dec * dlast * mdec;
+    if (g == 3) dgv[NTW - 1][3] = sanitize(fix3 + colsum, clip) + fix4;
+    // B5 (mega.py:53): dg = reverse cumsum over the chunk rows, row order (t, g, e): within a
+    // lane over e, then the later lane groups g of the same row tile (exclusive suffix across
+    // lanes r + 16 g), then the totals of the later row tiles.
+    float* __restrict__ o_dg = a.dg + tio;
+    float later = 0.f;                               // sum of the row tiles below t
+#pragma unroll
+    for (int t = NTW - 1; t >= 0; --t) {
+      float x[4];
+      x[3] = dgv[t][3];
+#pragma unroll
+      for (int e = 2; e >= 0; --e) x[e] = x[e + 1] + dgv[t][e];
+      const float s = x[0];
+      const float s1 = __shfl(s, (l + 16) & 63), s2 = __shfl(s, (l + 32) & 63), s3 = __shfl(s, (l + 48) & 63);
+      const float suf = ((g < 3 ? s1 : 0.f) + (g < 2 ? s2 : 0.f)) + (g < 1 ? s3 : 0.f);
+      const float tot = __shfl(suf + s, r);          // lane g = 0: the row tile's total
+      const float off = later + suf;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o_dg[(16 * t + 4 * g + e) * D + dcol] = sanitize(x[e] + off, clip);
+      later += tot;
+    }
+    return;
+  }
   if (g == 0) sColP[wv * 16 + r] = part;
   __syncthreads();
   if (owned(3) && g == 3) {
