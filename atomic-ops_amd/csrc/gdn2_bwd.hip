@@ -617,7 +617,9 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   }
   __syncthreads();
 
-  // dw = san(dwv v), dv = san(dwv w) (mega.py:57-58), row-major items, one float4 store each
+  // dw = san(dwv v), dv = san(dwv w) (mega.py:57-58), row-major items, one float4 store each.
+  // q (for B4) is waited for here, before the first store (see the gate phase's loads below).
+  __builtin_amdgcn_s_waitcnt(WAIT_VMCNT0);
   float* __restrict__ o_dw = a.dw + tio;
   float* __restrict__ o_dv = a.dv + tio;
 #pragma unroll
@@ -655,13 +657,21 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   }
   __syncthreads();
 
-  // Global operands of the gate phase: the dWp operand of the dkb chain depends on the k
-  // block only (loaded once); each tile's other operands are loaded one tile ahead, before the
-  // current tile's stores (the memory counter is in order, so a wait on a load issued after
-  // stores would wait for them too).  The first ones are issued here, to arrive during B4.
+  // Global operands of the gate phase, all issued before the phase's first store (the memory
+  // counter is in order and covers stores too, so a load issued after a store would wait for
+  // it): here, to arrive during B4, with fp32 products; after B4 with bf16 ones, whose B4
+  // holds more registers.
   const float* __restrict__ dqgp = a.dqg + tb;
   const float* __restrict__ dkgp = a.dkg + tb;
-  float4 ndq4 = fcol4(dqgp, St::rtile(wv, 0)), ndk4 = fcol4(dkgp, St::rtile(wv, 0));
+  float4 dqg4s[NTW], dkg4s[NTW];
+  auto gate_loads = [&]() {
+#pragma unroll
+    for (int m = 0; m < NTW; ++m) {
+      dqg4s[m] = fcol4(dqgp, St::rtile(wv, m));
+      dkg4s[m] = fcol4(dkgp, St::rtile(wv, m));
+    }
+  };
+  if constexpr (B3 == DOT_HIGHEST) gate_loads();
 
   // B4: VJP of the two-level scores on the owned tiles (b4.py:45-97)
   f4 dq4[NTW], dbk4[NTW], dk4[NTW], dgc4[NTW];
@@ -838,18 +848,14 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   const float dlast = owned(3) && g == 3 ? a.dlast[(size_t)chunk * D + dcol] : 0.f;
   float part = 0.f, fix3 = 0.f, fix4 = 0.f;
   float dgv[NTW][4];                                 // RT_STATIC: this lane's dgc3 + dgc4
+  if constexpr (B3 != DOT_HIGHEST) gate_loads();
   static_assert(NW * 16 * TRP <= T * LT, "transpose tiles fit in the dAqk buffer");
   if constexpr (!RT_STATIC) __syncthreads();
   float* tr = sDAq + wv * 16 * TRP;
 #pragma unroll
   for (int m = 0; m < NTW; ++m) {
     const int rt = St::rtile(wv, m), i0 = 16 * rt + 4 * g;
-    const float4 dqg4 = ndq4, dkg4 = ndk4;
-    if (m + 1 < NTW) {
-      const int rn = St::rtile(wv, m + 1);
-      ndq4 = fcol4(dqgp, rn);
-      ndk4 = fcol4(dkgp, rn);
-    }
+    const float4 dqg4 = dqg4s[m], dkg4 = dkg4s[m];
     f4 dkb = {0.f, 0.f, 0.f, 0.f};
     // straight-line MFMA chain: skip the zero k blocks only where rt is a compile-time value
     auto acol = [&](int kb) {

@@ -281,6 +281,9 @@ __device__ __forceinline__ float4 ldg4(const float* p) {
   return make_float4(v[0], v[1], v[2], v[3]);
 }
 __device__ __forceinline__ float4 in_ldg4(const float* p) { return ldg4(p); }
+// s_waitcnt vmcnt(0) with the other counters left alone (gfx9 encoding: vmcnt [3:0] and
+// [15:14], expcnt [6:4] = 7, lgkmcnt [11:8] = 15)
+constexpr int WAIT_VMCNT0 = 0x0F70;
 __device__ __forceinline__ float4 in_ldg4(const uint16_t* p) {
   const u2v u = __builtin_nontemporal_load(reinterpret_cast<const u2v*>(p));
   return make_float4(__uint_as_float(u[0] << 16), __uint_as_float(u[0] & 0xffff0000u), __uint_as_float(u[1] << 16),
