@@ -358,9 +358,10 @@ __global__ __launch_bounds__(NWW * WAVE) __attribute__((amdgpu_waves_per_eu(2)))
 // ------------------------------------------------------------------------------------
 template <int D>
 struct BwdWyLayout {
+  // X1 and X2 (T x LD each) are arrays of their own (X2 rounded up to whole DMA windows for the
+  // persistent kernel, which fills both by LDS DMA).
   static constexpr int LD = D + 4, LT = T + 4;
-  static constexpr int OFF_G = 0, OFF_X1 = T * LD, OFF_X2 = 2 * T * LD;
-  static constexpr int OFF_A = 3 * T * LD, OFF_DAQ = OFF_A + T * LT, OFF_DA = OFF_DAQ + T * LT;
+  static constexpr int OFF_G = 0, OFF_A = T * LD, OFF_DAQ = OFF_A + T * LT, OFF_DA = OFF_DAQ + T * LT;
   static constexpr int OFF_COL = OFF_DA + T * LT;
   static constexpr int TOTAL = OFF_COL + 8 * 16;
 };
@@ -393,25 +394,37 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   using Lay = BwdWyLayout<D>;
   using St = Strip<D>;
   constexpr int LD = Lay::LD, LT = Lay::LT, NT = 512, NW = 8, NTW = St::NTW, NKB = D / 16;
+  // RT_STATIC: every wave owns a whole column strip (D = 128), rt == m for every wave.
+  // PERSIST: one workgroup per CU walks the chunks blockIdx.x, + gridDim.x, ...; the next
+  // chunk's prologue operands are fetched during this chunk's B4 and gate phase (below).
+  // Other instantiations run the body once (one workgroup per chunk).
+  constexpr bool RT_STATIC = St::NS == NW, PERSIST = RT_STATIC && !LEAN;
+  // X2 as DMA windows of 256 floats, a whole number per wave (the tail past T x LD is slack)
+  constexpr int X2_WIN = PERSIST ? (T * LD / 256 + NW - 1) / NW * NW : (T * LD + 255) / 256;
   __shared__ __attribute__((aligned(16))) float smem[Lay::TOTAL];
+  __shared__ __attribute__((aligned(16))) float sX1[T * LD];
+  __shared__ __attribute__((aligned(16))) float sX2[X2_WIN * 256];
   float* sG = smem + Lay::OFF_G;
-  float* sX1 = smem + Lay::OFF_X1;
-  float* sX2 = smem + Lay::OFF_X2;
   float* sA = smem + Lay::OFF_A;
   float* sDAq = smem + Lay::OFF_DAQ;
   float* sDA = smem + Lay::OFF_DA;
   float* sColP = smem + Lay::OFF_COL;
-  const Cfg& cf = a.cfg;
+  constexpr int NIT = T * D / 4 / NT, NIA = T * T / 4 / NT;
+  float4 xa[NIA], xg[4];                            // PERSIST: next chunk's A and g column
+  const BwdWyArgs& a0 = a;
+
+  for (int chunk = blockIdx.x, first = 1; first || (PERSIST && chunk < a0.n_chunks); chunk += gridDim.x, first = 0) {
+  // In the loop the arguments are read through an opaque pointer to the kernel argument block
+  // and the lane indices come from an opaque copy of threadIdx.x, both fresh in every
+  // iteration: the argument pointers and the many lane-dependent addresses are then recomputed
+  // where they are used, instead of being hoisted out of the loop and held in registers.
+  const auto& a = *kernarg_fresh<BwdWyArgs>(PERSIST);
+  const auto& cf = a.cfg;
   const float clip = cf.clip, scale = cf.scale;
-  const int chunk = blockIdx.x, tid = threadIdx.x, wv = wave_id(), l = lane_id(), r = l & 15, g = l >> 4;
-  const size_t tb = (size_t)chunk * T * D, sb = (size_t)chunk * T * T, tio = io_off<D>(cf, chunk);
-  const float* __restrict__ q = a.q + tio;
-  const float* __restrict__ k = a.k + tio;
-  const float* __restrict__ b = a.b + tio;
-  const float* __restrict__ w = a.w + tio;
-  const float* __restrict__ v = a.v + tio;
-  const float* __restrict__ dout = a.dout + tio;
-  const float* __restrict__ dwp = a.dwp + tb;
+  int tid_;
+  asm volatile("" : "=v"(tid_) : "0"((int)threadIdx.x));
+  const int tid = tid_ & (NT - 1);                  // the range the optimiser knew for threadIdx.x
+  const int wv = __builtin_amdgcn_readfirstlane(tid / WAVE), l = tid & (WAVE - 1), r = l & 15, g = l >> 4;
   const int strip = St::strip(wv), dcol = 16 * strip + r;
   auto owned = [&](int t) { return t >= St::rtile(wv, 0) && (t - St::rtile(wv, 0)) % St::STEP == 0; };
 
@@ -425,7 +438,6 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
 
   // Item f of a row-major input is float4 f; item f of a FRAG(x^T) (v_new, dWp) or FRAG(x)
   // (dv_new) input is float4 f as well, placed into the row-major tile by put_fragT / put_frag.
-  constexpr int NIT = T * D / 4 / NT, NIA = T * T / 4 / NT;
   auto put_frag = [&](float* dst, const float4& x, int f) {
     const int lane = f & 63, blk = f >> 6;
     st4(dst + (16 * (blk / NKB) + (lane & 15)) * LD + 16 * (blk % NKB) + 4 * (lane >> 4), x);
@@ -439,9 +451,87 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     dst[(m + 3) * LD + n] = x.w;
   };
 
+  // PERSIST prologue operands of a chunk, fetched while the previous chunk is in B4:
+  //   v_new -> X1 by LDS DMA (global_load_lds_dwordx4, no registers): its 32 fragment blocks
+  //     FA(v_new^T) as they are stored, except that within a block quad q (lane q of the
+  //     fragment) lands in slot sig(q) = (q & 48) | ((q + (q >> 4)) & 15), which makes P1's
+  //     gathers of v_new rows free of bank conflicts (vnb below);
+  //   dO -> X2 by LDS DMA in the padded row-major layout: X2 is X2_WIN windows of 256 floats,
+  //     five per wave, lane i of window u fetches the quad at float 256 u + 4 i, and a quad in
+  //     a row's padding or past the last row fetches row 0 (never read); every wave issues the
+  //     same number of DMAs, so the compiler can count them in its waits;
+  //   A and this lane's g column (the in-wave cumsum below) in registers.
+  static_assert((D / 16) * (T / 16) % NW == 0 && X2_WIN * 256 >= T * LD, "DMA windows");
+  auto fetch_dma = [&](int ch) {
+    const float* vsrc = a.v_new_f + (size_t)ch * T * D;
+    const size_t cio = io_off<D>(cf, ch);
+    const int qi = (l & 48) | (((l & 15) - (l >> 4)) & 15);        // sig^-1(lane)
+#pragma unroll
+    for (int j = 0; j < (D / 16) * (T / 16) / NW; ++j) {
+      const int blk = wv + NW * j;
+      lds_dma16(vsrc + blk * 256 + 4 * qi, sX1 + blk * 256);
+    }
+#pragma unroll
+    for (int j = 0; j < X2_WIN / NW; ++j) {
+      const int u = wv + NW * j, f = 256 * u + 4 * l, row = f / LD, col = f - row * LD;
+      lds_dma16(a.dout + cio + (row < T && col < D ? row * D + col : 0), sX2 + 256 * u);
+    }
+  };
+  auto fetch_regs = [&](int ch) {
+    const size_t cio = io_off<D>(cf, ch);
+#pragma unroll
+    for (int it = 0; it < NIA; ++it) xa[it] = ldg4(a.A + (size_t)ch * T * T + 4 * (tid + it * NT));
+    const float* gp = a.g + cio + 4 * g * D + dcol;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) xg[t] = make_float4(gp[16 * t * D], gp[(16 * t + 1) * D], gp[(16 * t + 2) * D], gp[(16 * t + 3) * D]);
+  };
+  if constexpr (PERSIST) {
+    if (first) fetch_dma(chunk);
+    fetch_regs(chunk);
+  }
+  const size_t tb = (size_t)chunk * T * D, sb = (size_t)chunk * T * T, tio = io_off<D>(cf, chunk);
+  const float* __restrict__ q = a.q + tio;
+  const float* __restrict__ k = a.k + tio;
+  const float* __restrict__ b = a.b + tio;
+  const float* __restrict__ w = a.w + tio;
+  const float* __restrict__ v = a.v + tio;
+  const float* __restrict__ dout = a.dout + tio;
+  const float* __restrict__ dwp = a.dwp + tb;
+  const int next = chunk + gridDim.x;
+
   // X1 = v_new, X2 = dO, sA = A, sG = gc.  Every load is issued before the cumsum waits for
   // its g: one memory round trip for the whole prologue.
-  {
+  if constexpr (PERSIST) {
+    // A from registers; gc of this wave's columns by an in-wave cumsum that adds in the order
+    // chunk_cumsum does (runs of four rows, then the totals of the runs above in order), so gc
+    // is bit-identical to every other kernel's.  Run s = 4 t + g is this lane's row tile t.
+#pragma unroll
+    for (int it = 0; it < NIA; ++it) {
+      const int f = tid + it * NT;
+      st4(sA + (f >> 4) * LT + 4 * (f & 15), xa[it]);
+    }
+    float xr[4][4], offt[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      xr[t][0] = xg[t].x;
+      xr[t][1] = xr[t][0] + xg[t].y;
+      xr[t][2] = xr[t][1] + xg[t].z;
+      xr[t][3] = xr[t][2] + xg[t].w;
+    }
+    float run = 0.f;
+#pragma unroll
+    for (int s2 = 0; s2 < 16; ++s2) {
+      const int t2 = s2 >> 2, g2 = s2 & 3;
+      offt[t2] = g == g2 ? run : offt[t2];
+      run = run + __shfl(xr[t2][3], r + 16 * g2);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sG[(16 * t + 4 * g + e) * LD + dcol] = offt[t] + xr[t][e];
+    // the first chunk's DMA (later chunks' are waited for after B4)
+    if (first) __builtin_amdgcn_s_waitcnt(WAIT_VMCNT0);
+  } else {
     float4 xvn[NIT], xdo[NIT], xa[NIA];
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
@@ -494,12 +584,21 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     const int t = wv + NW * m2, ti = t >> 2, tj = t & 3;
     const float* ar = sX2 + (16 * ti + r) * LD + 4 * g;
     const float* br = sX1 + (16 * tj + r) * LD + 4 * g;
+    // B operand v_new[16 tj + r][16 kb + 4 g + e]: row-major X1, or (PERSIST) the swizzled
+    // fragment blocks: lane q = 4 g + e + 16 (r >> 2), element r & 3 of block (kb, tj)
+    const float* bq = sX1 + 64 * (r >> 2) + (r & 3);
+    auto vnb = [&](int kb) {
+      if constexpr (!PERSIST) return ld4(br + 16 * kb);
+      const float* p = bq + (4 * kb + tj) * 256;
+      return make_float4(p[4 * ((4 * g + (r >> 2)) & 15)], p[4 * ((4 * g + 1 + (r >> 2)) & 15)],
+                         p[4 * ((4 * g + 2 + (r >> 2)) & 15)], p[4 * ((4 * g + 3 + (r >> 2)) & 15)]);
+    };
     f4 acc = {0.f, 0.f, 0.f, 0.f};
     constexpr int KSTEP = B3 == DOT_HIGHEST ? 1 : 2;      // bf16: two k blocks per MFMA
 #pragma unroll
     for (int kb = 0; kb < NKB; kb += KSTEP) {
-      if constexpr (KSTEP == 1) mma16<B3>(acc, ld4(ar + 16 * kb), ld4(br + 16 * kb));
-      else mma32<B3>(acc, ld4(ar + 16 * kb), ld4(br + 16 * kb), ld4(ar + 16 * kb + 16), ld4(br + 16 * kb + 16));
+      if constexpr (KSTEP == 1) mma16<B3>(acc, ld4(ar + 16 * kb), vnb(kb));
+      else mma32<B3>(acc, ld4(ar + 16 * kb), vnb(kb), ld4(ar + 16 * kb + 16), vnb(kb + 1));
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int sl = m2 * NKB + kb; sl < m2 * NKB + kb + KSTEP; ++sl)
@@ -566,7 +665,6 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   // dwv = A^T dv_new on the owned tiles (mega.py:42; A^T is upper triangular, so row tile rt
   // only sees k blocks >= rt).  It needs no B4 result, so dw and dv leave before B4 (their
   // stores overlap P3 / P4 / B4) and the gate phase keeps only the dkb chain.
-  constexpr bool RT_STATIC = St::NS == NW;            // rt == m for every wave
   f4 dwv[NTW];
 #pragma unroll
   for (int m = 0; m < NTW; ++m) {
@@ -656,6 +754,11 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     for (int e = 0; e < 4; ++e) sDA[(16 * ti + 4 * g + e) * LT + 16 * tj + r] = ov[e];
   }
   __syncthreads();
+
+  // PERSIST: X1 and X2 are free from here on; the next chunk's v_new and dO start now, to
+  // land during B4, and are waited for after it.
+  if constexpr (PERSIST)
+    if (next < a.n_chunks) fetch_dma(next);
 
   // Global operands of the gate phase, all issued before the phase's first store (the memory
   // counter is in order and covers stores too, so a load issued after a store would wait for
@@ -781,7 +884,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     b4_piece(P2);
   } else {
     for (int pi = 0; pi < cf.pieces.n; ++pi) {
-      const Piece pc = cf.pieces.p[pi];
+      const Piece pc = load_piece(cf.pieces.p[pi]);
       if (pc.kind == 1 && lean) continue;
       b4_piece(pc);
     }
@@ -790,7 +893,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   // lean diagonal blocks (b4.py:20-30): exact E = exp(clip(gc_i - gc_j, +-diff_clip)) per element
   if constexpr (LEAN) {
     for (int pi = 0; pi < cf.pieces.n; ++pi) {
-      const Piece pc = cf.pieces.p[pi];
+      const Piece pc = load_piece(cf.pieces.p[pi]);
       if (pc.kind != 1) continue;
       const float dc = cf.diff_clip;
 #pragma unroll
@@ -829,6 +932,11 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
       }
     }
   }
+
+  // PERSIST: the next chunk's DMA has had B4 to land; it is waited for here (the compiler
+  // does not know of it) and published by the barrier that ends the chunk.  A and g of a chunk
+  // are loaded into registers at its start (held across the loop they would spill).
+  if constexpr (PERSIST) __builtin_amdgcn_s_waitcnt(WAIT_VMCNT0);
 
   // per owned tile: dkb = A^T dWp (mega.py:42; A^T is upper triangular, so row tile rt only
   // sees k blocks >= rt), then the gate gradients (mega.py:45-51) and the
@@ -949,7 +1057,9 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
       for (int e = 0; e < 4; ++e) o_dg[(16 * t + 4 * g + e) * D + dcol] = sanitize(x[e] + off, clip);
       later += tot;
     }
-    return;
+    // every wave is done with sA before the next chunk's A is written there
+    if constexpr (PERSIST) __syncthreads();
+    continue;
   }
   if (g == 0) sColP[wv * 16 + r] = part;
   __syncthreads();
@@ -979,6 +1089,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     for (int s2 = NSEG - 1; s2 > sg; --s2) off = add4(off, ld4(sTot + s2 * LD + d));
 #pragma unroll
     for (int i = 0; i < RUN; ++i) stg4(a.dg + tio + (sg * RUN + i) * D + d, san4(add4(x[i], off), clip));
+  }
   }
 }
 
@@ -1106,13 +1217,19 @@ static bool std_pieces(const PieceList& pl) {
 
 hipError_t launch_bwd_wy(int D, const BwdWyArgs& a, hipStream_t s) {
   const bool lean = a.cfg.diag == DIAG_LEAN, std_geom = !lean && std_pieces(a.cfg.pieces);
+  // D = 128 BTL kernels are persistent: one workgroup per CU (their LDS admits no second).
+  int dev = 0, ncu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu < 1)
+    return hipErrorInvalidDevice;
+  const dim3 pgrid(a.n_chunks < ncu ? a.n_chunks : ncu);
   dispatch_mode(a.cfg.b3_mode, [&](auto m) {
     constexpr int M = decltype(m)::value;
     const dim3 grid(a.n_chunks), block(512);
     if (D == 128) {
       if (lean) hipLaunchKernelGGL((bwd_wy_kernel<128, M, false, true>), grid, block, 0, s, a);
-      else if (std_geom) hipLaunchKernelGGL((bwd_wy_kernel<128, M, true, false>), grid, block, 0, s, a);
-      else hipLaunchKernelGGL((bwd_wy_kernel<128, M, false, false>), grid, block, 0, s, a);
+      else if (std_geom) hipLaunchKernelGGL((bwd_wy_kernel<128, M, true, false>), pgrid, block, 0, s, a);
+      else hipLaunchKernelGGL((bwd_wy_kernel<128, M, false, false>), pgrid, block, 0, s, a);
     } else {
       if (lean) hipLaunchKernelGGL((bwd_wy_kernel<64, M, false, true>), grid, block, 0, s, a);
       else if (std_geom) hipLaunchKernelGGL((bwd_wy_kernel<64, M, true, false>), grid, block, 0, s, a);

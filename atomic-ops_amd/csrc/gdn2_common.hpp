@@ -281,6 +281,28 @@ __device__ __forceinline__ float4 ldg4(const float* p) {
   return make_float4(v[0], v[1], v[2], v[3]);
 }
 __device__ __forceinline__ float4 in_ldg4(const float* p) { return ldg4(p); }
+// LDS DMA (gfx950 global_load_lds_dwordx4): lane i of the wave fetches the 16 bytes at its own
+// global address src into LDS at dst + 4 i floats (dst wave-uniform, 16-byte aligned).  No
+// registers are involved.  Issued from inline asm, so the compiler does not know of it: it
+// neither holds later LDS accesses for it (it cannot tell which LDS it writes) nor counts it in
+// its own waits (which then only wait longer: memory operations complete in order).  The
+// caller waits for it (s_waitcnt vmcnt(0)) and publishes it with a barrier.  It sets M0, which
+// the compiler reserves but does not use in the kernels that call this (no other LDS DMA, GWS
+// or message instruction), so the clobber is safe there.
+__device__ __forceinline__ void lds_dma16(const float* src, float* dst) {
+  const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)dst;
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds) : "memory", "m0");
+}
+// The kernel's argument block (its first and only explicit argument, at offset 0 of the
+// kernarg segment) seen through a pointer that is opaque to the optimiser when FRESH: loads
+// through it cannot be hoisted out of a loop, so a persistent kernel re-reads (scalar loads)
+// each argument where it is used instead of holding them all in SGPRs across the loop.
+template <typename A>
+__device__ __forceinline__ const __attribute__((address_space(4))) A* kernarg_fresh(bool fresh) {
+  auto p = (const __attribute__((address_space(4))) A*)__builtin_amdgcn_kernarg_segment_ptr();
+  if (fresh) asm volatile("" : "+s"(p));
+  return p;
+}
 // s_waitcnt vmcnt(0) with the other counters left alone (gfx9 encoding: vmcnt [3:0] and
 // [15:14], expcnt [6:4] = 7, lgkmcnt [11:8] = 15)
 constexpr int WAIT_VMCNT0 = 0x0F70;

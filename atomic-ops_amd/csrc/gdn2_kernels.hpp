@@ -18,6 +18,21 @@ struct PieceList {
   Piece p[MAX_PIECES];
   int n;
 };
+// A Piece read field by field, also from the kernel argument block seen in its own address
+// space (kernarg_fresh), where the implicit copy does not apply.
+template <typename P>
+__device__ __forceinline__ Piece load_piece(const P& s) {
+  Piece p;
+  p.row0 = s.row0;
+  p.col0 = s.col0;
+  p.P = s.P;
+  p.kind = s.kind;
+  p.anchor = s.anchor;
+  p.s0 = s.s0;
+  p.s1 = s.s1;
+  p.pad = s.pad;
+  return p;
+}
 
 struct Cfg {
   float scale, wy_eps, ome, clip, diff_clip;   // ome = 1 - wy_eps, rounded once on the host
@@ -41,8 +56,8 @@ struct Cfg {
 // Offset in floats of a chunk (index (b, h) * nc + chunk of the segment) in a raw operator
 // tensor -- q..g, o, dO and the input gradients, (B, H, seq_ld, D) with the segment starting at
 // the pointer passed in.  Per-segment buffers (residual, workspace) are chunk-contiguous.
-template <int D>
-__device__ __forceinline__ size_t io_off(const Cfg& c, int chunk) {
+template <int D, typename C>
+__device__ __forceinline__ size_t io_off(const C& c, int chunk) {
   const int bh = chunk / c.nc, cc = chunk - bh * c.nc;
   return ((size_t)bh * c.seq_ld + (size_t)cc * T) * D;
 }
