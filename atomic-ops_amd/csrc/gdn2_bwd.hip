@@ -1218,11 +1218,9 @@ static bool std_pieces(const PieceList& pl) {
 hipError_t launch_bwd_wy(int D, const BwdWyArgs& a, hipStream_t s) {
   const bool lean = a.cfg.diag == DIAG_LEAN, std_geom = !lean && std_pieces(a.cfg.pieces);
   // D = 128 BTL kernels are persistent: one workgroup per CU (their LDS admits no second).
-  int dev = 0, ncu = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu < 1)
-    return hipErrorInvalidDevice;
-  const dim3 pgrid(a.n_chunks < ncu ? a.n_chunks : ncu);
+  dim3 pgrid;
+  const hipError_t e = persistent_grid(a.n_chunks, &pgrid);
+  if (e != hipSuccess) return e;
   dispatch_mode(a.cfg.b3_mode, [&](auto m) {
     constexpr int M = decltype(m)::value;
     const dim3 grid(a.n_chunks), block(512);

@@ -150,6 +150,18 @@ struct BwdWyArgs {
 };
 
 hipError_t launch_wy_fwd(int D, const WyFwdArgs& a, hipStream_t s, bool bf16_inputs = false);
+
+// Grid of a persistent kernel (one workgroup per CU, each walking chunks blockIdx.x,
+// + gridDim.x, ...): min(n_chunks, CUs of the current device).
+inline hipError_t persistent_grid(int n_chunks, dim3* grid) {
+  int dev = 0, ncu = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return e;
+  if (ncu < 1) return hipErrorInvalidDevice;
+  *grid = dim3(n_chunks < ncu ? n_chunks : ncu);
+  return hipSuccess;
+}
 hipError_t launch_scan_fwd(int D, const ScanFwdArgs& a, hipStream_t s);
 hipError_t launch_out_fwd(int D, const OutFwdArgs& a, hipStream_t s);
 hipError_t launch_bwd_pre(int D, const BwdPreArgs& a, hipStream_t s);
