@@ -724,8 +724,8 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   for (int it = 0; it < NIT; ++it) {
     const int f = tid + it * NT, i = f / (D / 4), d = 4 * (f % (D / 4));
     const float4 x = ld4(sX1 + i * LD + d);
-    st4(o_dw + i * D + d, san4(mul4(x, xv[it]), clip));
-    st4(o_dv + i * D + d, san4(mul4(x, xw[it]), clip));
+    stg4(o_dw + i * D + d, san4(mul4(x, xv[it]), clip));
+    stg4(o_dv + i * D + d, san4(mul4(x, xw[it]), clip));
   }
 
   // P4: dAkk = san(-(1-eps) A^T tmp) * strict into sDA; tiles above the diagonal are zero
@@ -946,8 +946,10 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   // accumulator layout (four rows of 64 contiguous bytes per instruction), and the column sum
   // and B5 stay inside the wave, so no barrier follows P4.  Otherwise two waves share a
   // column: the tiles leave through a per-wave 16x16 LDS transpose (in the dAqk buffer, free
-  // once every wave has left B4), dgc goes to X1 and B5 runs over the workgroup.  Plain
-  // stores: streaming stores complete later, and the next tile's load waits would cover them.
+  // once every wave has left B4), dgc goes to X1 and B5 runs over the workgroup.  Every
+  // gradient store is a streaming (non-temporal) one: no load is issued after them in this
+  // chunk, and written lines that skip the cache drain faster before the next chunk's loads
+  // (measured: 143 -> 128 us in one probe pair).
   float* __restrict__ o_dq = a.dq + tio;
   float* __restrict__ o_dk = a.dk + tio;
   float* __restrict__ o_db = a.db + tio;
@@ -1016,16 +1018,16 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     if constexpr (RT_STATIC) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        o_dq[(i0 + e) * D + dcol] = oq[e];
-        o_dk[(i0 + e) * D + dcol] = ok[e];
-        o_db[(i0 + e) * D + dcol] = ob[e];
+        __builtin_nontemporal_store(oq[e], o_dq + (i0 + e) * D + dcol);
+        __builtin_nontemporal_store(ok[e], o_dk + (i0 + e) * D + dcol);
+        __builtin_nontemporal_store(ob[e], o_db + (i0 + e) * D + dcol);
       }
     } else {
       // lane (r, g) after the transpose: row 16 rt + r, columns 16 strip + 4 g .. + 3
       const int ro = (16 * rt + r) * D + 16 * strip + 4 * g;
-      st4(o_dq + ro, wave_transpose16(tr, make_float4(oq[0], oq[1], oq[2], oq[3]), r, g));
-      st4(o_dk + ro, wave_transpose16(tr, make_float4(ok[0], ok[1], ok[2], ok[3]), r, g));
-      st4(o_db + ro, wave_transpose16(tr, make_float4(ob[0], ob[1], ob[2], ob[3]), r, g));
+      stg4(o_dq + ro, wave_transpose16(tr, make_float4(oq[0], oq[1], oq[2], oq[3]), r, g));
+      stg4(o_dk + ro, wave_transpose16(tr, make_float4(ok[0], ok[1], ok[2], ok[3]), r, g));
+      stg4(o_db + ro, wave_transpose16(tr, make_float4(ob[0], ob[1], ob[2], ob[3]), r, g));
     }
   }
   // last-row decay gradient: sum over all rows of the column (lanes g, then the waves of the
@@ -1054,7 +1056,8 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
       const float tot = __shfl(suf + s, r);          // lane g = 0: the row tile's total
       const float off = later + suf;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o_dg[(16 * t + 4 * g + e) * D + dcol] = sanitize(x[e] + off, clip);
+      for (int e = 0; e < 4; ++e)
+        __builtin_nontemporal_store(sanitize(x[e] + off, clip), o_dg + (16 * t + 4 * g + e) * D + dcol);
       later += tot;
     }
     // every wave is done with sA before the next chunk's A is written there
