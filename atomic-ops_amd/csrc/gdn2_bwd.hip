@@ -702,14 +702,22 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     for (int e = 0; e < 4; ++e) sX1[(16 * rt + 4 * g + e) * LD + dcol] = dwv[m][e];
   }
 
-  // P3: tmp = san(dA A^T) into X2 (as T x LT; dv_new is done with)
+  // P3: tmp = san(dA A^T) into X2 (as T x LT; dv_new is done with).  A is lower triangular, so
+  // column tile tj only sees k blocks <= tj; tj is wave-uniform, and a switch keeps each chain
+  // straight-line with a compile-time length.
   float* sTmp = sX2;
   for (int t = wv; t < 16; t += NW) {
     const int ti = t >> 2, tj = t & 3;
     f4 acc = {0.f, 0.f, 0.f, 0.f};
-    mma_chain<B3, 4>(acc, 0, [&](int kb) { return ld4(sDA + (16 * ti + r) * LT + 16 * kb + 4 * g); },
-                     [&](int kb) { return ld4(sA + (16 * tj + r) * LT + 16 * kb + 4 * g); });
-    drain(acc);
+    auto fa = [&](int kb) { return ld4(sDA + (16 * ti + r) * LT + 16 * kb + 4 * g); };
+    auto fb = [&](int kb) { return ld4(sA + (16 * tj + r) * LT + 16 * kb + 4 * g); };
+    // each case drains its own chain: the accumulator is read (merged at the join) only after
+    switch (tj) {
+      case 0: mma_chain<B3, 1>(acc, 0, fa, fb); drain(acc); break;
+      case 1: mma_chain<B3, 2>(acc, 0, fa, fb); drain(acc); break;
+      case 2: mma_chain<B3, 3>(acc, 0, fa, fb); drain(acc); break;
+      default: mma_chain<B3, 4>(acc, 0, fa, fb); drain(acc); break;
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) sTmp[(16 * ti + 4 * g + e) * LT + 16 * tj + r] = sanitize(acc[e], clip);
   }
@@ -733,19 +741,23 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     const int ti = t >> 2, tj = t & 3;
     float ov[4] = {0.f, 0.f, 0.f, 0.f};
     if (tj <= ti) {
-      // full k range as one straight-line chain (the blocks kb < ti of A^T are exact zeros)
+      // the blocks kb < ti of A^T are exact zeros: the chain starts at ti (wave-uniform; a
+      // switch keeps it straight-line with a compile-time start)
       f4 acc = {0.f, 0.f, 0.f, 0.f};
-      mma_chain<B3, 4>(
-          acc, 0,
-          [&](int kb) {
-            const float* ac = sA + (16 * kb + 4 * g) * LT + 16 * ti + r;
-            return make_float4(ac[0], ac[LT], ac[2 * LT], ac[3 * LT]);
-          },
-          [&](int kb) {
-            const float* tc = sTmp + (16 * kb + 4 * g) * LT + 16 * tj + r;
-            return make_float4(tc[0], tc[LT], tc[2 * LT], tc[3 * LT]);
-          });
-      drain(acc);
+      auto fa = [&](int kb) {
+        const float* ac = sA + (16 * kb + 4 * g) * LT + 16 * ti + r;
+        return make_float4(ac[0], ac[LT], ac[2 * LT], ac[3 * LT]);
+      };
+      auto fb = [&](int kb) {
+        const float* tc = sTmp + (16 * kb + 4 * g) * LT + 16 * tj + r;
+        return make_float4(tc[0], tc[LT], tc[2 * LT], tc[3 * LT]);
+      };
+      switch (ti) {
+        case 0: mma_chain<B3, 4>(acc, 0, fa, fb); drain(acc); break;
+        case 1: mma_chain<B3, 4>(acc, 1, fa, fb); drain(acc); break;
+        case 2: mma_chain<B3, 4>(acc, 2, fa, fb); drain(acc); break;
+        default: mma_chain<B3, 4>(acc, 3, fa, fb); drain(acc); break;
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         ov[e] = (16 * tj + r < 16 * ti + 4 * g + e) ? sanitize(-acc[e] * cf.ome, clip) : 0.f;
@@ -808,6 +820,10 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
       bkt[kb] = mul4(mul4(pick4(bv, ti), pick4(kv, ti)), ra[kb]);
       kt[kb] = mul4(pick4(kv, tj), cbl[kb]);
     }
+    // A piece on the diagonal (row0 == col0) of 2 x 2 tiles has its upper tile (rows of tile 0,
+    // columns of tile 1) exactly zero in dAqk (causal) and dAkk (strict): the row chain of row
+    // tile 0 and the column chain of column tile 1 skip it.
+    const bool diag_sq = pc.row0 == pc.col0;
     // rows of the piece: dq, dbk, dgc
     for (int rb = 0; rb < nb; ++rb) {
       const int ti = tr0 + rb;
@@ -815,7 +831,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
       f4 dqt = {0.f, 0.f, 0.f, 0.f}, dbt = {0.f, 0.f, 0.f, 0.f};
       const float* pq = sDAq + (16 * ti + r) * LT + pc.col0 + 4 * g;
       const float* pk = sDA + (16 * ti + r) * LT + pc.col0 + 4 * g;
-      if (nb == 2) {          // whole chains per branch, each ending in drain()
+      if (nb == 2 && !(diag_sq && rb == 0)) {          // whole chains per branch, each ending in drain()
         mma16<DOT_HIGHEST>(dqt, ld4(pq), kt[0]);
         mma16<DOT_HIGHEST>(dbt, ld4(pk), kt[0]);
         mma16<DOT_HIGHEST>(dqt, ld4(pq + 16), kt[1]);
@@ -850,7 +866,11 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
         const float* p = base + (pc.row0 + 16 * kb + 4 * g) * LT + 16 * tj + r;
         return make_float4(p[0], p[LT], p[2 * LT], p[3 * LT]);
       };
-      if (nb == 2) {
+      if (nb == 2 && diag_sq && cb == 1) {
+        mma16<DOT_HIGHEST>(k1, colop(sDAq, 1), qt[1]);
+        mma16<DOT_HIGHEST>(k2, colop(sDA, 1), bkt[1]);
+        drain(k1, k2);
+      } else if (nb == 2) {
         mma16<DOT_HIGHEST>(k1, colop(sDAq, 0), qt[0]);
         mma16<DOT_HIGHEST>(k2, colop(sDA, 0), bkt[0]);
         mma16<DOT_HIGHEST>(k1, colop(sDAq, 1), qt[1]);
