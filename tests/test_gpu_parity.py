@@ -244,6 +244,19 @@ def test_grad_vs_forward_ref(small_cfg, name, seed, g, k, b, dom):
     compare(hip, kernel_oracle(cfg, 1 / 8.0, arrs), 1e-4, NAMES)
 
 
+@pytest.mark.parametrize("name,seed,g,k,b,dom", DOMAIN[4:])
+def test_grad_other_domain_seeds(small_cfg, name, seed, g, k, b, dom):
+    """The in-domain recipes of tests_gdn2/conftest.py:6-13 that T5 does not run (b close to 1,
+    large stable k), through the HIP operator against the float64 oracle, at T5's size and gate,
+    and against the kernel-semantics oracle at 1e-4."""
+    banner(f"T5-style {name}")
+    arrs = mk_inputs(1, 128, 1, 64, seed, g, k, b, layout="bhld")
+    cfg = small_cfg.with_(g_max=1e3, bs2=32, wy_eps=0.0)
+    hip = hip_grad(cfg, 1 / 8.0, arrs)
+    compare(hip, oracle_grad(cfg, 1 / 8.0, arrs), 3e-3, ("o", "h_final") + NAMES)
+    compare(hip, kernel_oracle(cfg, 1 / 8.0, arrs), 1e-4, NAMES)
+
+
 def test_forward_matches_token_serial(small_cfg):
     from oracle import gdn2_oracle as O
     banner("T5 token serial")
