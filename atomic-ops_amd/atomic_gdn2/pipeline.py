@@ -52,6 +52,10 @@ def _check_inputs(ts, names):
     q = ts[0]
     if q.dim() != 4:
         raise ValueError(f"expected (B,H,L,D) inputs, got q.shape={tuple(q.shape)}")
+    if q.numel() == 0:
+        # the reference's segment loop has nothing to concatenate at L = 0 and fails there
+        # (pipeline.py:57-64); the kernels need at least one chunk of one sequence
+        raise ValueError(f"empty input q.shape={tuple(q.shape)}: B, H, L and D must be positive")
     for t, n in zip(ts, names):
         if t.shape != q.shape:
             raise ValueError(f"{n}.shape={tuple(t.shape)} differs from q.shape={tuple(q.shape)}")

@@ -95,6 +95,8 @@ def test_residual_layout_and_workspaces():
     (dict(D=96), "D in"),
     (dict(bs2=8, g_max=20.0), "bs2 >= 16"),
     (dict(L=2000), "divisible"),
+    (dict(L=0), "non-positive"),
+    (dict(B=0), "non-positive"),
 ])
 def test_descriptor_validation(kw, msg):
     from atomic_gdn2 import _lib
@@ -149,6 +151,21 @@ def test_python_boundary_errors():
         fn(y, y, y, y, y, y)
     with pytest.raises(ValueError, match="shape"):
         fn(y, y, y, y, y, torch.zeros(1, 1, 128, 32))
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 0, 64), (0, 2, 128, 64), (1, 0, 128, 64)])
+def test_empty_inputs_rejected(shape):
+    """An empty batch, head or sequence axis is a ValueError at the Python boundary, with or
+    without gradients, before any device work (the C ABI's own check of such a descriptor is in
+    test_descriptor_validation)."""
+    from atomic_gdn2 import make_cfg, make_blr_trainable
+    fn = make_blr_trainable(make_cfg(bt=64, bc=32, score_bs=64, bs2=32), 0.125)
+    x = torch.zeros(shape)
+    with pytest.raises(ValueError, match="empty input"):
+        fn(x, x, x, x, x, x)
+    xg = [torch.zeros(shape, requires_grad=True) for _ in range(6)]
+    with pytest.raises(ValueError, match="empty input"):
+        fn(*xg)
 
 
 def test_synthetic_inputs_recipe():
