@@ -24,7 +24,8 @@ RES_STORAGE = {"aqk": ("T", "T", True, False), "A": ("T", "T", False, False),
                "h_pre": ("D", "D", True, True), "v_new": ("D", "T", True, True),
                "wpT": ("D", "T", True, True), "kg": ("T", "D", True, False),
                "qg": ("T", "D", True, False), "gl": (None, "D", False, False)}
-KERNEL_NAMES = ("wy_fwd", "scan_fwd", "scan_bwd", "bwd_state", "bwd_wy", "out_fwd", "bwd_pre", "bwd_state_rc")
+KERNEL_NAMES = ("wy_fwd", "scan_fwd", "scan_bwd", "bwd_state", "bwd_wy", "out_fwd", "bwd_pre", "bwd_state_rc",
+                "decode")
 ABI_VERSION = 2
 STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported configuration", 3: "HIP error"}
 
@@ -38,6 +39,13 @@ class Gdn2Desc(ctypes.Structure):
                 ("diag", _c_int), ("dot_mode", _c_int), ("solve_dot_mode", _c_int),
                 ("b3_dot_mode", _c_int), ("seq_ld", _c_int), ("state_ckpt", _c_int),
                 ("scale", _c_dbl), ("wy_eps", _c_dbl), ("clip", _c_dbl), ("diff_clip", _c_dbl)]
+
+
+class Gdn2DecodeDesc(ctypes.Structure):
+    """``struct gdn2_decode_desc`` (include/gdn2.h)."""
+    _fields_ = [("B", _c_int), ("H", _c_int), ("D", _c_int), ("n_tok", _c_int), ("seq_ld", _c_int),
+                ("in_dtype", _c_int), ("out_dtype", _c_int), ("state_dtype", _c_int),
+                ("fuse_prologue", _c_int), ("cap", _c_int), ("scale", _c_dbl), ("stability_tau", _c_dbl)]
 
 
 class Gdn2Error(RuntimeError):
@@ -65,13 +73,15 @@ def lib():
         L.gdn2_fwd.argtypes = [P(Gdn2Desc)] + [_vp] * 12
         L.gdn2_fwd_bf16.argtypes = [P(Gdn2Desc)] + [_vp] * 12
         L.gdn2_fwd_noalloc.argtypes = [P(Gdn2Desc)] + [_vp] * 10
+        L.gdn2_fwd_reset.argtypes = [P(Gdn2Desc), _c_int] + [_vp] * 12
+        L.gdn2_decode.argtypes = [P(Gdn2DecodeDesc)] + [_vp] * 13
         L.gdn2_bwd.argtypes = [P(Gdn2Desc)] + [_vp] * 18
         L.gdn2_wy_stage.argtypes = [P(Gdn2Desc)] + [_vp] * 15
         L.gdn2_debug_gemm.argtypes = [_c_int, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]
         L.gdn2_prof_begin.argtypes = [_c_int]
         L.gdn2_prof_end.argtypes = [P(_c_dbl), P(_c_int)]
-        for fn in ("gdn2_residual_layout", "gdn2_fwd", "gdn2_fwd_bf16", "gdn2_fwd_noalloc", "gdn2_bwd", "gdn2_wy_stage",
-                   "gdn2_debug_gemm", "gdn2_prof_begin", "gdn2_prof_end"):
+        for fn in ("gdn2_residual_layout", "gdn2_fwd", "gdn2_fwd_bf16", "gdn2_fwd_noalloc", "gdn2_fwd_reset",
+                   "gdn2_decode", "gdn2_bwd", "gdn2_wy_stage", "gdn2_debug_gemm", "gdn2_prof_begin", "gdn2_prof_end"):
             getattr(L, fn).restype = _c_int
         if L.gdn2_abi_version() != ABI_VERSION:
             raise Gdn2Error("libgdn2_hip.so ABI version mismatch")

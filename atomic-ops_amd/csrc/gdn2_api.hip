@@ -224,10 +224,11 @@ size_t gdn2_bwd_workspace_bytes(const gdn2_desc* d) {
 }  // extern "C"
 
 namespace {
-// Forward of one segment; q..g are fp32 or (bf16 = true) bfloat16 bits.
+// Forward of one segment; q..g are fp32 or (bf16 = true) bfloat16 bits.  reset: null, or (no
+// residual) one byte per (batch, head) and chunk, nonzero = zero state entering that chunk.
 int fwd_impl(const gdn2_desc* d, const void* q, const void* k, const void* v, const void* w, const void* b,
              const void* g, bool bf16, const float* h0, float* o, float* h_final, void* residual,
-             void* workspace, void* stream) {
+             void* workspace, void* stream, const uint8_t* reset = nullptr) {
   int st = residual ? validate_residual(d) : validate(d);
   if (st) return st;
   if (!q || !k || !v || !w || !b || !g || !o || !h_final || !workspace)
@@ -279,7 +280,7 @@ int fwd_impl(const gdn2_desc* d, const void* q, const void* k, const void* v, co
   const int ck = eff_ckpt(d);
   const bool fused_out = !residual || ck > 0;
   gdn2::ScanFwdArgs sa{wp, kgT, uT, gl, h0, qg, aqk, h_final, fused_out ? o : nullptr, hpre, vnew,
-                       (int)x.nc, (int)x.n_bh, ck, cfg};
+                       (int)x.nc, (int)x.n_bh, ck, cfg, reset};
   e = timed(1, s, [&] { return gdn2::launch_scan_fwd(d->D, sa, s); });
   if (e != hipSuccess) return hip_fail(e, "scan_fwd launch");
   if (!fused_out) {
@@ -303,6 +304,39 @@ int gdn2_fwd_bf16(const gdn2_desc* d, const uint16_t* q, const uint16_t* k, cons
                   const uint16_t* w, const uint16_t* b, const uint16_t* g, const float* h0, float* o,
                   float* h_final, void* residual, void* workspace, void* stream) {
   return fwd_impl(d, q, k, v, w, b, g, true, h0, o, h_final, residual, workspace, stream);
+}
+
+int gdn2_decode(const gdn2_decode_desc* d, const void* q, const void* k, const void* v, const void* w,
+                const void* b, const void* g, const float* a_log, const float* dt_bias, const uint8_t* reset,
+                const void* state_in, void* o, void* state_out, void* stream) {
+  if (!d) return fail(GDN2_ERR_INVALID, "null descriptor");
+  if (d->B < 1 || d->H < 1 || d->n_tok < 1) return fail(GDN2_ERR_INVALID, "non-positive shape");
+  if ((int64_t)d->B * d->H > (int64_t(1) << 22)) return fail(GDN2_ERR_UNSUPPORTED, "B*H above 4194304");
+  if (d->D != 64 && d->D != 128) return fail(GDN2_ERR_UNSUPPORTED, "D in {64, 128} only");
+  if (d->seq_ld < d->n_tok) return fail(GDN2_ERR_INVALID, "seq_ld below n_tok");
+  for (int32_t f : {d->in_dtype, d->out_dtype, d->state_dtype, d->fuse_prologue, d->cap})
+    if (f != 0 && f != 1) return fail(GDN2_ERR_INVALID, "dtype / flag fields must be 0 or 1");
+  if (!q || !k || !v || !w || !b || !g || !o || !state_out) return fail(GDN2_ERR_INVALID, "null tensor pointer");
+  if (d->fuse_prologue && (!a_log || !dt_bias)) return fail(GDN2_ERR_INVALID, "fuse_prologue needs a_log and dt_bias");
+  gdn2::DecodeArgs a{};
+  a.q = q; a.k = k; a.v = v; a.w = w; a.b = b; a.g = g;
+  a.a_log = a_log; a.dt_bias = dt_bias; a.reset = reset; a.state_in = state_in;
+  a.o = o; a.state_out = state_out;
+  a.H = d->H; a.n_tok = d->n_tok; a.seq_ld = d->seq_ld;
+  a.in_bf16 = d->in_dtype; a.out_bf16 = d->out_dtype; a.state_bf16 = d->state_dtype;
+  a.fuse = d->fuse_prologue; a.cap = d->cap;
+  a.scale = (float)d->scale; a.tau = (float)d->stability_tau;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const hipError_t e = timed(8, s, [&] { return gdn2::launch_decode(d->D, a, d->B * d->H, s); });
+  if (e != hipSuccess) return hip_fail(e, "decode launch");
+  return GDN2_OK;
+}
+
+int gdn2_fwd_reset(const gdn2_desc* d, int in_dtype, const void* q, const void* k, const void* v,
+                   const void* w, const void* b, const void* g, const float* h0, const uint8_t* chunk_reset,
+                   float* o, float* h_final, void* workspace, void* stream) {
+  if (in_dtype != 0 && in_dtype != 1) return fail(GDN2_ERR_INVALID, "in_dtype must be 0 (fp32) or 1 (bf16)");
+  return fwd_impl(d, q, k, v, w, b, g, in_dtype == 1, h0, o, h_final, nullptr, workspace, stream, chunk_reset);
 }
 
 }  // extern "C"

@@ -83,11 +83,15 @@ struct WyFwdArgs {
 // FA(Aqk) and writes o (row-major T x D per chunk); otherwise out_fwd computes o.
 // ckpt = K >= 2: h_pre_f keeps only the state entering chunks c = 0, K, 2K, ... of each
 // (batch, head), as checkpoint c / K of ceil(nc / K); ckpt 0 or 1: every chunk's.
+// reset (may be null): one byte per (batch, head) and chunk, row (b, h) of nc bytes; nonzero =
+// the state entering that chunk is zero (a document boundary at the chunk's first token; at
+// chunk 0 it replaces h0).
 struct ScanFwdArgs {
   const float *wp_f, *kgT_f, *uT_f, *gl, *h0, *qg_f, *aqk_f;
   float *hf, *o, *h_pre_f, *v_new_f;    // o, h_pre_f, v_new_f may be null
   int nc, n_bh, ckpt;
   Cfg cfg;
+  const uint8_t* reset;
 };
 
 // Chunk-parallel output: o = san(s Qg h_pre + Aqk v_new), o row-major (T x D per chunk).
@@ -148,6 +152,26 @@ struct BwdWyArgs {
   int n_chunks;
   Cfg cfg;
 };
+
+// Token recurrence for serving (gdn2_decode.hip): n_tok tokens per (batch, head) in order.
+// q..g (and o) at ((b H + h) seq_ld + t) D + d, fp32 or bfloat16 bits (in_bf16 / out_bf16);
+// state_in / state_out (B, H, D, D) row-major (key, value) in the state dtype (state_bf16),
+// state_in null = zero state, state_out may equal state_in; reset: null or B x n_tok bytes,
+// nonzero = zero state entering that token of batch row b; fuse: q, k l2-normalised, b, w
+// sigmoid, g = -exp(a_log[h]) softplus(g + dt_bias[d]) in the kernel; cap: per-head Frobenius
+// cap tau on the state.
+struct DecodeArgs {
+  const void *q, *k, *v, *w, *b, *g;
+  const float *a_log, *dt_bias;
+  const uint8_t* reset;
+  const void* state_in;
+  void *o, *state_out;
+  int H, n_tok, seq_ld;
+  int in_bf16, out_bf16, state_bf16, fuse, cap;
+  float scale, tau;
+};
+
+hipError_t launch_decode(int D, const DecodeArgs& a, int n_bh, hipStream_t s);
 
 hipError_t launch_wy_fwd(int D, const WyFwdArgs& a, hipStream_t s, bool bf16_inputs = false);
 

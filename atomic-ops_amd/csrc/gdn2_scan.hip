@@ -85,11 +85,14 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
   constexpr bool OWNS = V || NH == 8;           // keeps key tile w of the state (w < NH)
   auto base = [&](int c) { return (size_t)bh * nc + (c < nc ? c : nc - 1); };   // clamped chunk
 
+  // a set reset byte zeroes the state entering that chunk (wave-uniform: one byte per chunk)
+  auto reset_at = [&](int c) { return a.reset != nullptr && c < nc && a.reset[(size_t)bh * nc + c] != 0; };
   f4 h = {0.f, 0.f, 0.f, 0.f};
   if (OWNS) {
+    if (a.h0 && !reset_at(0)) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      h[e] = a.h0 ? a.h0[(size_t)bh * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r] : 0.f;
+      for (int e = 0; e < 4; ++e) h[e] = a.h0[(size_t)bh * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r];
+    }
     sH[w * WAVE + l] = f4_to_float4(h);
   }
 
@@ -244,7 +247,10 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
     }
     // every wave has read h_pre (window A) before the first barrier, so the new state may
     // overwrite it here
-    if (OWNS) sH[w * WAVE + l] = f4_to_float4(h);
+    if (OWNS) {
+      if (reset_at(cn)) h = f4{0.f, 0.f, 0.f, 0.f};
+      sH[w * WAVE + l] = f4_to_float4(h);
+    }
     __syncthreads();
   };
 

@@ -109,6 +109,50 @@ int gdn2_fwd_bf16(const gdn2_desc* d, const uint16_t* q, const uint16_t* k, cons
                   const uint16_t* w, const uint16_t* b, const uint16_t* g, const float* h0, float* o,
                   float* h_final, void* residual, void* workspace, void* stream);
 
+/* Forward-only prefill with document resets at chunk granularity: gdn2_fwd without a residual,
+ * q..g fp32 (in_dtype 0) or bfloat16 bits (in_dtype 1, as gdn2_fwd_bf16), and chunk_reset NULL
+ * or one byte per (batch, head, 64-token chunk), row (b*H + h) of L/64 bytes: nonzero = the
+ * state entering that chunk is zero (its first token starts a new document; at chunk 0 it
+ * replaces h0).  Replaces the chunkwise part of chunk_forward_inference in the reference's
+ * inference module (notebooks/gdn2_v031_stage2_tpu.ipynb, cell 1, INFERENCE_V031: the
+ * _cd_inference_body call with per-row segment resets).  With bt = 128 only even 64-token
+ * chunks may carry a reset.  workspace holds gdn2_fwd_workspace_bytes(d, 0). */
+int gdn2_fwd_reset(const gdn2_desc* d, int in_dtype, const void* q, const void* k, const void* v,
+                   const void* w, const void* b, const void* g, const float* h0,
+                   const uint8_t* chunk_reset, float* o, float* h_final, void* workspace,
+                   void* stream);
+
+/* Token recurrence for serving (no MFMA; see gdn2_decode). */
+typedef struct gdn2_decode_desc {
+  int32_t B, H, D;        /* D in {64, 128} */
+  int32_t n_tok;          /* tokens per (batch, head), >= 1, processed in order */
+  int32_t seq_ld;         /* tokens between consecutive (b,h) rows of q..g and o, >= n_tok */
+  int32_t in_dtype;       /* q..g: 0 fp32, 1 bfloat16 bits */
+  int32_t out_dtype;      /* o: 0 fp32, 1 bfloat16 bits */
+  int32_t state_dtype;    /* state_in / state_out: 0 fp32, 1 bfloat16 bits */
+  int32_t fuse_prologue;  /* 1: q, k raw (l2-normalised), b, w logits (sigmoid), g the raw
+                           * gate: g = -exp(a_log[h]) * softplus(g + dt_bias[d]) */
+  int32_t cap;            /* 1: cap the state's per-head Frobenius norm at stability_tau */
+  double scale;
+  double stability_tau;
+} gdn2_decode_desc;
+
+/* n_tok tokens of the recurrence per (batch, head): decode_step of the reference's inference
+ * module (INFERENCE_V031 decode_step / _decode_body) for n_tok = 1, and n_tok consecutive
+ * decode_step calls (the tail of chunk_forward_inference) otherwise.  q..g and o are
+ * (B, H, seq_ld, D) (element (b,h,t,d) at ((b*H + h)*seq_ld + t)*D + d; decode_step's (B,H,D)
+ * tensors are seq_ld = n_tok = 1); state_in / state_out (B, H, D, D) (key, value) in the state
+ * dtype; state_in NULL = zero state; state_out may equal state_in.  reset NULL or B*n_tok bytes
+ * (row b): nonzero = the state entering that token of batch row b is zero.  a_log (H) and
+ * dt_bias (D) are read only with fuse_prologue.  Per token: S = reset ? 0 : state;
+ * h = diag(e^min(g,0)) S; v_new = w*v - h^T (b*k); h += k v_new^T; o = h^T (scale*q); with cap,
+ * h *= min(1, tau / max(||h||_F, 1e-12)); NaN and +-Inf in h and o become 0; the state is
+ * rounded to the state dtype after every token, o to the output dtype. */
+int gdn2_decode(const gdn2_decode_desc* d, const void* q, const void* k, const void* v,
+                const void* w, const void* b, const void* g, const float* a_log,
+                const float* dt_bias, const uint8_t* reset, const void* state_in, void* o,
+                void* state_out, void* stream);
+
 /* Forward of one segment without a residual, like gdn2_fwd(d, ..., residual = NULL, ...), with
  * the workspace in a fixed 64 MiB (67108864-byte) device array inside the library instead of
  * a caller buffer.  No counterpart in the reference: it is for callers that cannot allocate
@@ -147,8 +191,8 @@ int gdn2_debug_gemm(int mode, const float* A, const float* B, float* C, int M, i
  * duration in milliseconds and the launch count, then stops recording.
  * Kernel ids: 0 wy_fwd, 1 scan_fwd (with the output unless state_ckpt == 0 in training),
  * 2 scan_bwd, 3 bwd_state (state_ckpt == 0), 4 bwd_wy, 5 out_fwd (training, state_ckpt == 0),
- * 6 bwd_pre, 7 bwd_state_rc (state_ckpt >= 1: bwd_state with the states recomputed). */
-#define GDN2_NUM_KERNELS 8
+ * 6 bwd_pre, 7 bwd_state_rc (state_ckpt >= 1: bwd_state with the states recomputed), 8 decode. */
+#define GDN2_NUM_KERNELS 9
 int gdn2_prof_begin(int max_launches);
 int gdn2_prof_end(double ms_sum[GDN2_NUM_KERNELS], int counts[GDN2_NUM_KERNELS]);
 

@@ -23,6 +23,9 @@ Reference anchors (``/root/reference``):
 * ``atomic_gdn2/fwd/cd_slim.py:8-31``  fused WY recompute + scan (kernel C+D)
 * ``atomic_gdn2/bwd/mega.py:9-58``     fused analytic backward (B1..B5)
 * ``atomic_gdn2/bwd/b4.py:7-97``       B4, the VJP of the two-level scores
+* ``notebooks/gdn2_v031_stage2_tpu.ipynb`` cell 1 (``INFERENCE_V031``, the inference module
+  inlined there): ``_decode_body`` / ``decode_step`` -> ``decode_step_ref``;
+  ``_cd_inference_body`` / ``chunk_forward_inference`` -> ``chunk_forward_inference_ref``
 
 Every function here is pinned by a test in ``tests/test_oracle_*.py`` (stored 80-digit
 Decimal known-answer values, token-serial equality, closed forms, scipy triangular solves,
@@ -46,6 +49,7 @@ __all__ = [
     "blr_scores_ref", "btl_scores", "micro_inv", "ladder_inverse", "recompute_wy_ref",
     "inter_chunk_scan_ref", "forward_ref", "forward_ref_blhd", "token_serial_ref",
     "b4_exact_f64_np", "backward_mega_ref", "grad_ref", "wy_stage_ref",
+    "decode_step_ref", "chunk_forward_inference_ref",
 ]
 
 
@@ -312,14 +316,18 @@ def recompute_wy_ref(q, k, v, w, b, gc, A, cfg: OracleCfg, dot=None):
     return sanitize(wp, c), sanitize(u, c), sanitize(k * ekg, c), sanitize(q * egc, c), gl
 
 
-def inter_chunk_scan_ref(Aqk, wp, u, kg, qg, gc_last, scale, h0, cfg: OracleCfg, dot=None):
-    """Sequential scan over the chunk axis (-3); returns o, h_final, h_pre_all, v_new_all."""
+def inter_chunk_scan_ref(Aqk, wp, u, kg, qg, gc_last, scale, h0, cfg: OracleCfg, dot=None, reset=None):
+    """Sequential scan over the chunk axis (-3); returns o, h_final, h_pre_all, v_new_all.
+    reset (B, nc) bool, optional: the state entering chunk i of batch row b is zero where set
+    (the document resets of the inference prefill, INFERENCE_V031 _cd_inference_body)."""
     dot = dot or torch.matmul
     c = cfg.clip
     nc = Aqk.shape[-3]
     h = h0
     os_, hp, vn = [], [], []
     for i in range(nc):
+        if reset is not None:
+            h = torch.where(reset[:, i][:, None, None, None], torch.zeros_like(h), h)
         Aq, wp_, u_, kg_, qg_, gl = (x[..., i, :, :] if x.dim() == Aqk.dim() else x[..., i, :]
                                      for x in (Aqk, wp, u, kg, qg, gc_last))
         v_new = u_ - dot(wp_, h)
@@ -384,6 +392,88 @@ def token_serial_ref(q, k, v, g, b, w, scale, h0=None):
         h = h + torch.einsum("bhd,bhv->bhdv", k[:, t], v_new)
         outs.append(torch.einsum("bhdv,bhd->bhv", h, q[:, t] * scale))
     return torch.stack(outs, 1), h
+
+
+# ----------------------------------------------------------------------------------------
+# Inference entry points (reference notebooks/gdn2_v031_stage2_tpu.ipynb, cell 1, INFERENCE_V031)
+# ----------------------------------------------------------------------------------------
+def _nan_to_num0(x):
+    return torch.where(torch.isfinite(x), x, torch.zeros_like(x))
+
+
+def decode_step_ref(q, k, v, w, b, g, state, scale, reset=None, state_bf16=False, stability_tau=None,
+                    fuse_prologue=False, a_log=None, dt_bias=None, out_bf16=False):
+    """One token of the recurrence, (B,H,D) inputs, (B,H,D,D) state (INFERENCE_V031
+    _decode_body / decode_step): the incoming state cast to the state dtype and zeroed for reset
+    rows; optional prologue (q, k l2-normalised with eps 1e-6, b, w sigmoid, g = -exp(a_log)
+    softplus(g + dt_bias)); h = diag(e^min(g,0)) S; v_new = w v - h^T (b k); h += k v_new^T;
+    o = h^T (s q); optional per-head Frobenius cap; NaN/Inf -> 0 in h and o; o and the state
+    rounded to their storage dtypes.  Computes in the inputs' dtype (float64 for the checks)."""
+    st = bf16_round(state) if state_bf16 else state
+    if reset is not None:
+        st = torch.where(reset.reshape(-1)[:, None, None, None] > 0, torch.zeros_like(st), st)
+    if fuse_prologue:
+        q = q / torch.sqrt((q * q).sum(-1, keepdim=True) + 1e-6)
+        k = k / torch.sqrt((k * k).sum(-1, keepdim=True) + 1e-6)
+        b = torch.sigmoid(b)
+        w = torch.sigmoid(w)
+        g = -torch.exp(a_log)[None, :, None] * torch.nn.functional.softplus(g + dt_bias[None, None, :])
+    h = st * torch.exp(torch.clamp(g, max=0.0))[..., None]
+    erase = ((b * k)[..., None] * h).sum(-2)
+    v_new = w * v - erase
+    h = h + k[..., None] * v_new[..., None, :]
+    o = (h * (q * scale)[..., None]).sum(-2)
+    if stability_tau is not None:
+        nrm = torch.sqrt((h * h).sum((-2, -1)))
+        f = torch.minimum(torch.ones_like(nrm), stability_tau / torch.maximum(nrm, torch.full_like(nrm, 1e-12)))
+        h = h * f[..., None, None]
+    h = _nan_to_num0(h)
+    o = _nan_to_num0(o)
+    return (bf16_round(o) if out_bf16 else o), (bf16_round(h) if state_bf16 else h)
+
+
+def chunk_forward_inference_ref(q, k, v, w, b, g, scale, cfg: OracleCfg, h0=None, segment_ids=None,
+                                state_bf16=False, stability_tau=None):
+    """Forward-only prefill (INFERENCE_V031 chunk_forward_inference) on head-major (B,H,L,D)
+    inputs of any length: g clamped to <= 0; the L // bt full chunks in kernel semantics
+    (wy_stage_ref + inter_chunk_scan_ref) with the state zeroed entering every chunk whose
+    document id (segment_ids (B,L) at the chunk's first token) differs from the previous
+    chunk's; the L % bt tail token by token (decode_step_ref, the state rounded to the state
+    dtype after each token) with a reset wherever the id differs from the previous token's;
+    then the optional per-head Frobenius cap.  Returns o, h_final (state dtype applied)."""
+    B, H, L, D = q.shape
+    bt = cfg.bt
+    n_full = L // bt
+    L_full = n_full * bt
+    g = torch.clamp(g, max=0.0)
+    h = q.new_zeros((B, H, D, D)) if h0 is None else h0.to(q.dtype)
+    outs = []
+    if n_full > 0:
+        sl = lambda t: t[:, :, :L_full]
+        st = wy_stage_ref(*(sl(t) for t in (q, k, v, w, b, g)), scale, cfg)
+        reset = None
+        if segment_ids is not None:
+            ids = segment_ids[:, :L_full:bt]
+            reset = torch.zeros_like(ids, dtype=torch.bool)
+            reset[:, 1:] = ids[:, 1:] != ids[:, :-1]
+        o, h, _, _ = inter_chunk_scan_ref(st["Aqk"], st["wp"], st["u"], st["kg"], st["qg"], st["gc_last"],
+                                          scale, h, cfg, make_dot(cfg.dot_mode), reset=reset)
+        outs.append(from_chunks(o))
+    if L > L_full:
+        h = bf16_round(h) if state_bf16 else h
+        for t in range(L_full, L):
+            rst = None
+            if segment_ids is not None:
+                prev = segment_ids[:, t - 1] if t > 0 else segment_ids[:, t]
+                rst = (segment_ids[:, t] != prev).to(torch.int32)
+            o_t, h = decode_step_ref(q[:, :, t], k[:, :, t], v[:, :, t], w[:, :, t], b[:, :, t], g[:, :, t],
+                                     h, scale, reset=rst, state_bf16=state_bf16)
+            outs.append(o_t[:, :, None])
+    o = torch.cat(outs, 2) if outs else None
+    if stability_tau is not None:
+        nrm = torch.sqrt((h * h).sum((-2, -1), keepdim=True))
+        h = h * torch.minimum(torch.ones_like(nrm), stability_tau / torch.maximum(nrm, torch.full_like(nrm, 1e-12)))
+    return o, (bf16_round(h) if state_bf16 else h)
 
 
 def b4_exact_f64_np(q, k, b, gc, dAq, dAk, scale, clip=1e4, dc=20.0, dblk=8):

@@ -1,0 +1,278 @@
+"""GPU parity of the inference entry points (atomic_gdn2.inference: decode_step and
+chunk_forward_inference, the reference's INFERENCE_V031 in notebooks/gdn2_v031_stage2_tpu.ipynb)
+against the float64 oracle (decode_step_ref / chunk_forward_inference_ref), plus bitwise
+identities of the HIP path itself: the prefill without documents equals the training
+operator's forward-only call, and with documents it equals separate calls per document.
+
+Bars: fp32 outputs within rel-L2 1e-5 of the oracle for the token recurrence (no products
+other than fp32 sums) and 2e-3 for the chunked prefill (the operator's gate; measured ~1e-6);
+bfloat16-stored outputs within 4e-3 (one bf16 rounding, 2^-8 relative)."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+GATE = 2e-3
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm GPU")
+
+
+def banner(msg):
+    print(f"[gpu-test] {msg}", flush=True)
+
+
+def _cfg(bt=64, **kw):
+    from atomic_gdn2 import make_cfg
+    d = dict(bt=bt, bc=bt // 2, score_bs=bt, bs2=32, mb=8, wy_eps=0.0, dot_mode="highest",
+             solve_dot_mode="highest", b3_dot_mode="highest")
+    d.update(kw)
+    return make_cfg(**d)
+
+
+def _inputs(B, H, L, D, seed):
+    from atomic_gdn2.synthetic import make_inputs_np
+    arrs, scale = make_inputs_np(B, H, L, D, seed=seed)
+    return [torch.from_numpy(a) for a in arrs], scale
+
+
+def _oracle():
+    from oracle import gdn2_oracle as O
+    return O
+
+
+def _doc_ids(B, L, starts):
+    ids = torch.zeros(B, L, dtype=torch.int64)
+    for b, ss in enumerate(starts):
+        for s in ss:
+            ids[b, s:] += 1
+    return ids
+
+
+# ---------------------------------------------------------------- decode_step
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("mode", ["fp32", "bf16_inputs", "bf16_state", "reset_cap", "fused"])
+def test_decode_step_matches_oracle(D, mode):
+    from atomic_gdn2.inference import decode_step
+    O = _oracle()
+    B, H = 3, 4
+    banner(f"decode_step D={D} {mode}")
+    xs, scale = _inputs(B, H, 1, D, seed=11)
+    x1 = [x[:, :, 0].contiguous() for x in xs]
+    rng = np.random.default_rng(2)
+    st = torch.from_numpy(rng.standard_normal((B, H, D, D)).astype(np.float32) * 0.2)
+    kw, ref_kw = {}, {}
+    if mode == "bf16_inputs":
+        x1 = [x.to(torch.bfloat16) for x in x1]
+        ref_kw["out_bf16"] = True
+    if mode == "bf16_state":
+        kw["state_dtype"] = torch.bfloat16
+        ref_kw["state_bf16"] = True
+    if mode == "reset_cap":
+        kw["reset"] = ref_kw["reset"] = torch.tensor([1, 0, 1])
+        kw["stability_tau"] = ref_kw["stability_tau"] = 1.5
+    if mode == "fused":
+        a_log = torch.from_numpy(rng.standard_normal(H).astype(np.float32) * 0.5)
+        dt = torch.from_numpy(rng.standard_normal(D).astype(np.float32) * 0.5)
+        x1 = [torch.from_numpy(rng.standard_normal((B, H, D)).astype(np.float32)) for _ in range(6)]
+        kw.update(fuse_prologue=True, a_log=a_log.cuda(), dt_bias=dt.cuda())
+        ref_kw.update(fuse_prologue=True, a_log=a_log.double(), dt_bias=dt.double())
+    o, h = decode_step(*(x.cuda() for x in x1), st.cuda(), scale, **kw)
+    torch.cuda.synchronize()
+    ro, rh = O.decode_step_ref(*(x.double() for x in x1), st.double(), scale, **ref_kw)
+    assert o.dtype == x1[0].dtype and o.shape == (B, H, D)
+    assert h.dtype == kw.get("state_dtype", torch.float32)
+    tol_o = 4e-3 if mode == "bf16_inputs" else 1e-5
+    tol_h = 4e-3 if mode == "bf16_state" else 1e-5
+    eo, eh = rel_l2(o.float(), ro), rel_l2(h.float(), rh)
+    banner(f"  rel-L2 o {eo:.2e} state {eh:.2e}")
+    assert eo <= tol_o and eh <= tol_h
+
+
+def test_decode_step_nonfinite_inputs_are_cleaned():
+    """INFERENCE_V031's A5 policy: NaN / Inf never persist in the state or the output."""
+    from atomic_gdn2.inference import decode_step
+    O = _oracle()
+    B, H, D = 2, 3, 128
+    xs, scale = _inputs(B, H, 1, D, seed=12)
+    x1 = [x[:, :, 0].contiguous() for x in xs]
+    x1[2][1, 2, 5] = float("nan")
+    x1[2][0, 1, 7] = float("inf")
+    st = torch.randn(B, H, D, D) * 0.1
+    for tau in (None, 1e30):
+        o, h = decode_step(*(x.cuda() for x in x1), st.cuda(), scale, stability_tau=tau)
+        ro, rh = O.decode_step_ref(*(x.double() for x in x1), st.double(), scale, stability_tau=tau)
+        assert torch.isfinite(o).all() and torch.isfinite(h).all()
+        # the poisoned value columns (and, with the cap, the poisoned heads) are exactly 0
+        assert o[1, 2, 5] == 0 and o[0, 1, 7] == 0
+        assert torch.count_nonzero(h[1, 2, :, 5]) == 0 and torch.count_nonzero(h[0, 1, :, 7]) == 0
+        if tau is not None:
+            assert torch.count_nonzero(h[1, 2]) == 0 and torch.count_nonzero(h[0, 1]) == 0
+        assert rel_l2(o, ro) < 1e-5 and rel_l2(h, rh) < 1e-5
+
+
+def test_decode_steps_chain_like_the_token_recurrence():
+    """64 consecutive decode_step calls carry the state as token_serial_ref does."""
+    from atomic_gdn2.inference import decode_step
+    O = _oracle()
+    B, H, L, D = 2, 2, 64, 128
+    xs, scale = _inputs(B, H, L, D, seed=13)
+    h = torch.zeros(B, H, D, D, device="cuda")
+    os_ = []
+    for t in range(L):
+        o, h = decode_step(*(x[:, :, t].contiguous().cuda() for x in xs), h, scale)
+        os_.append(o)
+    o = torch.stack(os_, 2)
+    q, k, v, w, b, g = (x.double().transpose(1, 2) for x in xs)
+    ro, rh = O.token_serial_ref(q, k, v, g, b, w, scale)
+    assert rel_l2(o, ro.transpose(1, 2)) < 1e-5 and rel_l2(h, rh) < 1e-5
+
+
+def test_fused_decode_equals_preactivated_decode():
+    """The notebook's R3 check (fused decode with checkpoint gates vs decode on the same inputs
+    activated outside): synthetic a_log / dt_bias stand in for the checkpoint's, which are not
+    available offline; rtol / atol 1e-3 as in the notebook (measured far below)."""
+    from atomic_gdn2.inference import decode_step
+    B, H, D = 2, 16, 128
+    gen = torch.Generator().manual_seed(41)
+    q, k, v, w, b = (torch.randn(B, H, D, generator=gen) * s for s in (0.5, 0.5, 1.0, 1.0, 1.0))
+    a_log = torch.randn(H, generator=gen) * 0.3
+    dt = torch.randn(D, generator=gen) * 0.3
+    g_raw = torch.randn(B, H, D, generator=gen) * 2.0
+    g_act = -torch.exp(a_log)[None, :, None] * torch.log1p(torch.exp(g_raw + dt[None, None, :]))
+    nrm = lambda x: x / torch.sqrt((x * x).sum(-1, keepdim=True) + 1e-6)
+    st0 = torch.zeros(B, H, D, D, device="cuda")
+    cu = lambda *ts: [t.cuda() for t in ts]
+    o_pre, _ = decode_step(*cu(nrm(q), nrm(k), v, torch.sigmoid(w), torch.sigmoid(b), g_act), st0, 1.0)
+    o_fus, _ = decode_step(*cu(q, k, v, w, b, g_raw), st0, 1.0, fuse_prologue=True, a_log=a_log.cuda(),
+                           dt_bias=dt.cuda())
+    np.testing.assert_allclose(o_pre.cpu().numpy(), o_fus.cpu().numpy(), rtol=1e-3, atol=1e-3)
+
+
+# ---------------------------------------------------------------- chunk_forward_inference
+CASES = [
+    dict(bt=64, L=256, starts=[[64, 192], [128]]),
+    dict(bt=64, L=3 * 64 + 40, starts=[[128, 3 * 64 + 11], []]),        # boundary in the tail
+    dict(bt=64, L=29, starts=[[7], [0]]),                                # tail only
+    dict(bt=128, L=384 + 20, starts=[[256], [128, 384 + 5]], wy_eps=1e-3),  # damped pairs
+    dict(bt=64, L=256, starts=None, state_dtype=torch.bfloat16, tau=3.0),
+    dict(bt=64, L=64 * 5 + 9, starts=[[64], [192, 64 * 5 + 1]], D=64, bf16_inputs=True),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: ",".join(f"{k}={v}" for k, v in c.items() if k != "starts"))
+def test_prefill_matches_oracle(case):
+    from atomic_gdn2.inference import chunk_forward_inference
+    O = _oracle()
+    B, H, D, L, bt = 2, 3, case.get("D", 128), case["L"], case["bt"]
+    banner(f"prefill {case}")
+    xs, scale = _inputs(B, H, L, D, seed=14)
+    if case.get("bf16_inputs"):
+        xs = [x.to(torch.bfloat16) for x in xs]
+    h0 = torch.randn(B, H, D, D, generator=torch.Generator().manual_seed(3)) * 0.05
+    cfg = _cfg(bt, wy_eps=case.get("wy_eps", 0.0))
+    ids = None if case["starts"] is None else _doc_ids(B, L, case["starts"])
+    sd = case.get("state_dtype", torch.float32)
+    o, h = chunk_forward_inference(*(x.cuda() for x in xs), scale, cfg, h0=h0.cuda(),
+                                   segment_ids=None if ids is None else ids.cuda(), state_dtype=sd,
+                                   stability_tau=case.get("tau"))
+    torch.cuda.synchronize()
+    ro, rh = O.chunk_forward_inference_ref(*(x.double() for x in xs), scale, O.OracleCfg.from_cfg(cfg),
+                                           h0=h0.double(), segment_ids=ids, state_bf16=sd == torch.bfloat16,
+                                           stability_tau=case.get("tau"))
+    assert o.dtype == torch.float32 and h.dtype == sd
+    eo, eh = rel_l2(o, ro), rel_l2(h.float(), rh)
+    banner(f"  rel-L2 o {eo:.2e} h {eh:.2e}")
+    assert eo <= GATE and eh <= (4e-3 if sd == torch.bfloat16 else GATE)
+
+
+def test_prefill_without_documents_equals_forward_only_bitwise():
+    from atomic_gdn2 import make_blr_trainable
+    from atomic_gdn2.inference import chunk_forward_inference
+    xs, scale = _inputs(2, 3, 256, 128, seed=15)
+    xs = [x.cuda() for x in xs]
+    h0 = (torch.randn(2, 3, 128, 128) * 0.05).cuda()
+    cfg = _cfg(64)
+    with torch.no_grad():
+        o1, h1 = make_blr_trainable(cfg, scale)(*xs, h0)
+    o2, h2 = chunk_forward_inference(*xs, scale, cfg, h0=h0)
+    assert torch.equal(o1, o2) and torch.equal(h1, h2)
+
+
+def test_prefill_documents_equal_separate_calls_bitwise():
+    """Chunk-aligned documents: the prefill with their ids equals one forward-only call per
+    document (each from a zero state, the first from h0), bit for bit -- and rows of a batch
+    do not see each other's boundaries (the notebook's R3 a1 check)."""
+    from atomic_gdn2 import make_blr_trainable
+    from atomic_gdn2.inference import chunk_forward_inference
+    B, H, L, D = 2, 3, 320, 128
+    xs, scale = _inputs(B, H, L, D, seed=16)
+    xs = [x.cuda() for x in xs]
+    h0 = (torch.randn(B, H, D, D) * 0.05).cuda()
+    starts = [[64, 192], [128]]
+    cfg = _cfg(64)
+    o, h = chunk_forward_inference(*xs, scale, cfg, h0=h0, segment_ids=_doc_ids(B, L, starts).cuda())
+    fn = make_blr_trainable(cfg, scale)
+    for b in range(B):
+        cuts = [0] + starts[b] + [L]
+        hb = h0[b:b + 1]
+        with torch.no_grad():
+            for i, (a, c) in enumerate(zip(cuts[:-1], cuts[1:])):
+                ob, hb = fn(*(x[b:b + 1, :, a:c] for x in xs), hb if i == 0 else None)
+                assert torch.equal(o[b:b + 1, :, a:c], ob), (b, a, c)
+        assert torch.equal(h[b:b + 1], hb), b
+
+
+def test_prefill_cu_seqlens_equals_segment_ids():
+    from atomic_gdn2.inference import chunk_forward_inference
+    B, H, L, D = 2, 2, 192 + 10, 64
+    xs, scale = _inputs(B, H, L, D, seed=17)
+    xs = [x.cuda() for x in xs]
+    cfg = _cfg(64)
+    o1, h1 = chunk_forward_inference(*xs, scale, cfg, cu_seqlens=[0, 64, 192 + 4, L])
+    o2, h2 = chunk_forward_inference(*xs, scale, cfg, segment_ids=_doc_ids(B, L, [[64, 196]] * 2).cuda())
+    assert torch.equal(o1, o2) and torch.equal(h1, h2)
+    o3, h3 = chunk_forward_inference(*xs, scale, cfg, cu_seqlens=torch.tensor([[0, 128, L], [0, 64, L]]))
+    o4, h4 = chunk_forward_inference(*xs, scale, cfg, segment_ids=_doc_ids(B, L, [[128], [64]]).cuda())
+    assert torch.equal(o3, o4) and torch.equal(h3, h4)
+
+
+def test_prefill_vs_token_serial_notebook_shape():
+    """The notebook's R3 'compiled prefill vs serial' check at its shape (B2 H16 D128 L128,
+    bs2 16, g_max 160/16, its input recipe) against the float64 token recurrence, with q and k
+    l2-normalised as the layer supplies them (the notebook's raw 0.5 N draws give |k|^2 ~ 32, an
+    erase factor 1 - b |k|^2 ~ -15 per token: an exploding recurrence that no fp32 bar can
+    hold; the notebook's own bar there is 0.15).  The operator's gate applies."""
+    from atomic_gdn2.inference import chunk_forward_inference
+    O = _oracle()
+    gen = torch.Generator().manual_seed(41)
+    B, H, D, L = 2, 16, 128, 128
+    q, k = (torch.nn.functional.normalize(torch.randn(B, L, H, D, generator=gen), dim=-1) for _ in range(2))
+    v = torch.randn(B, L, H, D, generator=gen)
+    w, b = (torch.sigmoid(torch.randn(B, L, H, D, generator=gen)) for _ in range(2))
+    g = -torch.exp(torch.randn(B, L, H, D, generator=gen) * 0.39 - 1.0)
+    cfg = _cfg(64, bs2=16, g_max=160.0 / 16)
+    hm = lambda t: t.transpose(1, 2).contiguous().cuda()
+    o, hf = chunk_forward_inference(hm(q), hm(k), hm(v), hm(w), hm(b), hm(g), 1.0, cfg)
+    ro, rh = O.token_serial_ref(*(t.double() for t in (q, k, v, g, b, w)), 1.0)
+    assert rel_l2(o.transpose(1, 2), ro) < GATE and rel_l2(hf, rh) < GATE
+
+
+def test_prefill_errors_on_gpu():
+    from atomic_gdn2.inference import chunk_forward_inference
+    xs, scale = _inputs(1, 2, 128, 128, seed=18)
+    xs = [x.cuda() for x in xs]
+    cfg = _cfg(64, bs2=16, g_max=10.0)
+    seg = torch.zeros(1, 128, dtype=torch.int64, device="cuda")
+    seg[:, 70:] = 1
+    with pytest.raises(ValueError, match="boundary inside chunk"):
+        chunk_forward_inference(*xs, scale, cfg, segment_ids=seg)
+    bad = xs[:5] + [torch.full_like(xs[5], -50.0)]
+    with pytest.raises(ValueError, match="outside the layer domain"):
+        chunk_forward_inference(*bad, scale, cfg)
