@@ -94,9 +94,19 @@ def _check_head_dim(D):
         raise ValueError(f"D={D}: the HIP kernels support head dimensions 64 and 128")
 
 
+def _aligned(t):
+    """The kernel reads 4 consecutive elements per access: a tensor whose first element is not
+    16-byte aligned (a view at an odd offset) is copied."""
+    return t if t is None or t.data_ptr() % 16 == 0 else t.clone()
+
+
 def _run_decode(xs, in_dtype, B, H, D, n_tok, seq_ld, scale, state_in, state_code, o, out_code,
                 reset=None, fuse=False, a_log=None, dt_bias=None, tau=None, offset=0):
     dev = xs[0].device
+    xs = [_aligned(x) for x in xs]
+    state_in = _aligned(state_in)
+    if o.data_ptr() % 16:
+        raise ValueError("o must be 16-byte aligned")
     state_out = torch.empty((B, H, D, D), dtype=_torch_dtype(state_code), device=dev)
     dd = _lib.Gdn2DecodeDesc(B, H, D, n_tok, seq_ld, in_dtype, out_code, state_code, int(fuse),
                              int(tau is not None), float(scale), float(tau) if tau is not None else 0.0)
@@ -217,32 +227,59 @@ def chunk_forward_inference(q=None, k=None, v=None, w=None, b=None, g=None,
     L_full = n_full * bt
     r_tail = L - L_full
     scale = float(scale)
-    # g <= 0 as on the decode path; the layer's domain is [-g_max, 0]
-    g = torch.clamp(g, max=0.0)
-    g_max_abs = float(cfg.g_max)
-    if L > 0 and bool(torch.amin(g).float() < -g_max_abs - 1e-6):
-        raise ValueError(
-            f"g outside the layer domain: min(g) < -g_max={g_max_abs} "
-            "(the layer constructs g = -min(softplus(...), g_max); clamp or "
-            "fix the projection before calling)")
     dev = q.device
+    g_max_abs = float(cfg.g_max)
+    # The domain of g and the document boundaries are checked on the device and read back in one
+    # synchronisation; g is clamped to <= 0 (as on the decode path) only when some g > 0.
+    stats = []
+    if L > 0:
+        g_lo, g_hi = torch.aminmax(g)
+        stats += [g_lo.float(), g_hi.float()]
+    bad = None
     if segment_ids is not None and n_full > 0:
         seg_tok = torch.as_tensor(segment_ids, device=dev).reshape(bsz, L)[:, :L_full]
         per_chunk_first = seg_tok[:, ::bt]
         same = seg_tok.reshape(bsz, n_full, bt) == per_chunk_first[:, :, None]
         bad = ~same.all(dim=-1)
-        if bool(bad.any()):
-            b_idx, c_idx = (int(x) for x in torch.nonzero(bad)[0])
-            raise ValueError(
-                f"document boundary inside chunk {c_idx} of batch row "
-                f"{b_idx} (tokens start at {c_idx * bt}): split "
-                "the sequence at document boundaries before calling "
-                "chunk_forward_inference (chunk-granularity resets only)")
-    if cu_seqlens is not None:
-        if segment_ids is not None:
-            raise ValueError("pass either segment_ids or cu_seqlens, not both")
+        stats.append(bad.any().float().to(dev))
+    both = segment_ids is not None and cu_seqlens is not None
+    if cu_seqlens is not None and not both:
         segment_ids = _segment_ids_from_cu_seqlens(cu_seqlens, bsz, L, dev)
-    seg = None if segment_ids is None else torch.as_tensor(segment_ids, device=dev).reshape(bsz, L)
+    seg = None if segment_ids is None or both else torch.as_tensor(segment_ids, device=dev).reshape(bsz, L)
+    # the reset bytes are formed before the synchronisation, so that the device is not left idle
+    # while the host builds them after it
+    flags = tflags = None
+    if seg is not None and n_full > 0:
+        sc_ids = seg[:, :L_full:bt]                                   # (B, n_full) id at each chunk start
+        chg = torch.zeros_like(sc_ids, dtype=torch.bool)
+        chg[:, 1:] = sc_ids[:, 1:] != sc_ids[:, :-1]
+        per64 = torch.zeros((bsz, L_full // 64), dtype=torch.uint8, device=dev)
+        per64[:, ::bt // 64] = chg.to(torch.uint8)                    # the chunk's first 64-token half
+        flags = per64[:, None, :].expand(bsz, H, L_full // 64).contiguous()
+    if seg is not None and r_tail > 0:
+        tail = seg[:, L_full:]
+        prev = seg[:, L_full - 1:L - 1] if L_full > 0 else torch.cat([tail[:, :1], tail[:, :-1]], dim=1)
+        tflags = (tail != prev).to(torch.uint8).contiguous()
+    vals = torch.stack([x.to(dev) for x in stats]).tolist() if stats else []
+    # errors in the reference's order: g's domain, a boundary inside a chunk, both id forms
+    if L > 0:
+        # the layer's domain is [-g_max, 0] (NaN compares false, as in the reference)
+        if min(vals[0], 0.0) < -g_max_abs - 1e-6:
+            raise ValueError(
+                f"g outside the layer domain: min(g) < -g_max={g_max_abs} "
+                "(the layer constructs g = -min(softplus(...), g_max); clamp or "
+                "fix the projection before calling)")
+        if vals[1] > 0:
+            g = torch.clamp(g, max=0.0)
+    if bad is not None and vals[-1] > 0:
+        b_idx, c_idx = (int(x) for x in torch.nonzero(bad)[0])
+        raise ValueError(
+            f"document boundary inside chunk {c_idx} of batch row "
+            f"{b_idx} (tokens start at {c_idx * bt}): split "
+            "the sequence at document boundaries before calling "
+            "chunk_forward_inference (chunk-granularity resets only)")
+    if both:
+        raise ValueError("pass either segment_ids or cu_seqlens, not both")
 
     h = None if h0 is None else h0.to(torch.float32)
     o = None
@@ -254,14 +291,6 @@ def chunk_forward_inference(q=None, k=None, v=None, w=None, b=None, g=None,
         o = torch.empty((bsz, H, L, D), dtype=torch.float32, device=dev)
         L_ = _lib.lib()
         if n_full > 0:
-            flags = None
-            if seg is not None:
-                sc_ids = seg[:, :L_full:bt]                               # (B, n_full)
-                chg = torch.zeros_like(sc_ids, dtype=torch.bool)
-                chg[:, 1:] = sc_ids[:, 1:] != sc_ids[:, :-1]
-                per64 = torch.zeros((bsz, L_full // 64), dtype=torch.uint8, device=dev)
-                per64[:, ::bt // 64] = chg.to(torch.uint8)                # first 64-token half
-                flags = per64[:, None, :].expand(bsz, H, L_full // 64).contiguous()
             desc = _lib.make_desc(cfg, bsz, H, L_full, D, scale, seq_ld=L)
             hf = torch.empty((bsz, H, D, D), dtype=torch.float32, device=dev)
             with torch.cuda.device(dev):
@@ -271,11 +300,6 @@ def chunk_forward_inference(q=None, k=None, v=None, w=None, b=None, g=None,
                                              _lib.stream_handle(dev)), "gdn2_fwd_reset")
             h = hf
         if r_tail > 0:
-            tflags = None
-            if seg is not None:
-                tail = seg[:, L_full:]
-                prev = seg[:, L_full - 1:L - 1] if L_full > 0 else torch.cat([tail[:, :1], tail[:, :-1]], dim=1)
-                tflags = (tail != prev).to(torch.uint8).contiguous()
             st = None if h is None else h.to(_torch_dtype(sc)).contiguous()
             h = _run_decode(xs, in_dtype, bsz, H, D, r_tail, L, scale, st, sc, o, 0, reset=tflags,
                             offset=L_full * D)

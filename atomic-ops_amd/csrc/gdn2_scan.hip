@@ -85,11 +85,27 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
   constexpr bool OWNS = V || NH == 8;           // keeps key tile w of the state (w < NH)
   auto base = [&](int c) { return (size_t)bh * nc + (c < nc ? c : nc - 1); };   // clamped chunk
 
-  // a set reset byte zeroes the state entering that chunk (wave-uniform: one byte per chunk)
-  auto reset_at = [&](int c) { return a.reset != nullptr && c < nc && a.reset[(size_t)bh * nc + c] != 0; };
+  // A set reset byte zeroes the state entering that chunk.  No load on the sequential path:
+  // lane l holds the bytes of chunks 64 m + l of the current block m (fl_cur) and of the next
+  // one (fl_nxt), read one block ahead; a step reads its next chunk's byte with readlane.
+  const bool has_reset = a.reset != nullptr;
+  auto load_flags = [&](int m) -> int {
+    const int c = 64 * m + lane_id();
+    return (has_reset && c < nc) ? (int)a.reset[(size_t)bh * nc + c] : 0;
+  };
+  int fl_cur = load_flags(0), fl_nxt = load_flags(1);
+  // the byte of chunk c (c >= 1 ascending, one call per step), rotating the blocks as c enters one
+  auto reset_at = [&](int c) -> int {
+    if (!has_reset || c >= nc) return 0;
+    if ((c & 63) == 0) {
+      fl_cur = fl_nxt;
+      fl_nxt = load_flags(c / 64 + 1);
+    }
+    return __builtin_amdgcn_readlane(fl_cur, c & 63);
+  };
   f4 h = {0.f, 0.f, 0.f, 0.f};
   if (OWNS) {
-    if (a.h0 && !reset_at(0)) {
+    if (a.h0 && !(has_reset && __builtin_amdgcn_readlane(fl_cur, 0))) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) h[e] = a.h0[(size_t)bh * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r];
     }
@@ -123,6 +139,7 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
     constexpr bool ODD = decltype(odd)::value;
     const size_t ch = (size_t)bh * nc + c, tb = ch * T * D;
     const size_t tbn = base(cn) * T * D, sbn = base(cn) * T * T;
+    const int rst_next = reset_at(cn);
     if (OWNS && a.h_pre_f && (a.ckpt <= 1 || c % a.ckpt == 0)) {
       const size_t hi = a.ckpt <= 1 ? ch : (size_t)bh * ((nc + a.ckpt - 1) / a.ckpt) + c / a.ckpt;
       stg4(a.h_pre_f + hi * D * D + frag_blk(vb, w, D) + 4 * l, f4_to_float4(h));
@@ -248,7 +265,7 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
     // every wave has read h_pre (window A) before the first barrier, so the new state may
     // overwrite it here
     if (OWNS) {
-      if (reset_at(cn)) h = f4{0.f, 0.f, 0.f, 0.f};
+      if (rst_next) h = f4{0.f, 0.f, 0.f, 0.f};
       sH[w * WAVE + l] = f4_to_float4(h);
     }
     __syncthreads();

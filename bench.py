@@ -15,8 +15,9 @@ Beside the headline line's fields: ``config3_sweep`` (grad-eval latency at B4 D1
 H in {2,4,6} x L in {2048,4096}, next to the reference's published TPU v5e latencies) and
 ``config4_long_context_fwd`` (forward-only B8 H16 L32768 D128 with bf16 inputs, 8 calls of
 4096 tokens carrying the state; tokens/s and canonical GB/s), and ``config5_e2e_lm`` (one
-training step of the reference's 8-block benchmark LM around the operator, B8 L2048).
-``--no-sweep`` skips configs 3 and 4, ``--no-e2e`` config 5.
+training step of the reference's 8-block benchmark LM around the operator, B8 L2048), and
+``inference`` (decode_step and the document-reset prefill at config 4's shape).
+``--no-sweep`` skips configs 3 and 4 and the inference entry points, ``--no-e2e`` config 5.
 """
 from __future__ import annotations
 
@@ -321,6 +322,63 @@ def bench_config4(cfg, seed):
             "tflops": round(flops / (ms * 1e-3) / 1e12, 2), "kernel_ms_per_call": kern}
 
 
+def bench_inference(cfg, seed):
+    """The inference entry points (atomic_gdn2.inference, the reference's INFERENCE_V031) at
+    config 4's serving shape B8 H16 D128: decode_step (one token, state read and written once,
+    no MFMA) with fp32 and with bfloat16 inputs / state, and at B64 (fp32), and the prefill
+    chunk_forward_inference of one config-4 call (L 4096, bf16 inputs) with four chunk-aligned
+    documents per row, beside the same call without documents through make_blr_trainable.
+    kernel_us / hbm_gb_per_s: HIP events around the decode kernel; ms: wall time per call,
+    host work included (the prefill's domain and boundary checks synchronise with the device)."""
+    import torch
+    from atomic_gdn2 import make_blr_trainable, _lib
+    from atomic_gdn2.inference import decode_step, chunk_forward_inference
+    from atomic_gdn2.synthetic import make_inputs_device
+    B, H, D = 8, 16, 128
+    out = {"B": B, "H": H, "D": D}
+    xs, scale = make_inputs_device(B, H, 1, D, seed=seed)
+    x1 = [x[:, :, 0].contiguous() for x in xs]
+    big, _ = make_inputs_device(64, H, 1, D, seed=seed)
+    x64 = [x[:, :, 0].contiguous() for x in big]
+    for name, dt, xb in (("decode_fp32", torch.float32, x1), ("decode_bf16", torch.bfloat16, x1),
+                         ("decode_fp32_B64", torch.float32, x64)):
+        Bn = xb[0].shape[0]
+        xi = [x.to(dt) for x in xb]
+        st = torch.zeros(Bn, H, D, D, device="cuda", dtype=dt)
+
+        def run():
+            decode_step(*xi, st, scale, state_dtype=dt)
+        ms = _median_ms(run, reps=20, rounds=3, warm=3)
+        _lib.prof_begin(64)
+        for _ in range(20):
+            run()
+        torch.cuda.synchronize()
+        t, c = _lib.prof_end()["decode"]
+        us = t / c * 1e3
+        eb = 2 if dt == torch.bfloat16 else 4
+        byts = 2 * Bn * H * D * D * eb + 7 * Bn * H * D * eb
+        out[name] = {"B": Bn, "ms_per_call": round(ms, 4), "kernel_us": round(us, 2), "bytes": byts,
+                     "hbm_gb_per_s": round(byts / (us * 1e-6) / 1e9, 1),
+                     "hbm_frac": round(byts / (us * 1e-6) / 1e9 / PEAK_HBM, 3)}
+    L = 4096
+    xs, scale = make_inputs_device(B, H, L, D, seed=seed + 1, dtype=torch.bfloat16)
+    ids = torch.zeros(B, L, dtype=torch.int64, device="cuda")
+    for s0 in (1024, 2048, 3072):
+        ids[:, s0:] += 1
+    fn = make_blr_trainable(cfg, scale)
+
+    def plain():
+        with torch.no_grad():
+            fn(*xs)
+
+    def docs():
+        chunk_forward_inference(*xs, scale, cfg, segment_ids=ids)
+    out["prefill_4_documents"] = {"L": L, "input_dtype": "bf16",
+                                  "ms": round(_median_ms(docs, reps=2, rounds=3, warm=1), 3),
+                                  "forward_only_ms": round(_median_ms(plain, reps=2, rounds=3, warm=1), 3)}
+    return out
+
+
 def bench_e2e_lm(seed, reps=4, rounds=3, warm=2):
     """Config 5: one training step of the reference's benchmark LM (8 GDN-2
     blocks, 34,873,952 parameters, B8 L2048, vocab 256, CE + clip_by_global_norm(1.0) + AdamW)
@@ -357,6 +415,7 @@ def main():
                          "default: the library's DEFAULT_STATE_CKPT")
     ap.add_argument("--ckpt-table", action="store_true", help="only print the state_ckpt table and exit")
     ap.add_argument("--dot-table", action="store_true", help="only print the dot-mode table and exit")
+    ap.add_argument("--inference", action="store_true", help="only print the inference entry points' figures and exit")
     ap.add_argument("--profile-only", action="store_true",
                     help="for rocprofv3: run --warmup then --steps gradient evaluations of the workload "
                          "(no timing loops, no forward-only pass, no other configs) and print nothing else")
@@ -404,6 +463,9 @@ def main():
         return
     if args.dot_table:
         print(json.dumps({"dot_mode_ms": dot_mode_table(args.seed)}), flush=True)
+        return
+    if args.inference:
+        print(json.dumps({"inference": bench_inference(cfg, args.seed)}), flush=True)
         return
     if args.profile_only:
         if args.seq_len == L_:
@@ -501,6 +563,7 @@ def main():
         out["dot_mode_ms"] = dot_mode_table(args.seed)
         out["config3_sweep"] = sweep_config3(cfg, args.seed)
         out["config4_long_context_fwd"] = bench_config4(cfg, args.seed)
+        out["inference"] = bench_inference(cfg, args.seed)
     if not args.no_e2e:
         out["config5_e2e_lm"] = bench_e2e_lm(args.seed)
     if not args.no_cpu_baseline:
