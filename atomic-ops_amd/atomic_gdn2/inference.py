@@ -221,6 +221,8 @@ def chunk_forward_inference(q=None, k=None, v=None, w=None, b=None, g=None,
     _same_shape((q, k, v, w, b, g), "qkvwbg", (bsz, H, L, D))
     if bsz == 0 or H == 0 or D == 0:
         raise ValueError(f"empty input q.shape={tuple(q.shape)}: B, H and D must be positive")
+    if h0 is not None and tuple(h0.shape) != (bsz, H, D, D):
+        raise ValueError(f"h0.shape={tuple(h0.shape)} must be {(bsz, H, D, D)}")
     sc = _state_code(state_dtype)
     bt = cfg.bt
     n_full = L // bt

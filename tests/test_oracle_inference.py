@@ -228,6 +228,8 @@ def test_prefill_validation_errors():
         cfi(*xs, 1.0, cfg, segment_ids=torch.zeros(1, 128, dtype=torch.int64), cu_seqlens=[0, 64, 128])
     with pytest.raises(ValueError, match="state_dtype"):
         cfi(*xs, 1.0, cfg, state_dtype=torch.float16)
+    with pytest.raises(ValueError, match="h0.shape"):                 # checked before any kernel reads it
+        cfi(*xs, 1.0, cfg, h0=torch.zeros(1, 2, 64, 32))
     with pytest.raises(RuntimeError, match="ROCm device"):     # valid call: no CPU fallback
         cfi(*xs, 1.0, cfg)
 
