@@ -276,3 +276,47 @@ def test_prefill_errors_on_gpu():
     bad = xs[:5] + [torch.full_like(xs[5], -50.0)]
     with pytest.raises(ValueError, match="outside the layer domain"):
         chunk_forward_inference(*bad, scale, cfg)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_prefill_resets_across_flag_blocks_bitwise(D):
+    """The scan holds the reset bytes of 64 chunks per register and rotates blocks every 64
+    chunks: documents starting at chunks 1, 63, 64, 65, 127, 128, 150 and 199 of a 200-chunk
+    sequence (row 0; row 1 without documents) equal one forward-only call per document, bit for
+    bit."""
+    from atomic_gdn2 import make_blr_trainable
+    from atomic_gdn2.inference import chunk_forward_inference
+    B, H, nc = 2, 2, 200
+    L = 64 * nc
+    banner(f"prefill reset blocks D={D} L={L}")
+    xs, scale = _inputs(B, H, L, D, seed=19)
+    xs = [x.cuda() for x in xs]
+    starts = [64 * c for c in (1, 63, 64, 65, 127, 128, 150, 199)]
+    cfg = _cfg(64)
+    o, h = chunk_forward_inference(*xs, scale, cfg, segment_ids=_doc_ids(B, L, [starts, []]).cuda())
+    fn = make_blr_trainable(cfg, scale)
+    with torch.no_grad():
+        cuts = [0] + starts + [L]
+        hb = None
+        for a, c in zip(cuts[:-1], cuts[1:]):
+            ob, hb = fn(*(x[:1, :, a:c] for x in xs))
+            assert torch.equal(o[:1, :, a:c], ob), (a, c)
+        assert torch.equal(h[:1], hb)
+        o1, h1 = fn(*(x[1:] for x in xs))
+    assert torch.equal(o[1:], o1) and torch.equal(h[1:], h1)
+
+
+def test_prefill_pairs_with_resets_across_flag_blocks():
+    """bt = 128 with wy_eps > 0 (damped pairs) and documents past chunk 64 of the 64-token
+    grid, against the float64 oracle at one (b,h) sequence."""
+    from atomic_gdn2.inference import chunk_forward_inference
+    O = _oracle()
+    B, H, D, L = 1, 2, 128, 128 * 40 + 50
+    xs, scale = _inputs(B, H, L, D, seed=20)
+    starts = [[128 * 31, 128 * 33, 128 * 39, 128 * 40 + 7]]
+    ids = _doc_ids(B, L, starts)
+    cfg = _cfg(128, wy_eps=1e-3)
+    o, h = chunk_forward_inference(*(x.cuda() for x in xs), scale, cfg, segment_ids=ids.cuda())
+    ro, rh = O.chunk_forward_inference_ref(*(x[:, :1].double() for x in xs), scale, O.OracleCfg.from_cfg(cfg),
+                                           segment_ids=ids)
+    assert rel_l2(o[:, :1], ro) <= GATE and rel_l2(h[:, :1], rh) <= GATE
