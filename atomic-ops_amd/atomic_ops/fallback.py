@@ -12,15 +12,16 @@ path runs chunk ``config.bt`` with ``config.wy_eps``; everywhere else it runs
 chunk only, so with wy_eps > 0 the chunk size is part of the operator; with wy_eps = 0 the
 chunked WY form equals the token recurrence for every chunk size and only the rounding
 depends on it.  This shim therefore runs chunk ``config.bt`` with ``config.wy_eps`` when the
-HIP kernels support that chunk size, and otherwise (the bt = 128 / 256 presets) the
-reference's off-TPU operator: wy_eps = 0, at the kernels' chunk of 64.  Products are fp32
+HIP kernels support that pair (bt 64 and 128 with any wy_eps, bt 256 without damping), and
+otherwise (the bt = 256 presets, whose wy_eps > 0) the reference's off-TPU operator:
+wy_eps = 0, at the kernels' chunk of 64.  Products are fp32
 everywhere (the legacy kernels use Precision.HIGHEST).
 """
 from __future__ import annotations
 
 
 from atomic_gdn2 import make_cfg, make_blr_trainable
-from atomic_gdn2.pipeline import SUPPORTED_BT
+from atomic_gdn2.pipeline import kernels_support
 
 from .configs import DEFAULT_CONFIG, KernelConfig, validate_inputs
 
@@ -37,7 +38,7 @@ def _operator(config: KernelConfig, scale: float):
 
 def operator_cfg(config: KernelConfig):
     """The operator configuration that stands in for ``config`` (see the module docstring)."""
-    bt = config.bt if config.bt in SUPPORTED_BT else 64
+    bt = config.bt if kernels_support(config.bt, config.wy_eps) else 64
     eps = config.wy_eps if bt == config.bt else 0.0
     return make_cfg(bt=bt, bc=bt // 2, score_bs=bt, bs2=32, mb=min(config.mb, bt), diag="btl",
                     clip=config.clip, wy_eps=eps, dot_mode="highest", solve_dot_mode="highest",

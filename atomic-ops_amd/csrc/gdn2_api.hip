@@ -36,10 +36,15 @@ int validate(const gdn2_desc* d) {
     if (m < GDN2_DOT_HIGHEST || m > GDN2_DOT_DEFAULT) return fail(GDN2_ERR_INVALID, "unknown dot mode");
   if (d->diag != GDN2_DIAG_BTL && d->diag != GDN2_DIAG_LEAN) return fail(GDN2_ERR_INVALID, "unknown diag");
   if (!(d->clip > 0.0)) return fail(GDN2_ERR_INVALID, "clip must be positive");
-  if (d->bt != gdn2::T && d->bt != 2 * gdn2::T)
-    return fail(GDN2_ERR_UNSUPPORTED, "this build supports bt in {64, 128}");
-  if (d->bt == 2 * gdn2::T && d->bs2 > gdn2::T)
-    return fail(GDN2_ERR_UNSUPPORTED, "this build supports bs2 <= 64 at bt == 128");
+  // bt = 256 without damping is the 64-token operator exactly (the damping is what couples the
+  // tokens of a chunk beyond the state); with wy_eps > 0 its quarters would need a second
+  // damped-state chain in the backward, which this build does not have
+  if (d->bt != gdn2::T && d->bt != 2 * gdn2::T && d->bt != 4 * gdn2::T)
+    return fail(GDN2_ERR_UNSUPPORTED, "this build supports bt in {64, 128, 256}");
+  if (d->bt == 4 * gdn2::T && d->wy_eps > 0.0)
+    return fail(GDN2_ERR_UNSUPPORTED, "this build supports bt == 256 with wy_eps == 0 only");
+  if (d->bt > gdn2::T && d->bs2 > gdn2::T)
+    return fail(GDN2_ERR_UNSUPPORTED, "this build supports bs2 <= 64 at bt >= 128");
   if (d->D != 64 && d->D != 128) return fail(GDN2_ERR_UNSUPPORTED, "this build supports D in {64, 128}");
   if (d->bs2 < 16) return fail(GDN2_ERR_UNSUPPORTED, "this build supports bs2 >= 16");
   if (d->seq_ld != 0 && d->seq_ld < d->L) return fail(GDN2_ERR_INVALID, "seq_ld must be 0 or >= L");

@@ -113,3 +113,22 @@ def test_bt128_checkpoints_segments_and_forward_only():
         o, hf = make_blr_trainable(cfg, scale)(*to_dev(arrs), torch.from_numpy(h0).cuda())
     torch.cuda.synchronize()
     assert torch.equal(o, ref["o"]) and torch.equal(hf, ref["h_final"])
+
+
+@pytest.mark.parametrize("kw", [dict(score_bs=256, bs2=32), dict(score_bs=128, bs2=64, mb=16)],
+                         ids=lambda kw: ",".join(f"{k}={v}" for k, v in kw.items()))
+def test_bt256_undamped_matches_oracle(kw):
+    """bt = 256 with wy_eps = 0 (the undamped operator, which the kernels run as 64-token chunks)
+    against the float64 oracle run at bt = 256 (its own two-level scores and 256-row ladder
+    inverse); with wy_eps > 0 the descriptor is rejected."""
+    from atomic_gdn2 import make_blr_trainable
+    D = 128
+    cfg = base_cfg(**{**dict(bt=256, bc=128, mb=8, wy_eps=0.0), **kw})
+    banner(f"bt=256 vs oracle {kw}")
+    scale = D ** -0.5
+    arrs = mk_inputs(1, 512, 2, D, 33, g=0.05, layout="bhld")       # two 256-token chunks
+    h0 = (np.random.default_rng(4).standard_normal((1, 2, D, D)) * 0.1).astype(np.float32)
+    hip = grad(cfg, scale, arrs, h0)
+    compare(hip, oracle_grad(cfg, scale, arrs, h0), GATE, ("o", "h_final") + NAMES + ("dh0",))
+    with pytest.raises(ValueError, match="wy_eps == 0 only"):
+        make_blr_trainable(cfg.with_(wy_eps=1e-3), scale)(*to_dev(arrs))
