@@ -26,14 +26,13 @@ from . import _lib
 from .precision import sanitize
 
 _FINAL_CLIP = 1e4
-# chunk sizes (cfg.bt) the HIP kernels run (bt = 128 as pairs of 64-token half chunks, exactly;
-# bt = 256 only without damping, where it is the 64-token operator)
+# chunk sizes (cfg.bt) the HIP kernels run (bt = 128 / 256 as 2 / 4 parts of 64 tokens, exactly)
 SUPPORTED_BT = (64, 128, 256)
 
 
 def kernels_support(bt, wy_eps):
     """Whether the HIP kernels run chunk ``bt`` with damping ``wy_eps``."""
-    return bt in (64, 128) or (bt == 256 and wy_eps == 0.0)
+    return bt in SUPPORTED_BT and 0.0 <= wy_eps < 1.0
 
 
 # How the residual keeps the state for the backward (gdn2_desc.state_ckpt): K >= 1 keeps the

@@ -12,9 +12,9 @@ path runs chunk ``config.bt`` with ``config.wy_eps``; everywhere else it runs
 chunk only, so with wy_eps > 0 the chunk size is part of the operator; with wy_eps = 0 the
 chunked WY form equals the token recurrence for every chunk size and only the rounding
 depends on it.  This shim therefore runs chunk ``config.bt`` with ``config.wy_eps`` when the
-HIP kernels support that pair (bt 64 and 128 with any wy_eps, bt 256 without damping), and
-otherwise (the bt = 256 presets, whose wy_eps > 0) the reference's off-TPU operator:
-wy_eps = 0, at the kernels' chunk of 64.  Products are fp32
+HIP kernels run that chunk (64, 128 and 256: every preset, as the reference's TPU path runs
+them), and otherwise the reference's off-TPU operator: wy_eps = 0, at the kernels' chunk of
+64.  Products are fp32
 everywhere (the legacy kernels use Precision.HIGHEST).
 """
 from __future__ import annotations

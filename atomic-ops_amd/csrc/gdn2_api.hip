@@ -36,13 +36,10 @@ int validate(const gdn2_desc* d) {
     if (m < GDN2_DOT_HIGHEST || m > GDN2_DOT_DEFAULT) return fail(GDN2_ERR_INVALID, "unknown dot mode");
   if (d->diag != GDN2_DIAG_BTL && d->diag != GDN2_DIAG_LEAN) return fail(GDN2_ERR_INVALID, "unknown diag");
   if (!(d->clip > 0.0)) return fail(GDN2_ERR_INVALID, "clip must be positive");
-  // bt = 256 without damping is the 64-token operator exactly (the damping is what couples the
-  // tokens of a chunk beyond the state); with wy_eps > 0 its quarters would need a second
-  // damped-state chain in the backward, which this build does not have
+  // bt = 128 / 256 run as 2 / 4 parts of 64 tokens (Cfg::group); without damping every chunk
+  // size is the 64-token operator
   if (d->bt != gdn2::T && d->bt != 2 * gdn2::T && d->bt != 4 * gdn2::T)
     return fail(GDN2_ERR_UNSUPPORTED, "this build supports bt in {64, 128, 256}");
-  if (d->bt == 4 * gdn2::T && d->wy_eps > 0.0)
-    return fail(GDN2_ERR_UNSUPPORTED, "this build supports bt == 256 with wy_eps == 0 only");
   if (d->bt > gdn2::T && d->bs2 > gdn2::T)
     return fail(GDN2_ERR_UNSUPPORTED, "this build supports bs2 <= 64 at bt >= 128");
   if (d->D != 64 && d->D != 128) return fail(GDN2_ERR_UNSUPPORTED, "this build supports D in {64, 128}");
@@ -56,18 +53,19 @@ int validate(const gdn2_desc* d) {
 int validate_residual(const gdn2_desc* d) {
   const int st = validate(d);
   if (st) return st;
-  if (d->bt == 2 * gdn2::T && d->wy_eps > 0.0 && d->state_ckpt == 0)
-    return fail(GDN2_ERR_UNSUPPORTED, "bt == 128 with wy_eps > 0 needs state_ckpt >= 1");
+  if (d->bt > gdn2::T && d->wy_eps > 0.0 && d->state_ckpt == 0)
+    return fail(GDN2_ERR_UNSUPPORTED, "bt >= 128 with wy_eps > 0 needs state_ckpt >= 1");
   return GDN2_OK;
 }
 
-// bt = 128 runs as pairs of 64-token half chunks (gdn2_kernels.hpp, Cfg::pair).  With
-// wy_eps > 0 the backward's state recompute needs both halves of a pair in one block, so the
-// checkpoint interval (in half chunks) is rounded up to an even number.
-bool damped_pairs(const gdn2_desc* d) { return d->bt == 2 * gdn2::T && d->wy_eps > 0.0; }
+// bt = 128 / 256 run as 2 / 4 parts of 64 tokens (gdn2_kernels.hpp, Cfg::group).  With
+// wy_eps > 0 the backward's state recompute needs every part of a big chunk in one block, so
+// the checkpoint interval (in 64-token chunks) is rounded up to a multiple of the group.
+int damped_group(const gdn2_desc* d) { return d->wy_eps > 0.0 ? d->bt / gdn2::T : 1; }
 int eff_ckpt(const gdn2_desc* d) {
   const int k = d->state_ckpt;
-  return (damped_pairs(d) && (k & 1)) ? k + 1 : k;
+  const int G = damped_group(d);
+  return (G > 1 && k % G) ? k + (G - k % G) : k;
 }
 
 // Pieces of the two-level block-local rescaling (fwd/scores.py:42-75): for each row block
@@ -107,10 +105,10 @@ gdn2::Cfg make_cfg(const gdn2_desc* d) {
   c.mb = d->mb < gdn2::T ? d->mb : gdn2::T;    // leaves inside a 64-token (half) chunk
   c.nc = d->L / gdn2::T;
   c.seq_ld = d->seq_ld ? d->seq_ld : d->L;
-  c.pair = damped_pairs(d) ? 1 : 0;
+  c.group = damped_group(d);
   // the score pieces inside one 64-token (half) chunk: at bt = 128 the pieces of the 128
   // geometry that lie inside a half are the 64 geometry's with the outer block capped at 64
-  // (the pieces crossing the halves are carried by the state, see Cfg::pair)
+  // (the pieces crossing the halves are carried by the state, see Cfg::group)
   make_pieces(gdn2::T, d->score_bs < gdn2::T ? d->score_bs : gdn2::T, d->bs2, &c.pieces);
   return c;
 }
@@ -222,7 +220,7 @@ size_t gdn2_bwd_workspace_bytes(const gdn2_desc* d) {
   const Dims x = dims(d);
   size_t n = 5 * align_up(x.n_chunks * x.tD * 4) + 2 * align_up(x.n_chunks * x.DD * 4) +
              align_up(x.n_chunks * x.D * 4);
-  if (damped_pairs(d)) n += align_up(x.n_chunks / 2 * x.DD * 4);     // eps Wp_b^T dv_new_b per pair
+  if (damped_group(d) > 1) n += align_up(x.n_chunks * x.DD * 4);     // EZ(j + 1) per 64-token part j
   return n;
 }
 
@@ -426,7 +424,7 @@ int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v,
   float* dlast = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.D * 4);
   float* xo = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
   float* yo = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.DD * 4);
-  float* ez = damped_pairs(d) ? at<float>(workspace, o2) : nullptr;
+  float* ez = damped_group(d) > 1 ? at<float>(workspace, o2) : nullptr;
 
   gdn2::BwdPreArgs pa{aqk, qg, d_o, xo, yo, (int)x.n_chunks, cfg};
   hipError_t e = timed(6, s, [&] { return gdn2::launch_bwd_pre(d->D, pa, s); });

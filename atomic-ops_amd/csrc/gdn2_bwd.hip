@@ -177,12 +177,14 @@ __global__ __launch_bounds__(NWW * WAVE) __attribute__((amdgpu_waves_per_eu(2)))
   static_assert(NKT % NWW == 0 && NKB % 2 == 0, "key tile groups, value block parity");
   __shared__ float4 sA[2 * SLAB];                // [buf][mat * 4 + tile][lane]
   __shared__ __attribute__((aligned(16))) float sTr[NWW * 16 * TRP];
-  // Cfg::pair: the damped state of a pair's second half (its dWp uses it), [wave][kb][lane],
-  // stored while stepping through the first half (K is even: a block holds whole pairs)
+  // Cfg::group = G > 1: the damped state h_d of the next part (its dWp uses it), [wave][kb][lane],
+  // stepped through the parts as the forward scan does (K is a multiple of G: a block holds
+  // whole big chunks)
   __shared__ float4 sHd[NWW * NKB * WAVE];
   const Cfg& cf = a.cfg;
   const int K = a.ckpt, nc = a.nc, nblk = (nc + K - 1) / K;
-  const bool damp = cf.pair != 0;
+  const int G = cf.group;
+  const float inv_eps = G > 1 ? 1.f / cf.wy_eps : 0.f;
   const int lin = xcd_remap(gridDim.x);
   const int grp = lin % NG, blk = (lin / NG) % nblk, bh = lin / (NG * nblk);
   const int c0 = blk * K, c1 = min(nc, c0 + K);
@@ -217,11 +219,11 @@ __global__ __launch_bounds__(NWW * WAVE) __attribute__((amdgpu_waves_per_eu(2)))
     base[(12 + w) * WAVE + l] = src[2];
   };
   auto dh_at = [&](int c, int kb) { return ld4(sbase(a.dh_next_f + chunk_idx(c) * D * D + frag_blk(kt, kb, D)) + lo4); };
-  // eps Wp_b^T dv_new_b of the pair chunk c belongs to (scan_bwd), added to dh_next in the first
-  // half's dKg; zero where unused
+  // EZ(part + 1) of chunk c (scan_bwd; Cfg::group), added to dh_next in its dKg; zero where
+  // unused (no damping, or the last part of a big chunk)
   auto ez_at = [&](int c, int kb) {
-    if (!damp || (c & 1)) return make_float4(0.f, 0.f, 0.f, 0.f);
-    return ld4(sbase(a.ez_f + ((size_t)bh * (nc / 2) + c / 2) * D * D + frag_blk(kt, kb, D)) + lo4);
+    if (G == 1 || c % G == G - 1) return make_float4(0.f, 0.f, 0.f, 0.f);
+    return ld4(sbase(a.ez_f + chunk_idx(c) * D * D + frag_blk(kt, kb, D)) + lo4);
   };
 
   f4 h[NKB];
@@ -246,7 +248,9 @@ __global__ __launch_bounds__(NWW * WAVE) __attribute__((amdgpu_waves_per_eu(2)))
   for (int c = c0; c < c1; ++c) {
     const size_t ch = chunk_idx(c), tb = ch * T * D;
     const bool step = c + 1 < c1;
-    const bool second = damp && (c & 1);            // a pair's second half: dWp from h_d
+    const int pj = G > 1 ? c % G : 0;                // part of a damped big chunk
+    const bool second = pj > 0;                      // dWp (the erase term) from h_d
+    const bool dterm = pj > 0 && pj < G - 1;         // gamma's gradient through Delta
     float4 kga[4] = {}, gm = make_float4(0.f, 0.f, 0.f, 0.f);
     if (step) {
       // Kg^T block (kt, u) in the A-operand layout = FA(Kg) block (u, kt) transposed
@@ -300,18 +304,28 @@ __global__ __launch_bounds__(NWW * WAVE) __attribute__((amdgpu_waves_per_eu(2)))
       part = fmaf(dhc.y, hp.y, part);
       part = fmaf(dhc.z, hp.z, part);
       part = fmaf(dhc.w, hp.w, part);
+      if (dterm) {
+        // sum_v EZ(pj + 1) Delta(pj), Delta = (h - h_d) / eps (gdn2_kernels.hpp, Cfg::group)
+        const float4 e4 = ezb[pb];
+        part = fmaf(e4.x, (hp.x - hpw.x) * inv_eps, part);
+        part = fmaf(e4.y, (hp.y - hpw.y) * inv_eps, part);
+        part = fmaf(e4.z, (hp.z - hpw.z) * inv_eps, part);
+        part = fmaf(e4.w, (hp.w - hpw.w) * inv_eps, part);
+      }
       if (step) {
         // the forward scan's Kg^T v_new chain (gdn2_scan.hip), the same MFMAs in the same order
         f4 hn = {0.f, 0.f, 0.f, 0.f};
         mma_chain<DOT, 4>(hn, 0, [&](int u) { return kga[u]; }, [&](int u) { return cur[(12 + u) * WAVE + l]; });
         drain(hn);
         const float gmv[4] = {gm.x, gm.y, gm.z, gm.w};
-        if (damp && !(c & 1)) {
-          // the forward scan's damped state (gdn2_scan.hip), bit for bit
+        if (G > 1 && pj < G - 1) {
+          // the forward scan's damped state of the next part (gdn2_scan.hip), bit for bit:
+          // h_d(pj + 1) = san(e^gamma h_d(pj) + (1 - eps) Kg^T v_new), h_d(0) = h
           const float ome = cf.ome;
-          sHd[(w * NKB + kb) * WAVE + l] =
-              make_float4(state_update(h[kb][0], gmv[0], ome * hn[0], clip), state_update(h[kb][1], gmv[1], ome * hn[1], clip),
-                          state_update(h[kb][2], gmv[2], ome * hn[2], clip), state_update(h[kb][3], gmv[3], ome * hn[3], clip));
+          float4& hd = sHd[(w * NKB + kb) * WAVE + l];
+          const float4 b0 = pj == 0 ? f4_to_float4(h[kb]) : hd;
+          hd = make_float4(state_update(b0.x, gmv[0], ome * hn[0], clip), state_update(b0.y, gmv[1], ome * hn[1], clip),
+                           state_update(b0.z, gmv[2], ome * hn[2], clip), state_update(b0.w, gmv[3], ome * hn[3], clip));
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) h[kb][e] = state_update(h[kb][e], gmv[e], hn[e], clip);

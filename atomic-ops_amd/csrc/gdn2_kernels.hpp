@@ -39,17 +39,21 @@ struct Cfg {
   int diag, dot_mode, solve_mode, b3_mode, mb;
   int nc;        // chunks per (batch, head) sequence of this segment
   int seq_ld;    // tokens between consecutive (batch, head) sequences of the raw operator tensors
-  // pair = 1: the operator's chunk is bt = 128 with wy_eps > 0, run as pairs of 64-token half
-  // chunks (a = chunks 2m, b = 2m + 1).  The WY inverse of the 128 chunk is block lower
-  // triangular; its diagonal blocks are the halves' own inverses (I + (1-eps) Akk_hh)^-1 and
-  // its off-diagonal block A_ba = -A_bb (1-eps) Akk_ba A_aa.  Expanding v_new = A (wv - X h)
-  // with it, the first half is the 64-chunk form, and the second half is the 64-chunk form
-  // from the damped state h_d = e^gamma_a h + (1-eps) Kg_a^T v_new_a instead of the state
-  // h_mid = e^gamma_a h + Kg_a^T v_new_a entering it: the cross-half scores (Aqk_ba, Akk_ba)
-  // are carried by the state, exactly, and only the erase term sees the damping.  The output
-  // and the state update use h_mid.  With wy_eps = 0 (pair = 0) bt = 128 and bt = 64 are the
-  // same operator.
-  int pair;
+  // group = G in {2, 4}: the operator's chunk is bt = 64 G with wy_eps > 0, run as G parts of
+  // 64 tokens (part j = chunk c with c % G == j).  The WY inverse of the big chunk is block
+  // lower triangular; its diagonal blocks are the parts' own inverses (I + (1-eps) Akk_jj)^-1,
+  // and forward substitution over the blocks gives, exactly, part j = the 64-chunk form whose
+  // erase term reads the damped state h_d(j) instead of the state h(j) entering the part:
+  //   h(0) = h_d(0) = the state entering the big chunk,
+  //   h(j+1) = e^gamma_j h(j) + Kg_j^T v_new_j,   h_d(j+1) = e^gamma_j h_d(j) + (1-eps) Kg_j^T v_new_j
+  // (the cross-part scores are carried by the states; only the erase term sees the damping).
+  // The output and the carried state use h.  Equivalently h_d(j) = h(j) - eps Delta(j) with
+  // Delta(0) = 0, Delta(j+1) = e^gamma_j Delta(j) + Kg_j^T v_new_j, so the backward adds to the
+  // undamped form the cotangent of Delta: EZ(j) = eps Wp_j^T dv_new_j + e^gamma_j EZ(j+1)
+  // (j >= 1, EZ(G) = 0), which reaches part j-1's Kg^T v_new term and, through the decay,
+  // gamma_j's gradient (sum_v EZ(j+1) Delta(j)).  group = 1: no damping across parts (with
+  // wy_eps = 0 every chunk size is the 64-chunk operator).
+  int group;
   PieceList pieces;
 };
 

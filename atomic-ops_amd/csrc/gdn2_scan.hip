@@ -68,9 +68,10 @@ struct FwdOps {
 // ROLE < 0: V wave (v_new tile w); ROLE = j >= 0: O wave of output tile j (wave 4 + j).
 // OUT = false: no output (the O waves keep only their state rows and the barriers; the
 // output is then computed chunk-parallel from h_pre and v_new, gdn2_fwd.hip).
-// With Cfg::pair (bt = 128, wy_eps > 0) the state rows also go to sHd after each pair's first
-// half as the damped state h_d = state_update(h, gamma, (1 - eps) Kg^T v_new), from which the
-// V waves compute the second half's v_new (the O waves and the state update keep h).
+// With Cfg::group = G > 1 (bt = 64 G, wy_eps > 0) the state rows also go to sHd after each part
+// j < G - 1 as the damped state h_d(j+1) = state_update(h_d(j), gamma, (1 - eps) Kg^T v_new)
+// (h_d(0) = h), from which the V waves compute the next part's v_new (the O waves and the
+// state update keep h).
 template <int D, int MODE, bool OUT, int ROLE>
 __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, float4* sHd, float4* sV) {
   constexpr int NH = D / 16, NVB = D / 16;
@@ -132,11 +133,15 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
     }
   };
 
-  const bool damp = a.cfg.pair != 0;
+  // Cfg::group = G > 1: chunk c is part c % G of a damped big chunk; the state rows keep the
+  // damped state h_d of the next part in registers (hdr) and pass it to the V waves through sHd
+  const int G = a.cfg.group;
   const float ome = a.cfg.ome;
-  // ODD: c is odd (the loop below is unrolled by two from c = 0), i.e. a pair's second half
+  f4 hdr = {0.f, 0.f, 0.f, 0.f};
+  // the loop below is unrolled by two from c = 0 (register sets A / B); odd is c's parity
   auto step = [&](const FwdOps<NH>& op, int c, FwdOps<NH>& nx, int cn, auto odd) {
-    constexpr bool ODD = decltype(odd)::value;
+    (void)odd;
+    const int part = G > 1 ? c % G : 0;
     const size_t ch = (size_t)bh * nc + c, tb = ch * T * D;
     const size_t tbn = base(cn) * T * D, sbn = base(cn) * T * T;
     const int rst_next = reset_at(cn);
@@ -147,7 +152,7 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
     // ---- window A ----
     float4 hb[NH];
     if constexpr (V || O) {
-      const float4* src = (V && ODD && damp) ? sHd : sH;
+      const float4* src = (V && part > 0) ? sHd : sH;
 #pragma unroll
       for (int kb = 0; kb < NH; ++kb) hb[kb] = src[kb * WAVE + l];
     }
@@ -207,13 +212,12 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
       }
       drain(hn);
       const float gmv[4] = {op.gm.x, op.gm.y, op.gm.z, op.gm.w};
-      if (!ODD && damp) {
-        float4 hd;
-        hd.x = state_update(h[0], gmv[0], ome * hn[0], clip);
-        hd.y = state_update(h[1], gmv[1], ome * hn[1], clip);
-        hd.z = state_update(h[2], gmv[2], ome * hn[2], clip);
-        hd.w = state_update(h[3], gmv[3], ome * hn[3], clip);
-        sHd[w * WAVE + l] = hd;       // read in the next step's window A, after its barrier
+      if (part < G - 1) {
+        // h_d(part + 1) = san(e^gamma h_d(part) + (1 - eps) Kg^T v_new), h_d(0) = h(0)
+        const f4 hb0 = part == 0 ? h : hdr;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) hdr[e] = state_update(hb0[e], gmv[e], ome * hn[e], clip);
+        sHd[w * WAVE + l] = f4_to_float4(hdr);   // read in the next step's window A, after its barrier
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) h[e] = state_update(h[e], gmv[e], hn[e], clip);
@@ -290,7 +294,7 @@ template <int D, int MODE, bool OUT>
 __global__ __launch_bounds__(8 * WAVE) void scan_fwd_kernel(ScanFwdArgs a) {
   constexpr int NH = D / 16;
   __shared__ float4 sH[NH * WAVE];     // h_pre of the current chunk, [key tile][lane]
-  __shared__ float4 sHd[NH * WAVE];    // the damped state of a pair's second half (Cfg::pair)
+  __shared__ float4 sHd[NH * WAVE];    // the damped state of the next part (Cfg::group)
   __shared__ float4 sV[4 * WAVE];      // v_new tiles, [token tile][lane]
   switch (wave_id()) {
     case 4: scan_fwd_role<D, MODE, OUT, 0>(a, sH, sHd, sV); break;
@@ -353,19 +357,22 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
     op.gm = ld4(a.gl + ch * D + 16 * w + 4 * g);
   };
 
-  // Cfg::pair: steps alternate between a pair's second half (s even, chunk nc - 1 - s odd) and
-  // its first half (s odd).  The second half's eps Wp^T dv_new (the cotangent its damped
-  // state passes to the first half's Kg^T v_new, beyond the state's own) is added to dh in the
-  // first half's Kg dh term and written out for bwd_state_rc; the carry itself is unchanged.
-  const bool damp = a.cfg.pair != 0;
+  // Cfg::group = G > 1: chunk c = nc - 1 - s is part c % G of a damped big chunk, and the parts
+  // come in reverse.  ez carries EZ(part + 1), the cotangent of the damping correction Delta
+  // (gdn2_kernels.hpp, Cfg::group): it is added to dh in this part's Kg dh term and written out
+  // for bwd_state_rc, then EZ(part) = eps Wp^T dv_new + e^gamma EZ(part + 1) follows (zero
+  // after part 0); the carry dh itself is the undamped form's.
+  const int G = a.cfg.group;
   const float eps = a.cfg.wy_eps;
   float4 ez = make_float4(0.f, 0.f, 0.f, 0.f);
   auto step = [&](const BwdOps& op, int s, BwdOps& nx, int sn, auto sodd) {
-    constexpr bool FIRST_HALF = decltype(sodd)::value;
+    (void)sodd;
     const size_t ch = chunk(s), tb = ch * T * D;
     const size_t chn = chunk(sn), tbn = chn * T * D;
+    const int c = nc - 1 - s, part = G > 1 ? c % G : 0;
+    const bool carry_ez = G > 1 && part < G - 1;
     const float4 db = f4_to_float4(dh);
-    const float4 dbk = (FIRST_HALF && damp) ? add4(db, ez) : db;
+    const float4 dbk = carry_ez ? add4(db, ez) : db;
     f4 p[4];
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) {
@@ -377,11 +384,8 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
     }
     // dh entering this chunk's step (mega.py:35) as FA(dh_next) block (w, slice)
     const float4 dhv = wave_transpose16(sTr + w * 16 * TRP, db, r, g);
-    if (FIRST_HALF && damp) {
-      const size_t c = ch - (size_t)bh * nc;
-      stg4(a.ez_f + ((size_t)bh * (nc / 2) + c / 2) * D * D + frag_blk(w, vb, D) + 4 * l,
-           wave_transpose16(sTr + w * 16 * TRP, ez, r, g));
-    }
+    if (carry_ez)
+      stg4(a.ez_f + ch * D * D + frag_blk(w, vb, D) + 4 * l, wave_transpose16(sTr + w * 16 * TRP, ez, r, g));
     drain(p[0], p[1], p[2], p[3]);
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) sP[(w * 4 + ti) * WAVE + l] = f4_to_float4(p[ti]);
@@ -423,8 +427,14 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
     float4 dvv = db;
     if (red) dvv = frag_transpose_lds(sDB, tp, lp);     // FA(dv_new) block (tp, slice)
     drain(z);
-    if (!FIRST_HALF && damp) ez = scale4(f4_to_float4(z), eps);
     const float gmv[4] = {op.gm.x, op.gm.y, op.gm.z, op.gm.w};
+    if (G > 1) {
+      if (part > 0)
+        ez = make_float4(fmaf(exp_nonpos(gmv[0]), ez.x, eps * z[0]), fmaf(exp_nonpos(gmv[1]), ez.y, eps * z[1]),
+                         fmaf(exp_nonpos(gmv[2]), ez.z, eps * z[2]), fmaf(exp_nonpos(gmv[3]), ez.w, eps * z[3]));
+      else
+        ez = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     const float yv[4] = {op.yy.x, op.yy.y, op.yy.z, op.yy.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) dh[e] = sanitize((yv[e] + dh[e] * exp_nonpos(gmv[e])) - z[e], clip);

@@ -64,7 +64,12 @@ def test_memory_estimate_and_recommendation():
 
 
 @pytest.mark.gpu
-def test_legacy_entry_points_match_oracle():
+@pytest.mark.parametrize("preset", ["KAGGLE_SMALL", "KAGGLE_MEDIUM"])
+def test_legacy_entry_points_match_oracle(preset):
+    """The preset's own operator (chunk config.bt = 128 / 256 with its wy_eps, as the
+    reference's TPU path runs it) through the legacy entry points, against the float64 oracle
+    at that chunk; the forward also against the token recurrence."""
+    config = {"KAGGLE_SMALL": KAGGLE_SMALL, "KAGGLE_MEDIUM": KAGGLE_MEDIUM}[preset]
     if not torch.cuda.is_available():
         pytest.skip("no ROCm GPU")
     import sys
@@ -73,13 +78,13 @@ def test_legacy_entry_points_match_oracle():
     from oracle.gdn2_oracle import OracleCfg, grad_ref, token_serial_ref
     from conftest import mk_inputs
     print("[gpu-test] legacy atomic_ops vs oracle", flush=True)
-    arrs = mk_inputs(1, 256, 2, 128, seed=3, g=0.05)               # (B, L, H, D)
+    arrs = mk_inputs(1, 512, 2, 128, seed=3, g=0.05)               # (B, L, H, D)
     rng = np.random.default_rng(7)
     h0 = (rng.normal(size=(1, 2, 128, 128)) * 0.1).astype(np.float32)
     scale = 128 ** -0.5
     dev = [torch.from_numpy(a).cuda() for a in arrs]
-    o, hf = atomic_ops.gdn2_forward(*dev, scale, h0=torch.from_numpy(h0).cuda(), config=KAGGLE_SMALL)
-    assert o.shape == (1, 256, 2, 128) and hf.shape == (1, 2, 128, 128)
+    o, hf = atomic_ops.gdn2_forward(*dev, scale, h0=torch.from_numpy(h0).cuda(), config=config)
+    assert o.shape == (1, 512, 2, 128) and hf.shape == (1, 2, 128, 128)
     t = [torch.from_numpy(a).double() for a in arrs]
     sw = lambda x: x.transpose(1, 2)
     q, k, v, w, b, g = (sw(x) for x in t)
@@ -88,12 +93,10 @@ def test_legacy_entry_points_match_oracle():
     assert rel_l2(o, ro) < 2e-3 and rel_l2(hf, rh) < 2e-3
     # gradients of sum(o^2) + sum(h_final^2) through the trainable entry point
     xs = [x.clone().requires_grad_(True) for x in dev]
-    o2, hf2 = atomic_ops.gdn2_forward_trainable(*xs, scale, config=KAGGLE_SMALL)
+    o2, hf2 = atomic_ops.gdn2_forward_trainable(*xs, scale, config=config)
     ((o2 * o2).sum() + (hf2 * hf2).sum()).backward()
-    # the preset's own operator: chunk config.bt = 128 with its wy_eps (the kernels run bt = 128)
     ref = grad_ref(q, k, v, w, b, g, scale, None,
-                   OracleCfg(bt=KAGGLE_SMALL.bt, score_bs=KAGGLE_SMALL.bt, bs2=32, mb=KAGGLE_SMALL.mb,
-                             wy_eps=KAGGLE_SMALL.wy_eps))
+                   OracleCfg(bt=config.bt, score_bs=config.bt, bs2=32, mb=config.mb, wy_eps=config.wy_eps))
     for x, n in zip(xs, ("dq", "dk", "dv", "dw", "db", "dg")):
         assert rel_l2(x.grad, sw(ref[n])) < 2e-3, n
 
@@ -115,13 +118,15 @@ def test_legacy_pallas_shapes():
 
 
 def test_operator_cfg_follows_the_reference_dispatch():
-    """Presets whose chunk the kernels do not run (bt = 256) get the reference's off-TPU
-    operator (wy_eps = 0, any chunk size); a supported chunk (64, 128) keeps its own wy_eps."""
+    """Every preset runs its own chunk (128, 256) with its wy_eps, as the reference's TPU path
+    does; a chunk the kernels do not run would get the reference's off-TPU operator (wy_eps = 0,
+    which is the same for every chunk size)."""
     from atomic_ops.fallback import operator_cfg
-    for preset in (KAGGLE_MEDIUM, KAGGLE_LARGE):
+    for preset in (KAGGLE_SMALL, KAGGLE_MEDIUM, KAGGLE_LARGE):
         c = operator_cfg(preset)
-        assert c.wy_eps == 0.0 and c.clip == preset.clip and c.bt == 64
-    c = operator_cfg(KAGGLE_SMALL)
-    assert c.bt == 128 and c.wy_eps == KAGGLE_SMALL.wy_eps and c.mb == KAGGLE_SMALL.mb
+        assert (c.bt, c.wy_eps, c.clip) == (preset.bt, preset.wy_eps, preset.clip)
+        assert c.mb == min(preset.mb, preset.bt)
+    c = operator_cfg(KernelConfig(bt=512, bc=256, mb=8, clip=1e4, wy_eps=1e-3))
+    assert c.bt == 64 and c.wy_eps == 0.0
     c = operator_cfg(KernelConfig(bt=64, bc=32, mb=8, clip=1e4, wy_eps=1e-3))
     assert c.bt == 64 and c.wy_eps == 1e-3 and c.mb == 8

@@ -91,7 +91,6 @@ def test_residual_layout_and_workspaces():
 
 @pytest.mark.parametrize("kw,msg", [
     (dict(bt=512, bc=256, score_bs=128), "bt in"),
-    (dict(bt=256, bc=128, score_bs=128, wy_eps=1e-3), "wy_eps == 0 only"),
     (dict(bt=128, bc=64, score_bs=128, bs2=128, g_max=2.5), "bs2 <= 64"),
     (dict(D=96), "D in"),
     (dict(bs2=8, g_max=20.0), "bs2 >= 16"),
