@@ -43,10 +43,8 @@ enum { GDN2_DIAG_BTL = 0, GDN2_DIAG_LEAN = 1 };
 enum { GDN2_OK = 0, GDN2_ERR_INVALID = 1, GDN2_ERR_UNSUPPORTED = 2, GDN2_ERR_HIP = 3 };
 
 /* One segment call.  Field meaning follows BLRConfig (atomic_gdn2/config.py:38-60).
- * Supported by this build: bt in {64, 128} (128 as pairs of 64-token half chunks; with
- * wy_eps > 0 it needs state_ckpt >= 1) and bt = 256 with wy_eps == 0 (run as 64-token chunks:
- * without damping every chunk size is the same operator), D in {64, 128}, L % bt == 0,
- * bs2 in {16, 32, 64},
+ * Supported by this build: bt in {64, 128, 256} (128 and 256 as 2 and 4 parts of 64 tokens;
+ * with wy_eps > 0 they need state_ckpt >= 1), D in {64, 128}, L % bt == 0, bs2 in {16, 32, 64},
  * bs2 | score_bs | bt, mb a power of two dividing bt.
  *   L        tokens of this segment (a multiple of bt).
  *   seq_ld   tokens between the starts of consecutive (b, h) sequences in the raw operator
