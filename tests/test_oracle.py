@@ -390,30 +390,54 @@ def test_nan_gate_is_zeroed_not_ignored(monkeypatch):
     monkeypatch.setattr(O, "exp_nonpos", orig)
 
 
-# ---------------------------------------------------------------- bt = 128 as pairs of halves
-def _pair_forward(q, k, v, w, b, g, scale, h0, cfg128):
-    """The kernels' algebra for bt = 128 (gdn2_kernels.hpp, Cfg::pair), restated in float64
-    from the chunk-64 pieces of the oracle: scores and WY inverse inside each 64-token half,
-    then a scan whose second halves erase from the damped state
-    h_d = e^gamma_a h + (1 - eps) Kg_a^T v_new_a while o and the state update use h."""
-    eps = cfg128.wy_eps
-    c64 = cfg128.with_(bt=64, score_bs=min(cfg128.score_bs, 64))
+# ---------------------------------------------------------------- bt = 128 / 256 as parts of 64
+def _group_forward(q, k, v, w, b, g, scale, h0, cfg, G):
+    """The kernels' algebra for bt = 64 G (gdn2_kernels.hpp, Cfg::group), restated in float64
+    from the chunk-64 pieces of the oracle: scores and WY inverse inside each 64-token part, then
+    a scan whose parts j >= 1 erase from the damped state h_d(j) (h_d(0) = h(0),
+    h_d(j+1) = e^gamma_j h_d(j) + (1 - eps) Kg_j^T v_new_j) while o and the state update use h."""
+    eps = cfg.wy_eps
+    c64 = cfg.with_(bt=64, score_bs=min(cfg.score_bs, 64))
     ch = lambda t: O.to_chunks(t, 64)
     qr, kr, vr, wr, br, gr = map(ch, (q, k, v, w, b, g))
     gc = O.chunk_gc(gr)
     Aqk, Akk = O.blr_scores_ref(qr, kr, br, gc, scale, c64)
-    A = O.ladder_inverse(Akk, eps, 64, min(cfg128.mb, 64))
+    A = O.ladder_inverse(Akk, eps, 64, min(cfg.mb, 64))
     wp, u, kg, qg, gl = O.recompute_wy_ref(qr, kr, vr, wr, br, gc, A, c64)
     h, hd, outs = h0, None, []
     for c in range(qr.shape[-3]):
-        vn = u[..., c, :, :] - wp[..., c, :, :] @ (hd if c % 2 else h)
+        j = c % G
+        vn = u[..., c, :, :] - wp[..., c, :, :] @ (hd if j else h)
         outs.append(scale * qg[..., c, :, :] @ h + Aqk[..., c, :, :] @ vn)
         hn = kg[..., c, :, :].transpose(-1, -2) @ vn
         dec = torch.exp(gl[..., c, :])[..., :, None]
-        if c % 2 == 0:
-            hd = dec * h + (1.0 - eps) * hn
+        if j < G - 1:
+            hd = dec * (hd if j else h) + (1.0 - eps) * hn
         h = dec * h + hn
     return torch.cat(outs, -2), h
+
+
+def _pair_forward(q, k, v, w, b, g, scale, h0, cfg128):
+    return _group_forward(q, k, v, w, b, g, scale, h0, cfg128, 2)
+
+
+@pytest.mark.parametrize("kw", [dict(wy_eps=0.05), dict(wy_eps=1e-3, bs2=64, mb=16), dict(wy_eps=0.2, score_bs=64)])
+def test_bt256_equals_four_parts_with_damped_erase(kw):
+    """The bt = 256 oracle (scores over 256 rows, ladder inverse over 256) equals the four-part
+    algebra of the kernels, values and gradients, to float64 rounding; the pair algebra (bt 128)
+    on the same inputs does not."""
+    q, k, v, w, b, g, h0 = rand_inputs(1, 2, 512, 16, 42, gscale=0.05, h0=True)
+    cfg = O.OracleCfg(bt=256, score_bs=256, bs2=32, mb=8).with_(**kw)
+    xs = [x.clone().requires_grad_(True) for x in (q, k, v, w, b, g, h0)]
+    o1, h1 = O.forward_ref(*xs[:6], 0.25, xs[6], cfg)
+    g1 = torch.autograd.grad((o1 * o1).sum() + (h1 * h1).sum(), xs)
+    o2, h2 = _group_forward(*xs[:6], 0.25, xs[6], cfg, 4)
+    g2 = torch.autograd.grad((o2 * o2).sum() + (h2 * h2).sum(), xs)
+    assert rel(o1, o2) < 1e-10 and rel(h1, h2) < 1e-10
+    assert max(rel(a, b_) for a, b_ in zip(g1, g2)) < 1e-9
+    if cfg.wy_eps > 0.01:
+        o3, _ = _group_forward(*xs[:6], 0.25, xs[6], cfg.with_(bt=128, score_bs=min(cfg.score_bs, 128)), 2)
+        assert rel(o1, o3) > 1e-4
 
 
 @pytest.mark.parametrize("kw", [dict(wy_eps=0.05), dict(wy_eps=0.05, bs2=64), dict(wy_eps=1e-3, score_bs=64, mb=16),
