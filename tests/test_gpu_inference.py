@@ -161,6 +161,7 @@ CASES = [
     dict(bt=64, L=3 * 64 + 40, starts=[[128, 3 * 64 + 11], []]),        # boundary in the tail
     dict(bt=64, L=29, starts=[[7], [0]]),                                # tail only
     dict(bt=128, L=384 + 20, starts=[[256], [128, 384 + 5]], wy_eps=1e-3),  # damped pairs
+    dict(bt=256, L=768 + 130, starts=[[512], [256, 768 + 70]], wy_eps=0.02),  # damped four parts
     dict(bt=64, L=256, starts=None, state_dtype=torch.bfloat16, tau=3.0),
     dict(bt=64, L=64 * 5 + 9, starts=[[64], [192, 64 * 5 + 1]], D=64, bf16_inputs=True),
 ]
