@@ -9,11 +9,11 @@
 // products without any data movement, and it is lane l of block (slice, w) of the
 // transposed state in fragment layout, so saving it is one float4 store per lane.
 //
-// Products whose contraction runs over the key dimension (Wp h, Kg dh) are split by key
-// rows across waves: each wave multiplies with its own state rows and writes a 16x16 partial
-// tile per output row tile to LDS; a fixed-order sum over waves finishes them.  Products
-// over the chunk's time axis (Kg^T v_new, Wp^T dv_new) read v_new / dv_new from LDS in
-// B-operand layout.  A-operands stream from global memory as one coalesced
+// Products whose contraction runs over the key dimension (Wp h, Kg dh) are computed by waves
+// of their own, one token tile each over all keys, with the state read from LDS (every wave
+// writes its rows there at the end of a step): no cross-wave reduction.  Products over the
+// chunk's time axis (Kg^T v_new, Wp^T dv_new) read v_new / dv_new from LDS in B-operand
+// layout.  A-operands stream from global memory as one coalesced
 // float4 per lane and block (fragment layout, written by the WY kernel) and are prefetched
 // one chunk ahead into the second of two register sets; the chunk loop is unrolled by two so
 // the sets never need copying, and all prefetch loads are unconditional so the compiler's
@@ -315,93 +315,107 @@ __device__ __forceinline__ float4 frag_transpose_lds(const float4* xs, int u, in
                      f[4 * (4 * gg + 3 + c) + e]);
 }
 
+template <int NH>
 struct BwdOps {
-  float4 kg[4];    // FA(Kg) block (ti, w):    Kg[16ti + r][16w + 4g .. +3]
+  float4 kg[NH];   // dv waves: FA(Kg) block (tp, kb):  Kg[16 tp + r][16 kb + 4 g .. +3]
   float4 wpT[4];   // FA(Wp^T) block (w, u):   Wp^T[16w + r][16u + 4g .. +3]
-  float4 xx;       // FA(X^T) block (slice, tp), lane lp: X = Aqk^T dO (the dv_new reduction pair)
+  float4 xx;       // dv waves: FA(X^T) block (slice, tp), lane lp: X = Aqk^T dO
   float4 yy;       // FA(Y^T) block (slice, w): Y = s Qg^T dO, this lane's 4 state rows
   float4 gm;       // gamma[16w + 4g .. +3]
 };
 
 // Reverse scan, chain only: the dO terms X = Aqk^T dO and Y = s Qg^T dO do not depend on dh and
-// come precomputed per chunk (bwd_pre_kernel).
-template <int D, int MODE>
-__global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) {
-  constexpr int NW = D / 16, NVB = D / 16;
-  __shared__ float4 sP[NW * 4 * WAVE];     // partial (Kg dh) tiles, [wave][ti][lane]
-  __shared__ float4 sDB[4 * WAVE];         // dv_new tiles in B-operand layout, [u][lane]
-  __shared__ __attribute__((aligned(16))) float sTr[NW * 16 * TRP];   // per-wave transpose tiles
+// come precomputed per chunk (bwd_pre_kernel).  D/16 waves; wave w keeps key rows 16 w .. + 15
+// of the dh slice in registers.  Per chunk, two barriers:
+//   window A  dv waves 0..3 (token tile tp = w): dv_new = san(X + Kg (dh + EZ)) over all D
+//             keys, dh read from LDS (sDH, written by every wave at the end of the previous
+//             step), the tile to LDS (sDB) and, transposed, to dv_new_f;
+//   window B  every wave: z = Wp^T dv_new (its key rows, over the chunk's tokens from sDB),
+//             dh = san(Y + e^gamma dh - z), then dh (+ the next chunk's EZ) to sDH.
+// RED: a dv wave (waves 0..3): the role is a compile-time parameter, so that each role's code
+// is straight-line and its prefetch loads unconditional.
+template <int D, int MODE, bool RED>
+__device__ __forceinline__ void scan_bwd_role(const ScanBwdArgs& a, float4* sDH, float4* sDB, float* sTr) {
+  constexpr int NW = D / 16, NVB = D / 16, NH = D / 16;
+  (void)NW;
   const float clip = a.cfg.clip;
   const int nc = a.nc;
   const int lin = xcd_remap(gridDim.x);
   const int vb = lin % NVB, bh = lin / NVB, c0 = 16 * vb;
   const int tid = threadIdx.x, l = lane_id(), r = l & 15, g = l >> 4, w = wave_id();
   const int tp = (tid & 255) >> 6, lp = tid & 63;
-  const bool red = tid < 4 * WAVE;
 
   f4 dh;
 #pragma unroll
   for (int e = 0; e < 4; ++e) dh[e] = a.dhf[(size_t)bh * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r];
+  sDH[w * WAVE + l] = f4_to_float4(dh);
 
   // step s processes chunk nc-1-s; steps past the last are clamped to chunk 0 (loads only)
   auto chunk = [&](int s) { return (size_t)bh * nc + (s < nc ? nc - 1 - s : 0); };
-  auto load_all = [&](BwdOps& op, int s) {
+  auto load_all = [&](BwdOps<NH>& op, int s) {
     const size_t ch = chunk(s), tb = ch * T * D;
+    if constexpr (RED) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      op.kg[i] = ld4(a.kg_f + tb + frag_blk(i, w, D) + 4 * l);
-      op.wpT[i] = ld4(a.wpT_f + tb + frag_blk(w, i, T) + 4 * l);
+      for (int kb = 0; kb < NH; ++kb) op.kg[kb] = ld4(a.kg_f + tb + frag_blk(tp, kb, D) + 4 * lp);
+      op.xx = ld4(a.x_f + tb + frag_blk(vb, tp, T) + 4 * lp);
     }
-    op.xx = ld4(a.x_f + tb + frag_blk(vb, tp, T) + 4 * lp);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) op.wpT[i] = ld4(a.wpT_f + tb + frag_blk(w, i, T) + 4 * l);
     op.yy = ld4(a.y_f + ch * D * D + frag_blk(vb, w, D) + 4 * l);
     op.gm = ld4(a.gl + ch * D + 16 * w + 4 * g);
   };
 
   // Cfg::group = G > 1: chunk c = nc - 1 - s is part c % G of a damped big chunk, and the parts
   // come in reverse.  ez carries EZ(part + 1), the cotangent of the damping correction Delta
-  // (gdn2_kernels.hpp, Cfg::group): it is added to dh in this part's Kg dh term and written out
-  // for bwd_state_rc, then EZ(part) = eps Wp^T dv_new + e^gamma EZ(part + 1) follows (zero
-  // after part 0); the carry dh itself is the undamped form's.
+  // (gdn2_kernels.hpp, Cfg::group): it is added to dh in this part's Kg dh term (through sDH)
+  // and written out for bwd_state_rc, then EZ(part) = eps Wp^T dv_new + e^gamma EZ(part + 1)
+  // follows (zero after part 0); the carry dh itself is the undamped form's.
   const int G = a.cfg.group;
   const float eps = a.cfg.wy_eps;
   float4 ez = make_float4(0.f, 0.f, 0.f, 0.f);
-  auto step = [&](const BwdOps& op, int s, BwdOps& nx, int sn, auto sodd) {
+  auto carries_ez = [&](int c) { return G > 1 && c >= 0 && c % G < G - 1; };
+  auto step = [&](const BwdOps<NH>& op, int s, BwdOps<NH>& nx, int sn, auto sodd) {
     (void)sodd;
     const size_t ch = chunk(s), tb = ch * T * D;
     const size_t chn = chunk(sn), tbn = chn * T * D;
     const int c = nc - 1 - s, part = G > 1 ? c % G : 0;
-    const bool carry_ez = G > 1 && part < G - 1;
     const float4 db = f4_to_float4(dh);
-    const float4 dbk = carry_ez ? add4(db, ez) : db;
-    f4 p[4];
+    // ---- window A: dv_new tile tp over all keys ----
+    if constexpr (RED) {
+      float4 hb[NH];
 #pragma unroll
-    for (int ti = 0; ti < 4; ++ti) {
-      p[ti] = f4{0.f, 0.f, 0.f, 0.f};
-      mma16<MODE>(p[ti], op.kg[ti], dbk);
-      GDN2_SCHED_FENCE();
-      nx.kg[ti] = ld4(a.kg_f + tbn + frag_blk(ti, w, D) + 4 * l);
-      GDN2_SCHED_FENCE();
+      for (int kb = 0; kb < NH; ++kb) hb[kb] = sDH[kb * WAVE + l];
+      f4 acc = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (MODE == DOT_HIGHEST) {
+#pragma unroll
+        for (int kb = 0; kb < NH; ++kb) {
+          mma16<MODE>(acc, op.kg[kb], hb[kb]);
+          GDN2_SCHED_FENCE();
+          nx.kg[kb] = ld4(a.kg_f + tbn + frag_blk(tp, kb, D) + 4 * lp);
+          GDN2_SCHED_FENCE();
+        }
+      } else {
+#pragma unroll
+        for (int kb = 0; kb < NH; kb += 2) {
+          mma32<MODE>(acc, op.kg[kb], hb[kb], op.kg[kb + 1], hb[kb + 1]);
+          GDN2_SCHED_FENCE();
+          nx.kg[kb] = ld4(a.kg_f + tbn + frag_blk(tp, kb, D) + 4 * lp);
+          nx.kg[kb + 1] = ld4(a.kg_f + tbn + frag_blk(tp, kb + 1, D) + 4 * lp);
+          GDN2_SCHED_FENCE();
+        }
+      }
+      drain(acc);
+      sDB[tid] = san4(add4(op.xx, f4_to_float4(acc)), clip);
+      nx.xx = ld4(a.x_f + tbn + frag_blk(vb, tp, T) + 4 * lp);
     }
     // dh entering this chunk's step (mega.py:35) as FA(dh_next) block (w, slice)
     const float4 dhv = wave_transpose16(sTr + w * 16 * TRP, db, r, g);
-    if (carry_ez)
+    if (carries_ez(c))
       stg4(a.ez_f + ch * D * D + frag_blk(w, vb, D) + 4 * l, wave_transpose16(sTr + w * 16 * TRP, ez, r, g));
-    drain(p[0], p[1], p[2], p[3]);
-#pragma unroll
-    for (int ti = 0; ti < 4; ++ti) sP[(w * 4 + ti) * WAVE + l] = f4_to_float4(p[ti]);
-    __syncthreads();
-    // dv_new = san(Aqk^T dO + Kg dh): fixed-order sum over waves, then the dO term
-    if (red) {
-      float4 sm = sP[tid];
-#pragma unroll
-      for (int w2 = 1; w2 < NW; ++w2) sm = add4(sm, sP[w2 * 4 * WAVE + tid]);
-      const float4 dv = san4(add4(op.xx, sm), clip);
-      sDB[tid] = dv;
-    }
-    nx.xx = ld4(a.x_f + tbn + frag_blk(vb, tp, T) + 4 * lp);
     nx.yy = ld4(a.y_f + chn * D * D + frag_blk(vb, w, D) + 4 * l);
     nx.gm = ld4(a.gl + chn * D + 16 * w + 4 * g);
     __syncthreads();
+    // ---- window B: this wave's key rows of dh ----
     float4 db4[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) db4[u] = sDB[u * WAVE + l];
@@ -425,7 +439,7 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
       }
     }
     float4 dvv = db;
-    if (red) dvv = frag_transpose_lds(sDB, tp, lp);     // FA(dv_new) block (tp, slice)
+    if constexpr (RED) dvv = frag_transpose_lds(sDB, tp, lp);     // FA(dv_new) block (tp, slice)
     drain(z);
     const float gmv[4] = {op.gm.x, op.gm.y, op.gm.z, op.gm.w};
     if (G > 1) {
@@ -438,13 +452,19 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
     const float yv[4] = {op.yy.x, op.yy.y, op.yy.z, op.yy.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) dh[e] = sanitize((yv[e] + dh[e] * exp_nonpos(gmv[e])) - z[e], clip);
+    // every dv wave has read sDH (window A) before the first barrier: the next chunk's rows
+    // may overwrite it here
+    const float4 dn = f4_to_float4(dh);
+    sDH[w * WAVE + l] = carries_ez(c - 1) ? add4(dn, ez) : dn;
     // stores last: the next step's waits for the prefetch loads above then do not also cover them
     stg4(a.dh_next_f + ch * D * D + frag_blk(w, vb, D) + 4 * l, dhv);
-    if (red) stg4(a.dv_new_f + tb + frag_blk(tp, vb, D) + 4 * lp, dvv);
+    if constexpr (RED) stg4(a.dv_new_f + tb + frag_blk(tp, vb, D) + 4 * lp, dvv);
+    __syncthreads();
   };
 
-  BwdOps A, B;
+  BwdOps<NH> A, B;
   load_all(A, 0);
+  __syncthreads();
   int s = 0;
   for (; s + 1 < nc; s += 2) {
     step(A, s, B, s + 1, std::false_type{});
@@ -453,6 +473,16 @@ __global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) 
   if (s < nc) step(A, s, B, s + 1, std::false_type{});
 #pragma unroll
   for (int e = 0; e < 4; ++e) a.dh0[(size_t)bh * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r] = dh[e];
+}
+
+template <int D, int MODE>
+__global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) {
+  constexpr int NW = D / 16;
+  __shared__ float4 sDH[NW * WAVE];        // dh (+ EZ) rows of every wave, B-operand layout, [w][lane]
+  __shared__ float4 sDB[4 * WAVE];         // dv_new tiles in B-operand layout, [u][lane]
+  __shared__ __attribute__((aligned(16))) float sTr[NW * 16 * TRP];   // per-wave transpose tiles
+  if (wave_id() < 4) scan_bwd_role<D, MODE, true>(a, sDH, sDB, sTr);
+  else scan_bwd_role<D, MODE, false>(a, sDH, sDB, sTr);
 }
 
 hipError_t launch_scan_fwd(int D, const ScanFwdArgs& a, hipStream_t s) {
