@@ -293,24 +293,21 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
   // 2b. column fragments FA(Kg^T) (D x T): the wave holds one whole 16x16 block of k per item
   //     (block wv + 8 it), which a per-wave LDS transpose (in S, free until the scores) turns
   //     into lane l of the transposed block: 4 consecutive tokens of one channel.
+  // The fragments stay in registers until the scores are done and the w / v loads issued: the
+  // vector memory counter is in order and counts stores, so stores issued here would hold back
+  // the score phase's q / k loads until they drained.
   float* tr = sS + wv * 16 * TRP;
   const bool colf = a.kgT_f != nullptr;
+  float4 kgv[NIT], qgv[NIT], ktv[NIT];
 #pragma unroll
   for (int it = 0; it < NIT; ++it) {
     const int f = tid + it * NT, blk = f >> 6, ln = f & 63;
     const int i = 16 * (blk / NKB) + (ln & 15), d = 16 * (blk % NKB) + 4 * (ln >> 4);
     const float4 gc = ld4(sG + i * LD + d);
     st4(sBK + i * LD + d, mul4(xb[it], xk[it]));
-    if (a.kg_f || a.kg) {
-      const float4 kg = san4(mul4(xk[it], expnp4(sub4(ld4(sG + (T - 1) * LD + d), gc))), clip);
-      if (a.kg_f) stg4(a.kg_f + tb + 4 * f, kg);
-      if (a.kg) stg4(a.kg + tb + i * D + d, kg);
-    }
-    if (a.qg_f || a.qg) {
-      const float4 qg = san4(mul4(xq[it], expnp4(gc)), clip);
-      if (a.qg_f) stg4(a.qg_f + tb + 4 * f, qg);
-      if (a.qg) stg4(a.qg + tb + i * D + d, qg);
-    }
+    kgv[it] = san4(mul4(xk[it], expnp4(sub4(ld4(sG + (T - 1) * LD + d), gc))), clip);
+    qgv[it] = san4(mul4(xq[it], expnp4(gc)), clip);
+    ktv[it] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (colf) {
       // lane (r, g): channel dc = 16 bj + r at tokens i0 + e, e = 0..3
       const int bi = blk / NKB, bj = blk % NKB, dc = 16 * bj + r, i0 = 16 * bi + 4 * g;
@@ -320,10 +317,9 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
       float kt[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) kt[e] = sanitize(kv4[e] * exp_nonpos(gl - sG[(i0 + e) * LD + dc]), clip);
-      stg4(a.kgT_f + tb + frag_blk(bj, bi, T) + 4 * l, make_float4(kt[0], kt[1], kt[2], kt[3]));
+      ktv[it] = make_float4(kt[0], kt[1], kt[2], kt[3]);
     }
   }
-  if (a.gl && tid < D) a.gl[(size_t)chunk * D + tid] = sG[(T - 1) * LD + tid];
   __syncthreads();
 
   // 3. scores, all pieces at once (scores.py:42-75): Aqk = s (q ra)(k cb)^T, Akk = (bk ra)(k cb)^T
@@ -377,6 +373,18 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
     xw[it] = in_ld4(w + o);
     xv[it] = in_ld4(v + o);
   }
+  // the fragment stores of step 2 (behind the w / v loads in the memory counter's order)
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int f = tid + it * NT, blk = f >> 6, ln = f & 63;
+    const int i = 16 * (blk / NKB) + (ln & 15), d = 16 * (blk % NKB) + 4 * (ln >> 4);
+    if (a.kg_f) stg4(a.kg_f + tb + 4 * f, kgv[it]);
+    if (a.kg) stg4(a.kg + tb + i * D + d, kgv[it]);
+    if (a.qg_f) stg4(a.qg_f + tb + 4 * f, qgv[it]);
+    if (a.qg) stg4(a.qg + tb + i * D + d, qgv[it]);
+    if (colf) stg4(a.kgT_f + tb + frag_blk(blk % NKB, blk / NKB, T) + 4 * l, ktv[it]);
+  }
+  if (a.gl && tid < D) a.gl[(size_t)chunk * D + tid] = sG[(T - 1) * LD + tid];
 
   // 4. masks + sanitize (scores.py:84-87); Se = (1-eps) Akk for the solve (solve.py:25)
   for (int f = tid; f < T * T / 4; f += NT) {
