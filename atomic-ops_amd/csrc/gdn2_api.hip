@@ -484,6 +484,18 @@ int gdn2_debug_gemm(int mode, const float* A, const float* B, float* C, int M, i
   return GDN2_OK;
 }
 
+int gdn2_debug_stream(int mode, const void* src, void* dst, size_t bytes, void* stream) {
+  if (mode < 0 || mode > 2) return fail(GDN2_ERR_INVALID, "stream probe mode must be 0 (copy), 1 (read) or 2 (fill)");
+  if (bytes == 0 || bytes % 4096) return fail(GDN2_ERR_INVALID, "stream probe bytes must be a positive multiple of 4096");
+  if (bytes / 4096 > 0x7fffffffu) return fail(GDN2_ERR_INVALID, "stream probe bytes too large");
+  if ((mode != 2 && !src) || !dst) return fail(GDN2_ERR_INVALID, "null buffer pointer");
+  if ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15)
+    return fail(GDN2_ERR_INVALID, "stream probe buffers must be 16-byte aligned");
+  hipError_t e = gdn2::launch_stream_probe(mode, src, dst, bytes / 16, reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "stream probe launch");
+  return GDN2_OK;
+}
+
 int gdn2_prof_begin(int max_launches) {
   if (max_launches <= 0) return fail(GDN2_ERR_INVALID, "max_launches must be positive");
   while ((int)g_prof.pool.size() < max_launches) {

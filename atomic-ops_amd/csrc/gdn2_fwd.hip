@@ -600,6 +600,34 @@ hipError_t launch_gemm_probe(int mode, const float* A, const float* B, float* C,
   return hipGetLastError();
 }
 
+// diagnostics: the HBM streaming rates the kernels' bytes are measured against.  One float4 per
+// thread, so each workgroup moves one contiguous 4 KB piece (the fastest of the plain patterns
+// on MI355X: several float4 per thread at a grid stride run 5-30 % slower).
+// MODE 0 copy src -> dst, 1 read src (dst[0] written only if the sum hits a sentinel, which
+// keeps the loads live), 2 fill dst.
+template <int MODE>
+__global__ __launch_bounds__(256) void stream_probe_kernel(const float4* __restrict__ src, float4* __restrict__ dst) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if constexpr (MODE == 0) {
+    dst[i] = src[i];
+  } else if constexpr (MODE == 1) {
+    const float4 x = src[i];
+    if (x.x + x.y + x.z + x.w == 1.2345e-30f) dst[0] = x;
+  } else {
+    dst[i] = make_float4(1.f, 2.f, 3.f, (float)(i & 255));
+  }
+}
+
+hipError_t launch_stream_probe(int mode, const void* src, void* dst, size_t n4, hipStream_t s) {
+  const dim3 grid((unsigned)(n4 / 256)), block(256);
+  const float4* a = static_cast<const float4*>(src);
+  float4* b = static_cast<float4*>(dst);
+  if (mode == 0) hipLaunchKernelGGL(stream_probe_kernel<0>, grid, block, 0, s, a, b);
+  else if (mode == 1) hipLaunchKernelGGL(stream_probe_kernel<1>, grid, block, 0, s, a, b);
+  else hipLaunchKernelGGL(stream_probe_kernel<2>, grid, block, 0, s, a, b);
+  return hipGetLastError();
+}
+
 hipError_t launch_wy_fwd(int D, const WyFwdArgs& a, hipStream_t s, bool bf16_inputs) {
   dispatch_mode(a.cfg.dot_mode, [&](auto m) {
     constexpr int M = decltype(m)::value;

@@ -202,6 +202,9 @@ hipError_t launch_bwd_wy(int D, const BwdWyArgs& a, hipStream_t s);
 // routine of the given dot mode.  M, N, K multiples of 16, at most 64 x 64 x 128.
 hipError_t launch_gemm_probe(int mode, const float* A, const float* B, float* C, int M, int N,
                              int K, hipStream_t s);
+// Diagnostics: stream n4 float4s (a multiple of 256): mode 0 copy src -> dst, 1 read src,
+// 2 fill dst.
+hipError_t launch_stream_probe(int mode, const void* src, void* dst, size_t n4, hipStream_t s);
 
 // Linear work index of this workgroup such that consecutive indices (workgroups of one
 // (batch, head), which read the same chunk operands) land on the same XCD (blockIdx % 8 picks

@@ -379,6 +379,39 @@ def bench_inference(cfg, seed):
     return out
 
 
+def hbm_stream_rates(n_bytes=1 << 30, reps=10):
+    """The box's HBM streaming rates (TB/s): copy (bytes read + written), read and fill, by the
+    library's one-float4-per-thread probe (gdn2_debug_stream), timed with HIP events on the
+    stream it runs on; the median of 3 rounds of `reps` launches after 3 untimed ones."""
+    import torch
+    from atomic_gdn2 import _lib
+    src = torch.ones(n_bytes // 4, device="cuda")
+    dst = torch.empty_like(src)
+    L_ = _lib.lib()
+    stream = _lib.stream_handle(src.device)
+    out = {}
+    for mode, name, moved in ((0, "copy", 2 * n_bytes), (1, "read", n_bytes), (2, "fill", n_bytes)):
+        def run():
+            _lib.check(L_.gdn2_debug_stream(mode, _lib.ptr(src), _lib.ptr(dst), n_bytes, stream),
+                       "gdn2_debug_stream")
+        for _ in range(3):
+            run()
+        per = []
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()                              # torch's current stream = the launch stream
+            for _ in range(reps):
+                run()
+            e1.record()
+            e1.synchronize()
+            per.append(e0.elapsed_time(e1) / reps)
+        ms = sorted(per)[1]
+        out[name] = round(moved / (ms * 1e-3) / 1e12, 3)
+    del src, dst
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_e2e_lm(seed, reps=4, rounds=3, warm=2):
     """Config 5: one training step of the reference's benchmark LM (8 GDN-2
     blocks, 34,873,952 parameters, B8 L2048, vocab 256, CE + clip_by_global_norm(1.0) + AdamW)
@@ -424,6 +457,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sweep", action="store_true", help="skip the config-3 sweep and the config-4 run")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end LM training step")
+    ap.add_argument("--hbm-rates", action="store_true",
+                    help="only print the HBM copy / read / fill rates of the streaming probe and exit")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 5 plain device copies of a 256 MiB fp32 buffer (reference for the "
                          "FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -466,6 +501,9 @@ def main():
         return
     if args.inference:
         print(json.dumps({"inference": bench_inference(cfg, args.seed)}), flush=True)
+        return
+    if args.hbm_rates:
+        print(json.dumps({"hbm_stream_tb_s": hbm_stream_rates()}), flush=True)
         return
     if args.profile_only:
         if args.seq_len == L_:
@@ -557,6 +595,12 @@ def main():
                      "unit": "TFLOP/s", "frac": round(ach / PEAK_FP32_MFMA, 4), "traffic": traffic},
         "reference_tpu_v5e_ms": 2.888,
     }
+    # each kernel's achieved HBM rate against what a plain copy reaches on this box
+    rates = hbm_stream_rates()
+    out["hbm_stream_tb_s"] = rates
+    for kd in kern.values():
+        if "hbm_gb_per_s" in kd:
+            kd["hbm_frac_of_copy"] = round(kd["hbm_gb_per_s"] / 1e3 / rates["copy"], 3)
     if not args.no_sweep:
         out["config2_seeds"] = seeds_config2(cfg)
         out["state_ckpt_table"] = state_ckpt_table(cfg, args.seed)

@@ -185,6 +185,12 @@ int gdn2_wy_stage(const gdn2_desc* d, const float* q, const float* k, const floa
 int gdn2_debug_gemm(int mode, const float* A, const float* B, float* C, int M, int N, int K,
                     void* stream);
 
+/* Diagnostics (no counterpart in the reference): the HBM streaming rate that the kernels' byte
+ * counts are judged against.  mode 0 copies `bytes` from src to dst, 1 reads src (dst: at least
+ * 16 bytes, written only on a sentinel sum), 2 fills dst; one float4 per thread, bytes a positive
+ * multiple of 4096, both buffers 16-byte aligned. */
+int gdn2_debug_stream(int mode, const void* src, void* dst, size_t bytes, void* stream);
+
 /* Per-kernel timing with HIP events recorded on the launch stream around every kernel.
  * gdn2_prof_begin(n) starts recording for up to n launches (process-wide, not re-entrant);
  * gdn2_prof_end synchronises on the recorded events and returns, per kernel id, the summed

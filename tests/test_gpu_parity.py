@@ -121,6 +121,29 @@ def test_mfma_tile_layout(mode, shape):
     assert rel_l2(C, ref) < 1e-6
 
 
+def test_stream_probe_copy_and_fill():
+    """The HBM rate probe moves exactly the bytes it is given (copy) and writes its pattern
+    (fill); the read mode leaves its sentinel target alone."""
+    from atomic_gdn2 import _lib
+    banner("stream probe 3 x 1 MiB")
+    n = 1 << 20
+    src = torch.randn(n // 4, device="cuda")
+    dst = torch.full((n // 4 + 1024,), -7.0, device="cuda")        # 4 KB guard past the end
+    L = _lib.lib()
+    _lib.check(L.gdn2_debug_stream(0, _lib.ptr(src), _lib.ptr(dst), n, _lib.stream_handle()), "copy")
+    torch.cuda.synchronize()
+    assert torch.equal(dst[: n // 4], src) and bool((dst[n // 4:] == -7.0).all())
+    _lib.check(L.gdn2_debug_stream(1, _lib.ptr(src), _lib.ptr(dst), n, _lib.stream_handle()), "read")
+    torch.cuda.synchronize()
+    assert torch.equal(dst[: n // 4], src)
+    _lib.check(L.gdn2_debug_stream(2, None, _lib.ptr(dst), n, _lib.stream_handle()), "fill")
+    torch.cuda.synchronize()
+    i = torch.arange(n // 16, device="cuda")
+    want = torch.stack([torch.ones_like(i, dtype=torch.float32), torch.full_like(i, 2, dtype=torch.float32),
+                        torch.full_like(i, 3, dtype=torch.float32), (i & 255).float()], 1).reshape(-1)
+    assert torch.equal(dst[: n // 4], want) and bool((dst[n // 4:] == -7.0).all())
+
+
 # ---------------------------------------------------------------- config 1 (golden)
 @pytest.fixture(scope="module")
 def cfg1():

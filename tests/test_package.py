@@ -139,6 +139,20 @@ def test_null_pointers_rejected_without_gpu_work():
     assert st == 1 and b"null" in _lib.lib().gdn2_last_error()
 
 
+@pytest.mark.parametrize("mode,nbytes,src,dst,msg", [
+    (3, 4096, 16, 16, b"mode"),
+    (0, 0, 16, 16, b"multiple of 4096"),
+    (0, 4095, 16, 16, b"multiple of 4096"),
+    (0, 4096, None, 16, b"null"),
+    (2, 4096, None, None, b"null"),
+    (0, 4096, 16, 24, b"aligned"),
+])
+def test_stream_probe_arguments_rejected_without_gpu_work(mode, nbytes, src, dst, msg):
+    from atomic_gdn2 import _lib
+    st = _lib.lib().gdn2_debug_stream(mode, src, dst, nbytes, None)
+    assert st == 1 and msg in _lib.lib().gdn2_last_error()
+
+
 def test_python_boundary_errors():
     from atomic_gdn2 import make_cfg, make_blr_trainable
     cfg = make_cfg(bt=64, bc=32, score_bs=64, bs2=32)
