@@ -2,7 +2,7 @@
 
 The kernels run a 128-token chunk as two 64-token halves; with wy_eps > 0 the second half
 erases from the damped state e^gamma_a h + (1 - eps) Kg_a^T v_new_a (gdn2_kernels.hpp,
-Cfg::pair), which is the block form of the 128 chunk's WY inverse.  The oracle computes the
+Cfg::group), which is the block form of the 128 chunk's WY inverse (bt = 256: four parts).  The oracle computes the
 128 chunk directly (its own two-level scores, ladder inverse over 128 rows, scan), so these
 tests pin that algebra (measured ~4e-7 rel-L2); as a control, the chunk-64 operator with the
 same eps = 0.05 differs from the bt = 128 oracle by more than twice the gate (~5e-3).
@@ -120,7 +120,7 @@ def test_bt128_checkpoints_segments_and_forward_only():
 def test_bt256_undamped_matches_oracle(kw):
     """bt = 256 with wy_eps = 0 (the undamped operator, which the kernels run as 64-token chunks)
     against the float64 oracle run at bt = 256 (its own two-level scores and 256-row ladder
-    inverse); with wy_eps > 0 the descriptor is rejected."""
+    inverse)."""
     from atomic_gdn2 import make_blr_trainable
     D = 128
     cfg = base_cfg(**{**dict(bt=256, bc=128, mb=8, wy_eps=0.0), **kw})
@@ -130,6 +130,34 @@ def test_bt256_undamped_matches_oracle(kw):
     h0 = (np.random.default_rng(4).standard_normal((1, 2, D, D)) * 0.1).astype(np.float32)
     hip = grad(cfg, scale, arrs, h0)
     compare(hip, oracle_grad(cfg, scale, arrs, h0), GATE, ("o", "h_final") + NAMES + ("dh0",))
+
+
+@pytest.mark.parametrize("which", ["make_cfg", "bt256"])
+def test_damped_big_chunks_bf16_inputs_forward(which):
+    """bf16 inputs at the damped bt = 128 of make_cfg() and at a damped bt = 256: the no-grad
+    forward widens them on load, equals the fp32 path on the same values bit for bit, and is
+    within the gate of the float64 oracle at that chunk size."""
+    from atomic_gdn2 import make_blr_trainable, make_cfg
+    from oracle import gdn2_oracle as O
+    cfg = make_cfg() if which == "make_cfg" else base_cfg(bt=256, bc=128, score_bs=128, bs2=64, mb=16,
+                                                          wy_eps=0.02)
+    banner(f"bf16 forward, damped bt={cfg.bt} eps={cfg.wy_eps}")
+    D = 128
+    scale = D ** -0.5
+    arrs = mk_inputs(1, 512, 2, D, 38, g=0.05, layout="bhld")
+    xb = [t.to(torch.bfloat16) for t in to_dev(arrs)]
+    h0 = torch.randn(1, 2, D, D, device="cuda", generator=torch.Generator("cuda").manual_seed(39)) * 0.1
+    fn = make_blr_trainable(cfg, scale)
+    with torch.no_grad():
+        ob, hb = fn(*xb, h0)
+        of, hf = fn(*[t.float() for t in xb], h0)
+    torch.cuda.synchronize()
+    assert ob.dtype == torch.float32 and torch.equal(ob, of) and torch.equal(hb, hf)
+    t = [x.double().cpu() for x in xb]
+    ro, rh = O.forward_ref(*t, scale, h0.double().cpu(), O.OracleCfg.from_cfg(cfg))
+    eo, eh = rel_l2(ob, ro), rel_l2(hb, rh)
+    banner(f"bf16 damped bt={cfg.bt} rel-L2 o {eo:.2e} h {eh:.2e}")
+    assert eo < GATE and eh < GATE
 
 
 BT256 = [

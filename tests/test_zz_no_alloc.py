@@ -15,21 +15,24 @@ def _need_gpu():
         pytest.skip("no ROCm GPU")
 
 
-def _cfg():
+def _cfg(**kw):
     from atomic_gdn2 import make_cfg
-    return make_cfg(bt=64, bc=32, score_bs=64, bs2=32, mb=8, wy_eps=0.0, dot_mode="highest",
-                    solve_dot_mode="highest", b3_dot_mode="highest")
+    base = dict(bt=64, bc=32, score_bs=64, bs2=32, mb=8, wy_eps=0.0, dot_mode="highest",
+                solve_dot_mode="highest", b3_dot_mode="highest")
+    return make_cfg(**{**base, **kw})
 
 
-def _run_both(B, H, L, D, seed, with_h0):
+def _run_both(B, H, L, D, seed, with_h0, cfg=None):
     from atomic_gdn2 import _lib
     from atomic_gdn2.synthetic import make_inputs
-    print(f"[gpu-test] noalloc vs gdn2_fwd B{B} H{H} L{L} D{D} seed {seed} h0={with_h0}", flush=True)
+    cfg = _cfg() if cfg is None else cfg
+    print(f"[gpu-test] noalloc vs gdn2_fwd B{B} H{H} L{L} D{D} seed {seed} h0={with_h0} bt={cfg.bt} "
+          f"wy_eps={cfg.wy_eps}", flush=True)
     xs, scale = make_inputs(B, H, L, D, seed=seed)
     h0 = None
     if with_h0:
         h0 = torch.randn(B, H, D, D, device="cuda", generator=torch.Generator("cuda").manual_seed(seed)) * 0.1
-    desc = _lib.make_desc(_cfg(), B, H, L, D, scale)
+    desc = _lib.make_desc(cfg, B, H, L, D, scale)
     lib = _lib.lib()
     stream = _lib.stream_handle()
     o1 = torch.empty(B, H, L, D, device="cuda")
@@ -49,6 +52,17 @@ def test_noalloc_forward_equals_gdn2_fwd_twice_second_smaller():
     (o1, h1), (o2, h2) = _run_both(2, 3, 512, 128, 11, True)
     assert torch.isfinite(o1).all() and torch.equal(o1, o2) and torch.equal(h1, h2)
     (o1, h1), (o2, h2) = _run_both(1, 2, 192, 64, 12, False)
+    assert torch.isfinite(o1).all() and torch.equal(o1, o2) and torch.equal(h1, h2)
+
+
+def test_noalloc_damped_big_chunks_equal_gdn2_fwd_twice_second_smaller():
+    """The reference's default geometry (make_cfg(): bt 128, wy_eps 1e-3, two damped parts per
+    chunk) and a damped bt = 256 (four parts), the second call smaller than the first."""
+    from atomic_gdn2 import make_cfg
+    (o1, h1), (o2, h2) = _run_both(2, 2, 1024, 128, 21, True, cfg=make_cfg())
+    assert torch.isfinite(o1).all() and torch.equal(o1, o2) and torch.equal(h1, h2)
+    cfg256 = _cfg(bt=256, bc=128, score_bs=128, bs2=64, mb=16, wy_eps=0.02)
+    (o1, h1), (o2, h2) = _run_both(1, 2, 512, 64, 22, False, cfg=cfg256)
     assert torch.isfinite(o1).all() and torch.equal(o1, o2) and torch.equal(h1, h2)
 
 
