@@ -601,17 +601,26 @@ def main():
     for kd in kern.values():
         if "hbm_gb_per_s" in kd:
             kd["hbm_frac_of_copy"] = round(kd["hbm_gb_per_s"] / 1e3 / rates["copy"], 3)
+    t_start = time.perf_counter()
+
+    def section(name, fn):
+        # one progress line per section on stderr (the JSON line on stdout stays the only output there)
+        r = fn()
+        print(f"[bench] {name} done at {time.perf_counter() - t_start:.0f} s", file=sys.stderr, flush=True)
+        return r
+
+    print(f"[bench] config 2: {ms:.4f} ms per grad-eval", file=sys.stderr, flush=True)
     if not args.no_sweep:
-        out["config2_seeds"] = seeds_config2(cfg)
-        out["state_ckpt_table"] = state_ckpt_table(cfg, args.seed)
-        out["dot_mode_ms"] = dot_mode_table(args.seed)
-        out["config3_sweep"] = sweep_config3(cfg, args.seed)
-        out["config4_long_context_fwd"] = bench_config4(cfg, args.seed)
-        out["inference"] = bench_inference(cfg, args.seed)
+        out["config2_seeds"] = section("config2 seeds", lambda: seeds_config2(cfg))
+        out["state_ckpt_table"] = section("state_ckpt table", lambda: state_ckpt_table(cfg, args.seed))
+        out["dot_mode_ms"] = section("dot modes", lambda: dot_mode_table(args.seed))
+        out["config3_sweep"] = section("config3 sweep", lambda: sweep_config3(cfg, args.seed))
+        out["config4_long_context_fwd"] = section("config4", lambda: bench_config4(cfg, args.seed))
+        out["inference"] = section("inference", lambda: bench_inference(cfg, args.seed))
     if not args.no_e2e:
-        out["config5_e2e_lm"] = bench_e2e_lm(args.seed)
+        out["config5_e2e_lm"] = section("config5 e2e LM", lambda: bench_e2e_lm(args.seed))
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline()
+        out["cpu_baseline"] = section("cpu baseline", cpu_baseline)
     print(json.dumps(out), flush=True)
 
 
