@@ -36,11 +36,12 @@ def kernels_support(bt, wy_eps):
 
 
 # How the residual keeps the state for the backward (gdn2_desc.state_ckpt): K >= 1 keeps the
-# state entering every K-th chunk and the backward recomputes the others inside its state
+# state entering the first chunk of each checkpoint block (blocks of K chunks; up to two chunks
+# left over become blocks of their own) and the backward recomputes the others inside its state
 # reductions; 0 keeps every chunk's (as the reference's residual does, pipeline.py:25).
-# K = 3 keeps a third of the states at the stored form's speed (MI355X, B4 H6 D128, rounds
-# interleaved: 0.5124 vs 0.5128 ms at L = 2048, 1.0218 vs 1.0209 ms at L = 4096); K = 4 keeps a
-# quarter for 2 % more time, K = 8 an eighth for 6 %.
+# K = 3 keeps 12 of every 32 states at or slightly below the stored form's time (MI355X, B4 H6
+# D128, rounds interleaved: 0.5024 vs 0.5043 ms at L = 2048, 0.9726 vs 0.9776 ms at L = 4096);
+# K = 4 keeps a quarter for 2 % more time, K = 8 an eighth for 8 %.
 DEFAULT_STATE_CKPT = 3
 
 

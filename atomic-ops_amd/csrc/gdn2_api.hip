@@ -132,8 +132,7 @@ void residual_sizes(const gdn2_desc* d, size_t sz[GDN2_RES_COUNT]) {
   const Dims x = dims(d);
   sz[GDN2_RES_AQK] = x.n_chunks * x.tT * 4;
   sz[GDN2_RES_A] = x.n_chunks * x.tT * 4;
-  const size_t K = (size_t)eff_ckpt(d);
-  const size_t nck = K > 0 ? (x.nc + K - 1) / K : x.nc;
+  const size_t nck = (size_t)gdn2::CkptBlocks((int)x.nc, eff_ckpt(d), damped_group(d)).nblk;
   sz[GDN2_RES_HPRE] = x.n_bh * nck * x.DD * 4;
   sz[GDN2_RES_VNEW] = x.n_chunks * x.tD * 4;
   sz[GDN2_RES_WPT] = x.n_chunks * x.tD * 4;

@@ -182,12 +182,36 @@ __global__ __launch_bounds__(NWW * WAVE) __attribute__((amdgpu_waves_per_eu(2)))
   // whole big chunks)
   __shared__ float4 sHd[NWW * NKB * WAVE];
   const Cfg& cf = a.cfg;
-  const int K = a.ckpt, nc = a.nc, nblk = (nc + K - 1) / K;
+  const int nc = a.nc;
   const int G = cf.group;
+  const CkptBlocks cb(nc, a.ckpt, G);
+  const int nblk = cb.nblk;
   const float inv_eps = G > 1 ? 1.f / cf.wy_eps : 0.f;
-  const int lin = xcd_remap(gridDim.x);
-  const int grp = lin % NG, blk = (lin / NG) % nblk, bh = lin / (NG * nblk);
-  const int c0 = blk * K, c1 = min(nc, c0 + K);
+  // Work order: each XCD (blockIdx % 8) takes whole (batch, head)s, all their full blocks first
+  // and then their remainder blocks, so that the short blocks are the ones left waiting for a
+  // free slot; the two key-tile groups of a block, which stage the same operands, are adjacent
+  // on one XCD.  When n_bh is not a multiple of 8: the same order over the whole grid.
+  int grp, blk, bh;
+  {
+    const int nF = cb.nfull * NG, nR = (nblk - cb.nfull) * NG;
+    const bool xcd = a.n_bh % 8 == 0;
+    const int per = xcd ? a.n_bh / 8 : a.n_bh;                 // (batch, head)s per XCD
+    const int x = xcd ? blockIdx.x % 8 : 0, p = xcd ? blockIdx.x / 8 : blockIdx.x;
+    int bhl, r;
+    if (p < per * nF) {
+      bhl = p / nF;
+      r = p % nF;
+      blk = r / NG;
+    } else {
+      const int q = p - per * nF;
+      bhl = q / nR;
+      r = q % nR;
+      blk = cb.nfull + r / NG;
+    }
+    grp = r % NG;
+    bh = x * per + bhl;
+  }
+  const int c0 = cb.start(blk), c1 = c0 + cb.len(blk);
   const int w = wave_id(), kt = grp * NWW + w, l = lane_id(), r = l & 15, g = l >> 4;
   const float sc = cf.scale, clip = cf.clip;
   float* tr = sTr + w * 16 * TRP;
@@ -1223,7 +1247,7 @@ hipError_t launch_bwd_state(int D, const BwdStateArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_bwd_state_rc(int D, const BwdStateRcArgs& a, hipStream_t s) {
-  const int nblk = (a.nc + a.ckpt - 1) / a.ckpt;
+  const int nblk = CkptBlocks(a.nc, a.ckpt, a.cfg.group).nblk;
   dispatch_mode(a.cfg.b3_mode, [&](auto m3) {
     dispatch_mode(a.cfg.dot_mode, [&](auto md) {
       constexpr int M3 = decltype(m3)::value, MD = decltype(md)::value;

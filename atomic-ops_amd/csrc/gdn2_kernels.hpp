@@ -81,12 +81,41 @@ struct WyFwdArgs {
   Cfg cfg;
 };
 
+// Checkpoint blocks of the selective recompute (state_ckpt = K): per (batch, head) the nc chunks
+// are cut into nfull = nc / K blocks of K chunks, then the R = nc % K chunks left over: into
+// blocks of S = Cfg::group chunks (one chunk each without damping; R is a multiple of S, since
+// nc and K are) when that makes at most two blocks, else into one block of R.  Every block
+// starts from a stored checkpoint (slot j of nblk per (batch, head)) and the backward steps the
+// state through it.  The short remainder blocks keep the backward's grid within one round: at
+// K = 3 and nc = 32 one remainder block of two chunks per (batch, head) needed 16 workgroups
+// more than the chip holds at once, which started only when the first blocks finished, while
+// single-chunk blocks dispatched after the full ones run in the slots that finish first (at the
+// cost of one more checkpoint).  K <= 1: every chunk is a block of its own.
+struct CkptBlocks {
+  int K, RL, nfull, nblk;    // RL: length of a remainder block
+  __host__ __device__ CkptBlocks(int nc, int K_, int S) : K(K_ > 1 ? K_ : 1), RL(1), nfull(0), nblk(0) {
+    nfull = nc / K;
+    const int R = nc - nfull * K;
+    const int s = K_ > 1 ? S : 1;
+    RL = R == 0 ? 1 : (R / s <= 2 ? s : R);
+    nblk = nfull + R / RL;
+  }
+  __host__ __device__ int start(int j) const { return j < nfull ? j * K : nfull * K + (j - nfull) * RL; }
+  __host__ __device__ int len(int j) const { return j < nfull ? K : RL; }
+  // the checkpoint slot of chunk c (its block's index when c starts a block), else -1
+  __host__ __device__ int slot(int c) const {
+    if (c < nfull * K) return c % K == 0 ? c / K : -1;
+    const int r = c - nfull * K;
+    return r % RL == 0 ? nfull + r / RL : -1;
+  }
+};
+
 // Forward state scan: reads FA(Wp), FA(Kg^T), FA(U^T), gl; writes the final state hf
 // (row-major D x D) and, when h_pre_f / v_new_f are set, per chunk the entering state h_pre as
 // FA(h_pre^T) (D x D) and v_new as FA(v_new^T) (D x T).  With o set it also reads FA(Qg),
 // FA(Aqk) and writes o (row-major T x D per chunk); otherwise out_fwd computes o.
-// ckpt = K >= 2: h_pre_f keeps only the state entering chunks c = 0, K, 2K, ... of each
-// (batch, head), as checkpoint c / K of ceil(nc / K); ckpt 0 or 1: every chunk's.
+// h_pre_f keeps the state entering the first chunk of each checkpoint block (CkptBlocks of
+// ckpt and Cfg::group), at its slot of nblk per (batch, head); ckpt 0 or 1: every chunk's.
 // reset (may be null): one byte per (batch, head) and chunk, row (b, h) of nc bytes; nonzero =
 // the state entering that chunk is zero (a document boundary at the chunk's first token; at
 // chunk 0 it replaces h0).
@@ -137,8 +166,8 @@ struct BwdStateArgs {
   Cfg cfg;
 };
 
-// bwd_state with the states recomputed from checkpoints: per (batch, head) block of ckpt = K
-// chunks the state entering the block (checkpoint FA(h^T), ceil(nc / K) per (batch, head)) is
+// bwd_state with the states recomputed from checkpoints: per (batch, head) checkpoint block
+// (CkptBlocks) the state entering the block (checkpoint FA(h^T), nblk per (batch, head)) is
 // stepped forward through the block, h <- san(e^gamma h + Kg^T v_new), from FA(Kg), gl and the
 // stored FA(v_new^T) -- the forward scan's own update, bit for bit -- and each chunk's
 // reductions use it as h_pre.  Outputs as BwdStateArgs.

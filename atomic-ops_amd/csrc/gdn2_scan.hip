@@ -138,6 +138,9 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
   const int G = a.cfg.group;
   const float ome = a.cfg.ome;
   f4 hdr = {0.f, 0.f, 0.f, 0.f};
+  // checkpoint blocks: the next chunk that starts one and its slot (no division per chunk)
+  const CkptBlocks ckb(nc, a.ckpt, G);
+  int ck_next = 0, ck_slot = 0;
   // the loop below is unrolled by two from c = 0 (register sets A / B); odd is c's parity
   auto step = [&](const FwdOps<NH>& op, int c, FwdOps<NH>& nx, int cn, auto odd) {
     (void)odd;
@@ -145,9 +148,10 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
     const size_t ch = (size_t)bh * nc + c, tb = ch * T * D;
     const size_t tbn = base(cn) * T * D, sbn = base(cn) * T * T;
     const int rst_next = reset_at(cn);
-    if (OWNS && a.h_pre_f && (a.ckpt <= 1 || c % a.ckpt == 0)) {
-      const size_t hi = a.ckpt <= 1 ? ch : (size_t)bh * ((nc + a.ckpt - 1) / a.ckpt) + c / a.ckpt;
-      stg4(a.h_pre_f + hi * D * D + frag_blk(vb, w, D) + 4 * l, f4_to_float4(h));
+    if (OWNS && a.h_pre_f && c == ck_next) {
+      stg4(a.h_pre_f + ((size_t)bh * ckb.nblk + ck_slot) * D * D + frag_blk(vb, w, D) + 4 * l, f4_to_float4(h));
+      ck_next += ckb.len(ck_slot);
+      ++ck_slot;
     }
     // ---- window A ----
     float4 hb[NH];

@@ -69,8 +69,10 @@ typedef struct gdn2_desc {
  *   AQK   (B,H,nc, bt*bt)  gated q.k scores, FRAG(Aqk)                         (pipeline.py:25)
  *   A     (B,H,nc,bt,bt)   the WY inverse (I + (1-eps) Akk)^-1, row-major        (pipeline.py:25)
  *   HPRE  (B,H,nck, D*D)   state entering each chunk (nck = nc, state_ckpt 0 or 1) or only
- *                          chunks 0, K, 2K, .. (state_ckpt = K: nck = ceil(nc / K)),
- *                          FRAG(h_pre^T)                                          (cd_slim.py:22)
+ *                          the first chunk of each checkpoint block (state_ckpt = K: chunks
+ *                          0, K, .., K (nc / K - 1), then the nc % K chunks left over as one
+ *                          block, or as blocks of bt / 64 chunks -- single chunks without
+ *                          damping -- when those are at most two), FRAG(h_pre^T)  (cd_slim.py:22)
  *   VNEW  (B,H,nc, D*bt)   v_new of each chunk, FRAG(v_new^T)                    (cd_slim.py:23)
  *   WPT   (B,H,nc, D*bt)   W = A (b k e^gc), FRAG(W^T)                           (cd_slim.py:17)
  *   KG    (B,H,nc, bt*D)   gated k, FRAG(Kg)                                     (cd_slim.py:20)

@@ -70,13 +70,17 @@ def test_recompute_other_dot_modes_and_segments():
             assert torch.equal(got[n], ref[n]), (kw, L, n)
 
 
-def test_checkpoints_are_the_stored_states():
-    """The residual of state_ckpt = 3 keeps FA(h_pre^T) of chunks 0, 3, 6 only, equal to the
-    stored form's h_pre of those chunks."""
+@pytest.mark.parametrize("L,keep", [(448, [0, 3, 6]), (512, [0, 3, 6, 7])],
+                         ids=["7 chunks", "8 chunks"])
+def test_checkpoints_are_the_stored_states(L, keep):
+    """The residual of state_ckpt = 3 keeps FA(h_pre^T) of the first chunk of each checkpoint
+    block only, equal to the stored form's h_pre of those chunks: blocks [0, 3), [3, 6), [6, 7)
+    for 7 chunks; for 8 the two chunks left over become single-chunk blocks (checkpoints 6, 7)."""
     from atomic_gdn2 import _lib
     from atomic_gdn2.synthetic import make_inputs
-    banner("checkpoint residual")
-    B, H, L, D = 1, 2, 448, 128                      # 7 chunks -> 3 checkpoints
+    banner(f"checkpoint residual L={L}")
+    B, H, D = 1, 2, 128
+    nc = L // 64
     xs, scale = make_inputs(B, H, L, D, seed=25)
     lib = _lib.lib()
     res = {}
@@ -90,12 +94,12 @@ def test_checkpoints_are_the_stored_states():
         _lib.check(lib.gdn2_fwd(ctypes.byref(desc), *map(_lib.ptr, xs), None, _lib.ptr(o), _lib.ptr(hf),
                                 _lib.ptr(r), _lib.ptr(ws), _lib.stream_handle()), "gdn2_fwd")
         torch.cuda.synchronize()
-        nck = 7 if ck == 0 else 3
+        nck = nc if ck == 0 else len(keep)
         hp = r[offs[2]:offs[2] + B * H * nck * D * D * 4].view(torch.float32)
         res[ck] = (_lib.decode_residual("h_pre", hp, B, H, nck, 64, D), o)
         if ck:
-            assert offs[3] - offs[2] < B * H * 4 * D * D * 4      # 3 states, not 7
+            assert offs[3] - offs[2] < B * H * (nck + 1) * D * D * 4      # len(keep) states, not nc
     stored, o0 = res[0]
     ckpts, o3 = res[3]
-    assert torch.equal(ckpts, stored[:, :, 0::3])
+    assert torch.equal(ckpts, stored[:, :, keep])
     assert torch.equal(o3, o0)

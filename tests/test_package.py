@@ -105,12 +105,13 @@ def test_descriptor_validation(kw, msg):
 
 
 def test_state_checkpoint_residual_layout():
-    """state_ckpt = K keeps ceil(nc / K) states per (batch, head) instead of nc; negative K is
-    rejected."""
+    """state_ckpt = K keeps one state per checkpoint block instead of nc: nc // K blocks of K,
+    then the nc % K chunks left over as single-chunk blocks when they are at most two (K = 3, 5
+    at nc = 32: two more), else as one block (K = 7: one of 4); negative K is rejected."""
     from atomic_gdn2 import _lib
     d0 = _desc()
     offs0, tot0 = _lib.residual_layout(d0)
-    for K, nck in ((1, 32), (2, 16), (3, 11), (32, 1), (100, 1)):
+    for K, nck in ((1, 32), (2, 16), (3, 12), (4, 8), (5, 8), (7, 5), (32, 1), (100, 1)):
         d = _desc()
         d.state_ckpt = K
         offs, tot = _lib.residual_layout(d)
