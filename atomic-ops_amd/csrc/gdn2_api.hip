@@ -275,8 +275,8 @@ int fwd_impl(const gdn2_desc* d, const void* q, const void* k, const void* v, co
   if (e != hipSuccess) return hip_fail(e, "wy_fwd launch");
 
   // Without a residual the scan computes the output itself and h_pre / v_new never leave it.
-  // Training with state_ckpt = K >= 1 likewise, keeping v_new and every K-th chunk's entering
-  // state (the backward recomputes the others).  Training with state_ckpt = 0 keeps every
+  // Training with state_ckpt = K >= 1 likewise, keeping v_new and the state entering each
+  // checkpoint block (gdn2::CkptBlocks; the backward recomputes the others).  Training with state_ckpt = 0 keeps every
   // chunk's h_pre and v_new: the scan carries only the state and the output follows
   // chunk-parallel from them.
   const int ck = eff_ckpt(d);
