@@ -1182,6 +1182,11 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdPreArgs a) {
 #pragma unroll
     for (int m = 0; m < NYW; ++m) ay[m][u] = ldg4(a.qg_f + tb + frag_blk(u, w + NW * m, D) + 4 * l);
   }
+  // dO in the same memory round trip (row-major items, scattered into dO^T below)
+  constexpr int NDO = T * D / 4 / NT;
+  float4 xo[NDO];
+#pragma unroll
+  for (int it = 0; it < NDO; ++it) xo[it] = ld4(dout + 4 * (tid + it * NT));
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     ax[u] = wave_transpose16(tr, ax[u], r, g);
@@ -1189,9 +1194,10 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdPreArgs a) {
     for (int m = 0; m < NYW; ++m) ay[m][u] = wave_transpose16(tr, ay[m][u], r, g);
   }
   __syncthreads();
-  for (int f = tid; f < T * D / 4; f += NT) {
-    const int t = f / (D / 4), c = 4 * (f % (D / 4));
-    const float4 x = ld4(dout + t * D + c);
+#pragma unroll
+  for (int it = 0; it < NDO; ++it) {
+    const int f = tid + it * NT, t = f / (D / 4), c = 4 * (f % (D / 4));
+    const float4 x = xo[it];
     sOT[(c + 0) * LT + t] = x.x;
     sOT[(c + 1) * LT + t] = x.y;
     sOT[(c + 2) * LT + t] = x.z;
