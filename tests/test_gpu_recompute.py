@@ -54,6 +54,21 @@ def test_recompute_equals_stored_bitwise(D):
     compare(got, ora, GATE, names=("o", "h_final") + NAMES + ("dh0",))
 
 
+def test_recompute_xcd_grouped_order_bitwise():
+    """With B*H a multiple of 8 the backward groups whole (batch, head)s per XCD and dispatches
+    their full checkpoint blocks before the single-chunk ones: B2 H4 (8 sequences) at 5 and 8
+    chunks with K = 3 (two single-chunk blocks each) equals the stored form bit for bit."""
+    banner("recompute vs stored, 8 sequences (XCD-grouped block order)")
+    cfg = base_cfg()
+    for L in (320, 512):
+        arrs = mk_inputs(2, L, 4, 128, 26, g=0.1, layout="bhld")
+        h0 = (np.random.default_rng(27).normal(size=(2, 4, 128, 128)) * 0.1).astype(np.float32)
+        ref = _grad(cfg, 128 ** -0.5, arrs, h0, 0)
+        got = _grad(cfg, 128 ** -0.5, arrs, h0, 3)
+        for n in ref:
+            assert torch.equal(got[n], ref[n]), (L, n)
+
+
 def test_recompute_other_dot_modes_and_segments():
     """bf16x3 products, lean diagonal, eps > 0, and L = 4096 as two segments: recompute equals
     stored bit for bit."""
