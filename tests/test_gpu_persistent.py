@@ -44,7 +44,7 @@ def test_persistent_later_rounds_match_oracle(kw):
     nchunks = B * H * (L // 64)
     if ncu >= nchunks:
         pytest.skip(f"{ncu} CUs: {nchunks} chunks fit in one round")
-    late = ncu // (L // 64)                       # first sequence whose chunks run in round 2
+    late = ncu // (L // 64)                       # first sequence whose chunks a workgroup takes second
     seqs = [(late // H, late % H), (0, 1)]
     banner(f"persistent rounds {kw}: {nchunks} chunks on {ncu} CUs, sequences {seqs}")
     arrs, scale = make_inputs_np(B, H, L, D, seed=5)
