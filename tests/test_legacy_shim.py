@@ -64,12 +64,12 @@ def test_memory_estimate_and_recommendation():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("preset", ["KAGGLE_SMALL", "KAGGLE_MEDIUM"])
+@pytest.mark.parametrize("preset", ["KAGGLE_SMALL", "KAGGLE_MEDIUM", "KAGGLE_LARGE"])
 def test_legacy_entry_points_match_oracle(preset):
-    """The preset's own operator (chunk config.bt = 128 / 256 with its wy_eps, as the
+    """The preset's own operator (chunk config.bt = 128 / 256 with its wy_eps and clip, as the
     reference's TPU path runs it) through the legacy entry points, against the float64 oracle
     at that chunk; the forward also against the token recurrence."""
-    config = {"KAGGLE_SMALL": KAGGLE_SMALL, "KAGGLE_MEDIUM": KAGGLE_MEDIUM}[preset]
+    config = {"KAGGLE_SMALL": KAGGLE_SMALL, "KAGGLE_MEDIUM": KAGGLE_MEDIUM, "KAGGLE_LARGE": KAGGLE_LARGE}[preset]
     if not torch.cuda.is_available():
         pytest.skip("no ROCm GPU")
     import sys
@@ -96,7 +96,8 @@ def test_legacy_entry_points_match_oracle(preset):
     o2, hf2 = atomic_ops.gdn2_forward_trainable(*xs, scale, config=config)
     ((o2 * o2).sum() + (hf2 * hf2).sum()).backward()
     ref = grad_ref(q, k, v, w, b, g, scale, None,
-                   OracleCfg(bt=config.bt, score_bs=config.bt, bs2=32, mb=config.mb, wy_eps=config.wy_eps))
+                   OracleCfg(bt=config.bt, score_bs=config.bt, bs2=32, mb=config.mb, wy_eps=config.wy_eps,
+                             clip=config.clip))
     for x, n in zip(xs, ("dq", "dk", "dv", "dw", "db", "dg")):
         assert rel_l2(x.grad, sw(ref[n])) < 2e-3, n
 
