@@ -291,6 +291,36 @@ def test_forward_matches_token_serial(small_cfg):
     assert rel_l2(hip["o"].cpu().transpose(1, 2), ots) < 5e-3
 
 
+@pytest.mark.parametrize("seed", [0, 1])
+def test_directional_derivative_vs_token_serial_fd(seed):
+    """T1 (tests_gdn2/test_t1_finite_diff.py:12-33) on the HIP operator: the derivative of
+    sum(o^2) along a random direction in (q, k, v, b, g), from the kernels' VJP, against a
+    central finite difference (eps 1e-5) of the float64 token recurrence, which shares no
+    formula with the chunked WY form.  D = 64, L = 128."""
+    from oracle import gdn2_oracle as O
+    banner(f"T1 directional derivative, seed {seed}")
+    D, L, H = 64, 128, 2
+    scale = D ** -0.5
+    arrs = mk_inputs(1, L, H, D, 40 + seed, layout="bhld")         # (B,H,L,D): q, k, v, w, b, g
+    hip = hip_grad(base_cfg(), scale, arrs, loss_h=False)
+    rng = np.random.default_rng(50 + seed)
+    idx = {"dq": 0, "dk": 1, "dv": 2, "db": 4, "dg": 5}
+    dirs = {n: torch.from_numpy(rng.normal(size=arrs[0].shape)) for n in idx}
+    dd_hip = sum(float((hip[n].double().cpu() * dirs[n]).sum()) for n in idx)
+
+    def f(theta):
+        xs = [torch.from_numpy(np.asarray(a, np.float64)) for a in arrs]
+        for n, i in idx.items():
+            xs[i] = xs[i] + theta * dirs[n]
+        q, k, v, w, b, g = (x.transpose(1, 2) for x in xs)          # (B,L,H,D)
+        o, _ = O.token_serial_ref(q, k, v, g, b, w, scale)
+        return float((o * o).sum())
+
+    eps = 1e-5
+    fd = (f(eps) - f(-eps)) / (2 * eps)
+    assert abs(dd_hip - fd) / abs(fd) < 5e-3, (dd_hip, fd)
+
+
 def test_causality_dq(small_cfg):
     """tests_gdn2/test_t5_grad_vs_reference.py:41-48: exact invariance of the prefix."""
     from atomic_gdn2 import make_blr_trainable
