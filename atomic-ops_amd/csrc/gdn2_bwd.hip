@@ -293,8 +293,9 @@ __global__ __launch_bounds__(NWW * WAVE) __attribute__((amdgpu_waves_per_eu(2)))
       const int pb = kb & 1;
       const float4 hp = wave_transpose16(tr, f4_to_float4(h[kb]), r, g);
       const float4 hpw = second ? wave_transpose16(tr, sHd[(w * NKB + kb) * WAVE + l], r, g) : hp;
-      const float4 dhc = dhb[pb];
-      const float4 dhk = add4(dhc, ezb[pb]);
+      // this value block's dh_next and EZ, taken before the prefetch below refills their slots
+      const float4 dhc = dhb[pb], ezc = ezb[pb];
+      const float4 dhk = add4(dhc, ezc);
       {
         // two value blocks ahead, across the chunk boundary
         const int kn = kb + 2 < NKB ? kb + 2 : kb + 2 - NKB, cn = kb + 2 < NKB ? c : c + 1;
@@ -330,11 +331,10 @@ __global__ __launch_bounds__(NWW * WAVE) __attribute__((amdgpu_waves_per_eu(2)))
       part = fmaf(dhc.w, hp.w, part);
       if (dterm) {
         // sum_v EZ(pj + 1) Delta(pj), Delta = (h - h_d) / eps (gdn2_kernels.hpp, Cfg::group)
-        const float4 e4 = ezb[pb];
-        part = fmaf(e4.x, (hp.x - hpw.x) * inv_eps, part);
-        part = fmaf(e4.y, (hp.y - hpw.y) * inv_eps, part);
-        part = fmaf(e4.z, (hp.z - hpw.z) * inv_eps, part);
-        part = fmaf(e4.w, (hp.w - hpw.w) * inv_eps, part);
+        part = fmaf(ezc.x, (hp.x - hpw.x) * inv_eps, part);
+        part = fmaf(ezc.y, (hp.y - hpw.y) * inv_eps, part);
+        part = fmaf(ezc.z, (hp.z - hpw.z) * inv_eps, part);
+        part = fmaf(ezc.w, (hp.w - hpw.w) * inv_eps, part);
       }
       if (step) {
         // the forward scan's Kg^T v_new chain (gdn2_scan.hip), the same MFMAs in the same order

@@ -132,6 +132,30 @@ def test_bt256_undamped_matches_oracle(kw):
     compare(hip, oracle_grad(cfg, scale, arrs, h0), GATE, ("o", "h_final") + NAMES + ("dh0",))
 
 
+@pytest.mark.parametrize("eps", [0.02, 1e-3])
+def test_bt256_damped_gate_gradient_per_chunk(eps):
+    """dg chunk by chunk at damped bt = 256: the parts 1 and 2 of a big chunk carry the extra
+    decay term sum_v EZ(j+1) Delta(j) (gdn2_kernels.hpp, Cfg::group), which lands as a constant
+    per column on the chunk's rows after the reverse cumsum.  The aggregate rel-L2 of dg is
+    dominated by the last chunk's large gradient, so a wrong term in an earlier part (an EZ
+    taken from another value block: 3.6e-3 on one chunk, 3.5e-5 in aggregate) shows only per
+    chunk.  fp32 puts every chunk within ~1e-6 of the oracle; the bar is 1e-4."""
+    from atomic_gdn2 import make_blr_trainable
+    from oracle import gdn2_oracle as O
+    banner(f"bt=256 damped dg per chunk, eps={eps}")
+    D = 128
+    cfg = base_cfg(bt=256, bc=128, score_bs=128, bs2=32, mb=8, wy_eps=eps)
+    arrs = mk_inputs(1, 512, 2, D, 77, g=0.05, layout="bhld")          # two 256-token chunks
+    xs = [t.requires_grad_(True) for t in to_dev(arrs)]
+    o, hf = make_blr_trainable(cfg, D ** -0.5, state_ckpt=4)(*xs)
+    dg = torch.autograd.grad((o * o).sum() + (hf * hf).sum(), xs)[5].double().cpu()
+    t = [torch.from_numpy(np.asarray(a, np.float64)) for a in arrs]
+    ref = O.grad_ref(*t, D ** -0.5, None, O.OracleCfg.from_cfg(cfg))["dg"]
+    errs = [rel_l2(dg[:, :, 64 * c:64 * (c + 1)], ref[:, :, 64 * c:64 * (c + 1)]) for c in range(8)]
+    banner(f"bt=256 damped dg per chunk: {['%.1e' % e for e in errs]}")
+    assert max(errs) < 1e-4, errs
+
+
 @pytest.mark.parametrize("which", ["make_cfg", "bt256"])
 def test_damped_big_chunks_bf16_inputs_forward(which):
     """bf16 inputs at the damped bt = 128 of make_cfg() and at a damped bt = 256: the no-grad
