@@ -54,8 +54,9 @@ enum { GDN2_OK = 0, GDN2_ERR_INVALID = 1, GDN2_ERR_UNSUPPORTED = 2, GDN2_ERR_HIP
  *            the reference's segment loop slices and concatenates (pipeline.py:57-64).
  *   state_ckpt  how the residual keeps the state for the backward (no counterpart in the
  *            reference, whose residual keeps the state entering every chunk, pipeline.py:25):
- *            0 = the state entering every chunk; K >= 1 = only every K-th chunk's, the backward
- *            recomputes the others. */
+ *            0 = the state entering every chunk; K >= 1 = only the state entering each
+ *            checkpoint block (blocks of K chunks, see HPRE below), the backward recomputes the
+ *            others. */
 typedef struct gdn2_desc {
   int32_t B, H, L, D;
   int32_t bt, score_bs, bs2, mb;
