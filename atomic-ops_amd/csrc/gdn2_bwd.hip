@@ -1047,7 +1047,9 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
       const float be = ba[e], ke = ka[e], qe = qa[e];
       const float gi = sG[i * LD + dcol];
       const float egc = exp_nonpos(gi), ekg = exp_nonpos(gl - gi);
-      const float mgc = gi < 0.f ? 1.f : 0.f, mkg = (gl - gi) < 0.f ? 1.f : 0.f;
+      // derivative masks 1{x <= 0} of exp(min(x, 0)); the reference's 1{x < 0} (bwd/mega.py:47-48)
+      // drops the terms of rows whose later gates round away against gc (gl - gc == 0 in fp32)
+      const float mgc = gi <= 0.f ? 1.f : 0.f, mkg = (gl - gi) <= 0.f ? 1.f : 0.f;
       const float kbv = (be * ke) * egc;
       const float kg = sanitize(ke * ekg, clip), qg = sanitize(qe * egc, clip);
       const float dqg = qga[e], dkg = kga[e];
@@ -1089,12 +1091,12 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     }
   }
   // last-row decay gradient: sum over all rows of the column (lanes g, then the waves of the
-  // strip in order) + e^gamma sum_v(dh_next h_pre) [gl < 0]
+  // strip in order) + e^gamma sum_v(dh_next h_pre) [gl <= 0]
   part += __shfl_xor(part, 16);
   part += __shfl_xor(part, 32);
   if constexpr (RT_STATIC) {
     // the strip is this wave's alone; row T-1 is element 3 of row tile 3 on the lanes g = 3
-    const float dec = exp_nonpos(gl), mdec = gl < 0.f ? 1.f : 0.f;
+    const float dec = exp_nonpos(gl), mdec = gl <= 0.f ? 1.f : 0.f;
     const float colsum = part + dec * dlast * mdec;
     if (g == 3) dgv[NTW - 1][3] = sanitize(fix3 + colsum, clip) + fix4;
     // B5 (mega.py:53): dg = reverse cumsum over the chunk rows, row order (t, g, e): within a
@@ -1127,7 +1129,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   if (owned(3) && g == 3) {
     float colsum = 0.f;
     for (int w2 = strip; w2 < NW; w2 += St::NS) colsum += sColP[w2 * 16 + r];
-    const float dec = exp_nonpos(gl), mdec = gl < 0.f ? 1.f : 0.f;
+    const float dec = exp_nonpos(gl), mdec = gl <= 0.f ? 1.f : 0.f;
     colsum += dec * dlast * mdec;
     sDgc[(T - 1) * LD + dcol] = sanitize(fix3 + colsum, clip) + fix4;
   }

@@ -44,7 +44,7 @@ import numpy as np
 import torch
 
 __all__ = [
-    "OracleCfg", "sanitize", "exp_nonpos", "exp_clipped", "make_dot", "bf16_round",
+    "OracleCfg", "sanitize", "exp_nonpos", "exp_nonpos_grad", "exp_clipped", "make_dot", "bf16_round",
     "to_chunks", "from_chunks", "chunk_gc", "causal_masks",
     "blr_scores_ref", "btl_scores", "micro_inv", "ladder_inverse", "recompute_wy_ref",
     "inter_chunk_scan_ref", "forward_ref", "forward_ref_blhd", "token_serial_ref",
@@ -89,6 +89,19 @@ def sanitize(x, clip):
 def exp_nonpos(x):
     """exp(min(x,0)) and the 1{x<0} mask  (precision.py:41-44)."""
     return torch.exp(torch.clamp(x, max=0.0)), (x < 0.0).to(x.dtype)
+
+
+def exp_nonpos_grad(x):
+    """exp(min(x,0)) and its derivative mask 1{x<=0}: the gate on the dgc terms of the
+    backward.  The reference's mega backward gates them with 1{x<0} (bwd/mega.py:25-26,32,
+    47-48) although precision.py:42-43 states that this mask must not gate dgc terms
+    (x == 0 on flat gc segments); its B4 drops the masks for that reason (bwd/b4.py:1,66).
+    In fp32, gl - gc rounds to exactly 0 wherever the later gates of the chunk are below half
+    an ulp of gc, and 1{x<0} then drops those rows' terms although the true x is negative.
+    1{x<=0} is torch's derivative of clamp(x, max=0), so it agrees with the autograd gradient
+    of forward_ref; it equals 1 on the log-decay domain (g <= 0) and stays 0 for x > 0.  On
+    the last row x = gl - gc is identically 0 and its term cancels against the last-row sum."""
+    return torch.exp(torch.clamp(x, max=0.0)), (x <= 0.0).to(x.dtype)
 
 
 def exp_clipped(x, lo, hi):
@@ -614,15 +627,15 @@ def backward_mega_ref(q, k, v, w, b, g, A, Aqk, h_pre, v_new, do, dhf, scale, cf
         qc, kc, bc_, wc, vc, gc = map(sl, (q, k, b, w, v, gc_all))
         Ac, Aqc, hp, vn, doc = map(sl, (A, Aqk, h_pre, v_new, do))
         gl = gc[..., T - 1, :]
-        egc, mgc = exp_nonpos(gc)
-        ekg, mkg = exp_nonpos(gl[..., None, :] - gc)
+        egc, mgc = exp_nonpos_grad(gc)
+        ekg, mkg = exp_nonpos_grad(gl[..., None, :] - gc)
         kb = bc_ * kc * egc
         kg = sanitize(kc * ekg, c_)
         qg = sanitize(qc * egc, c_)
         wp = sanitize(dot_hi(Ac, kb), c_)
         dAqk = dot3(doc, tr(vn)) * causal
         dv_new = sanitize(dot3(tr(Aqc), doc) + dot3(kg, dh), c_)
-        dec, mdec = exp_nonpos(gl)
+        dec, mdec = exp_nonpos_grad(gl)
         dh_next = dh
         dh = sanitize(dot3(tr(qg), scale * doc) + dh * dec[..., :, None] - dot3(tr(wp), dv_new), c_)
         wv = wc * vc

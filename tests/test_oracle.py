@@ -231,6 +231,51 @@ def test_analytic_backward_matches_autograd(kw):
     assert rel(bw["dh0"], gr["dh0"]) < 1e-9
 
 
+def flat_gate_inputs(B, H, L, D, seed, tiny=0.0):
+    """rand_inputs with flat gc segments in every 64-token chunk: zero gates on rows 0-4 of
+    columns 0-3 (gc == 0 at the chunk start), gates equal to ``tiny`` on rows 40-63 of
+    columns 4-7 (gl - gc == 0 on the tail when ``tiny`` is 0 or rounds away against gc), and
+    column 8 zero over the whole chunk (gl == 0)."""
+    q, k, v, w, b, g, h0 = rand_inputs(B, H, L, D, seed, gscale=0.3, h0=True)
+    g = g.clone().reshape(B, H, L // 64, 64, D)
+    g[..., 0:5, 0:4] = 0.0
+    g[..., 40:64, 4:8] = -tiny
+    g[..., :, 8] = 0.0
+    return q, k, v, w, b, g.reshape(B, H, L, D), h0
+
+
+def test_analytic_backward_flat_gate_segments(monkeypatch):
+    """Where x = gc, gl - gc or gl is exactly 0, the derivative of exp(min(x, 0)) that
+    autograd takes is 1 (torch's clamp gradient at the bound), and the analytic backward's
+    masks 1{x <= 0} agree with it.  The reference backward's 1{x < 0} (bwd/mega.py:47-48)
+    drops those terms; planted here, the dg check fails.  In fp32 the tail gates of 1e-9
+    round away against gc and produce the same zeros: the fp32 analytic backward still
+    meets the float64 autograd gradient on every chunk."""
+    cfg = O.OracleCfg()
+    ch = lambda t: O.to_chunks(t, 64)
+
+    def mega(args, h0, dt):
+        a = [x.to(dt) for x in args]
+        kf = O.kernel_forward_ref(*a, 0.25, h0.to(dt), cfg)
+        return O.backward_mega_ref(*map(ch, a), kf["A"], kf["Aqk"], kf["h_pre"], kf["v_new"],
+                                   ch(2 * kf["o"]), 2 * kf["h_final"], 0.25, cfg)
+
+    *args, h0 = flat_gate_inputs(1, 2, 128, 16, 21)
+    gr = O.grad_ref(*args, 0.25, h0, cfg)
+    bw = mega(args, h0, torch.float64)
+    for n in ("dq", "dk", "dv", "dw", "db", "dg"):
+        assert rel(O.from_chunks(bw[n]), gr[n]) < 1e-9, n
+    monkeypatch.setattr(O, "exp_nonpos_grad", O.exp_nonpos)          # the strict 1{x < 0}
+    assert rel(O.from_chunks(mega(args, h0, torch.float64)["dg"]), gr["dg"]) > 1e-2
+    monkeypatch.undo()
+
+    *args, h0 = flat_gate_inputs(1, 2, 256, 16, 22, tiny=1e-9)
+    gr = O.grad_ref(*args, 0.25, h0, cfg)
+    dg = O.from_chunks(mega(args, h0, torch.float32)["dg"]).double()
+    for c in range(4):
+        assert rel(dg[..., 64 * c:64 * c + 64, :], gr["dg"][..., 64 * c:64 * c + 64, :]) < 1e-5, c
+
+
 @pytest.mark.parametrize("kw", [dict(), dict(bs2=16), dict(score_bs=32, bs2=16), dict(bs2=64)])
 def test_b4_closed_form_vs_autograd(kw):
     cfg = O.OracleCfg(**kw)
