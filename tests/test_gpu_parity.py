@@ -289,14 +289,16 @@ def test_grad_other_domain_seeds(small_cfg, name, seed, g, k, b, dom):
     compare(hip, kernel_oracle(cfg, 1 / 8.0, arrs), 1e-4, NAMES)
 
 
-@pytest.mark.parametrize("case", ["absorbed_tail", "planted_flat"])
+@pytest.mark.parametrize("case", ["absorbed_tail", "planted_flat", "planted_flat_bt128", "planted_flat_bt256"])
 def test_dg_on_flat_gate_segments(case):
     """dg where x = gc, gl - gc or gl is exactly 0 in fp32.  absorbed_tail: sequence (0, 1)
     of this seed has chunks whose last gates round away against gc, so gl - gc == 0 on a row
     whose true x is negative (with the strict mask 1{x < 0} of bwd/mega.py:47-48 its dg chunk
-    missed the float64 gradient by 1.5e-3).  planted_flat: zero gates at the chunk start,
-    tails of 1e-9 and of exact zeros, and a column zero over whole chunks.  Every chunk of
-    every gradient within 1e-4 of the float64 autograd oracle."""
+    missed the float64 gradient by 1.5e-3).  planted_flat: zero gates at the start of every
+    64 tokens, tails of 1e-9 and of exact zeros, and a column zero over whole chunks; also at
+    make_cfg()'s damped bt = 128 and at a damped bt = 256 (the kernels' 64-token parts).
+    Every chunk of every gradient within 1e-4 of the float64 autograd oracle."""
+    from atomic_gdn2 import make_cfg
     if case == "absorbed_tail":
         arrs = [np.ascontiguousarray(a[0:1, 1:2]) for a in mk_inputs(3, 2048, 6, 128, 903, g=0.05, layout="bhld")]
     else:
@@ -308,7 +310,8 @@ def test_dg_on_flat_gate_segments(case):
         g[..., :, 8] = 0.0
         arrs[5] = g.reshape(1, 2, 512, 128)
     banner(f"flat gate segments {case} {arrs[0].shape}")
-    cfg = base_cfg()
+    cfg = {"planted_flat_bt128": make_cfg(),
+           "planted_flat_bt256": base_cfg(bt=256, bc=128, score_bs=128, bs2=32, mb=8, wy_eps=1e-3)}.get(case, base_cfg())
     hip = hip_grad(cfg, 128 ** -0.5, arrs)
     errs = compare(hip, oracle_grad(cfg, 128 ** -0.5, arrs), 1e-4)
     banner(f"flat gate segments {case}: max rel-L2 {max(errs.values()):.2e}")
