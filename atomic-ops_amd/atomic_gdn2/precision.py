@@ -1,7 +1,11 @@
 """Host-side numerics helpers (reference: atomic_gdn2/precision.py:41-52).
 
 The matmul dot modes themselves (``highest`` / ``bf16x3`` / ``default``) live in the HIP
-kernels; these torch helpers serve the host-side finishing step (``_fin``) and callers.
+kernels; these torch helpers serve the host-side finishing step (``_fin``, ``sanitize``) and
+callers that import the reference's precision module (``exp_nonpos``, ``exp_clipped``: the
+kernels compute the same functions on the device, ``gdn2_common.hpp``).  The backward kernels
+gate the derivative of exp(min(x, 0)) with 1{x <= 0}, the derivative autograd takes, not with
+the mask returned here.
 """
 import torch
 
