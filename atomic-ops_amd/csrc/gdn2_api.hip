@@ -21,6 +21,8 @@ size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
 
+gdn2::Cfg make_cfg(const gdn2_desc* d);
+
 // Validation mirrors BLRConfig.__post_init__ (atomic_gdn2/config.py:62-75) plus this
 // build's supported geometry.
 int validate(const gdn2_desc* d) {
@@ -46,6 +48,11 @@ int validate(const gdn2_desc* d) {
   if (d->bs2 < 16) return fail(GDN2_ERR_UNSUPPORTED, "this build supports bs2 >= 16");
   if (d->seq_ld != 0 && d->seq_ld < d->L) return fail(GDN2_ERR_INVALID, "seq_ld must be 0 or >= L");
   if (d->state_ckpt < 0) return fail(GDN2_ERR_INVALID, "state_ckpt must be >= 0");
+  // the score pieces partition the lower triangle, so every 16 x 16 tile on or below the
+  // diagonal has one (the kernels index the piece list with Cfg::tile_piece)
+  const gdn2::Cfg c = make_cfg(d);
+  for (int t = 0; t < 16; ++t)
+    if (t / 4 >= t % 4 && c.tile_piece[t] < 0) return fail(GDN2_ERR_UNSUPPORTED, "score tile without a piece");
   return GDN2_OK;
 }
 
@@ -110,6 +117,15 @@ gdn2::Cfg make_cfg(const gdn2_desc* d) {
   // geometry that lie inside a half are the 64 geometry's with the outer block capped at 64
   // (the pieces crossing the halves are carried by the state, see Cfg::group)
   make_pieces(gdn2::T, d->score_bs < gdn2::T ? d->score_bs : gdn2::T, d->bs2, &c.pieces);
+  for (int t = 0; t < 16; ++t) {
+    const int ti = t / 4, tj = t % 4;
+    c.tile_piece[t] = -1;
+    for (int pi = 0; pi < c.pieces.n && ti >= tj; ++pi) {
+      const gdn2::Piece& p = c.pieces.p[pi];
+      if (16 * ti >= p.row0 && 16 * ti < p.row0 + p.P && 16 * tj >= p.col0 && 16 * tj < p.col0 + p.P)
+        c.tile_piece[t] = pi;
+    }
+  }
   return c;
 }
 

@@ -140,6 +140,27 @@ __device__ __forceinline__ void mfma_bf16x3_k32(f4& acc, const s8& ah, const s8&
       : "+v"(acc)
       : "v"(ah), "v"(al), "v"(bh), "v"(bl));
 }
+// The bf16x3 passes with the cross terms in the other order (hi*hi, lo*hi, hi*lo): with the
+// operands' roles exchanged this issues the products of mfma_bf16x3(acc, bh, bl, ah, al) in
+// that call's order, so the two accumulate bit-identically (one is the other's transpose).
+__device__ __forceinline__ void mfma_bf16x3_tr(f4& acc, const s4& ah, const s4& al, const s4& bh, const s4& bl) {
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_mfma_f32_16x16x16_bf16 %0, %1, %3, %0\n\t"
+      "v_mfma_f32_16x16x16_bf16 %0, %2, %3, %0\n\t"
+      "v_mfma_f32_16x16x16_bf16 %0, %1, %4, %0"
+      : "+v"(acc)
+      : "v"(ah), "v"(al), "v"(bh), "v"(bl));
+}
+__device__ __forceinline__ void mfma_bf16x3_k32_tr(f4& acc, const s8& ah, const s8& al, const s8& bh, const s8& bl) {
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_mfma_f32_16x16x32_bf16 %0, %1, %3, %0\n\t"
+      "v_mfma_f32_16x16x32_bf16 %0, %2, %3, %0\n\t"
+      "v_mfma_f32_16x16x32_bf16 %0, %1, %4, %0"
+      : "+v"(acc)
+      : "v"(ah), "v"(al), "v"(bh), "v"(bl));
+}
 __device__ __forceinline__ void drain(f4& a) {
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(a));
 }
@@ -222,6 +243,35 @@ __device__ __forceinline__ void mma32(f4& acc, const float4& a0, const float4& b
     mfma_bf16x3_k32(acc, cat8(a0h, a1h), cat8(a0l, a1l), cat8(b0h, b1h), cat8(b0l, b1l));
   } else {
     mfma_bf16x1_k32(acc, cat8(round4(a0), round4(a1)), cat8(round4(b0), round4(b1)));
+  }
+}
+// The transposed product: mma16_tr<MODE>(acc, a, b) takes a as the A operand and b as the B
+// operand and issues the products of mma16<MODE>(acc', b, a) in that call's order, so acc ends
+// up as the transpose of acc', bit for bit (each MFMA's sum is symmetric in its operands).
+// A producer that needs a tile in the other orientation swaps the operands instead of
+// transposing the result.
+template <int MODE>
+__device__ __forceinline__ void mma16_tr(f4& acc, const float4& a, const float4& b) {
+  if constexpr (MODE == DOT_BF16X3) {
+    s4 ah, al, bh, bl;
+    split4(a, ah, al);
+    split4(b, bh, bl);
+    mfma_bf16x3_tr(acc, ah, al, bh, bl);
+  } else {
+    mma16<MODE>(acc, a, b);
+  }
+}
+template <int MODE>
+__device__ __forceinline__ void mma32_tr(f4& acc, const float4& a0, const float4& b0, const float4& a1, const float4& b1) {
+  if constexpr (MODE == DOT_BF16X3) {
+    s4 a0h, a0l, a1h, a1l, b0h, b0l, b1h, b1l;
+    split4(a0, a0h, a0l);
+    split4(a1, a1h, a1l);
+    split4(b0, b0h, b0l);
+    split4(b1, b1h, b1l);
+    mfma_bf16x3_k32_tr(acc, cat8(a0h, a1h), cat8(a0l, a1l), cat8(b0h, b1h), cat8(b0l, b1l));
+  } else {
+    mma32<MODE>(acc, a0, b0, a1, b1);
   }
 }
 // acc += sum over the k blocks kb in [k0, K1) of the lane operands a(kb), b(kb): fp32 one block
@@ -470,5 +520,52 @@ __device__ __forceinline__ void chunk_cumsum(const TIn* __restrict__ g, float* s
   for (int i = 0; i < RUN; ++i) st4(sG + (s * RUN + i) * LD + d, add4(off, x[i]));
   __syncthreads();
 }
+
+// chunk_cumsum<D, ., NVIRT> for the columns [c0, c0 + 4 NQP) only, run by NREAL threads, with the
+// result in fragment layout (T x 4 NQP).  Every virtual thread (s, cq) of chunk_cumsum that owns
+// one of those columns (float4 column cq, rows s RUN .. s RUN + RUN - 1) is run by one real thread
+// (the first NSEG NQP threads, several virtual threads each if there are fewer real ones), adding
+// in exactly its order, so gc is bit-identical to chunk_cumsum's.  load() issues the g loads
+// (into registers); run() needs NSEG x NQP float4 of LDS for the run totals, is called by every
+// thread and ends with a barrier.
+template <int D, int NVIRT, int NREAL, int NQP>
+struct CumsumPass {
+  static constexpr int NQ = D / 4, NSEG = NVIRT / NQ, RUN = T / NSEG, NACT = NSEG * NQP;
+  static constexpr int NV = (NACT + NREAL - 1) / NREAL;
+  static_assert(NVIRT % NQ == 0 && T % NSEG == 0 && (NACT <= NREAL || NACT % NREAL == 0), "cumsum split");
+  float4 x[NV][RUN];
+  __device__ __forceinline__ bool active(int m) const { return NACT >= NREAL || (int)threadIdx.x < NACT; }
+  __device__ __forceinline__ int seg(int m) const { return (threadIdx.x + NREAL * m) / NQP; }
+  __device__ __forceinline__ int col(int m) const { return (threadIdx.x + NREAL * m) % NQP; }
+  template <typename TIn>
+  __device__ __forceinline__ void load(const TIn* __restrict__ g, int c0) {
+#pragma unroll
+    for (int m = 0; m < NV; ++m)
+      if (active(m)) {
+#pragma unroll
+        for (int i = 0; i < RUN; ++i) x[m][i] = in_ld4(g + (seg(m) * RUN + i) * D + c0 + 4 * col(m));
+      }
+  }
+  __device__ __forceinline__ void run(float* sGf, float4* sTot) {
+#pragma unroll
+    for (int m = 0; m < NV; ++m)
+      if (active(m)) {
+#pragma unroll
+        for (int i = 1; i < RUN; ++i) x[m][i] = add4(x[m][i - 1], x[m][i]);
+        sTot[seg(m) * NQP + col(m)] = x[m][RUN - 1];
+      }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < NV; ++m)
+      if (active(m)) {
+        const int s = seg(m), cq = col(m);
+        float4 off = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int s2 = 0; s2 < s; ++s2) off = add4(off, sTot[s2 * NQP + cq]);
+#pragma unroll
+        for (int i = 0; i < RUN; ++i) st4(sGf + frag_off(s * RUN + i, 4 * cq, 4 * NQP), add4(off, x[m][i]));
+      }
+    __syncthreads();
+  }
+};
 
 }  // namespace gdn2

@@ -1,12 +1,13 @@
 // Forward chunk-parallel kernels of the GDN-2 operator on gfx950.
 //
-//   wy_fwd_kernel   one workgroup (8 waves) per chunk: in-chunk cumulative decay gc, gated
-//                   Kg / Qg, gated scores Aqk / Akk (two-level block-local rescaling, BTL or
-//                   lean diagonal) on MFMA with the rescaling legs applied to the operands as
-//                   they are loaded, unit-lower-triangular inverse A = (I + (1-eps) Akk)^-1 by
-//                   leaf forward substitution in registers + block doubling (MFMA for blocks
-//                   of 16 and up), then Wp = A (b k e^gc) and U = A (w v) on MFMA.
-//                   Semantics: fwd/scores.py:42-87, fwd/solve.py:9-48, fwd/cd_slim.py:14-21.
+//   wy_fwd_kernel   one workgroup (4 waves, three per CU) per chunk: in-chunk cumulative decay
+//                   gc, gated Kg / Qg, gated scores Aqk / Akk (two-level block-local
+//                   rescaling, BTL or lean diagonal) on MFMA with the rescaling legs applied to
+//                   the LDS-staged operands as they are read, in passes of 32 channels;
+//                   unit-lower-triangular inverse A = (I + (1-eps) Akk)^-1 by leaf forward
+//                   substitution in registers + block doubling (MFMA for blocks of 16 and up),
+//                   then Wp = A (b k e^gc) and U = A (w v) on MFMA.
+//                   Semantics: fwd/scores.py:16-97, fwd/solve.py:9-59, fwd/cd_slim.py:14-21.
 //                   The raw inputs are fp32 or bfloat16 (template TIn), widened to fp32 on load.
 //   out_fwd_kernel  one workgroup per chunk after the state scan, when the backward needs
 //                   h_pre and v_new anyway (training):
@@ -20,81 +21,85 @@
 namespace gdn2 {
 
 // ------------------------------------------------------------------------------------
-// WY build
+// WY build: one workgroup of four waves per chunk, 40 KB of LDS and at most 168 VGPRs, so that
+// three workgroups share a CU (768 chunks at config 2 = 3 per CU, all resident at once) and their
+// load / store bursts overlap each other's score, inverse and Wp / U phases.  The D channels
+// are taken in passes of DC = 32: each pass forms
+// gc for its channels, the gated fragments Kg / Qg / Kg^T and X = b k e^gc in registers, and
+// stages gc, q, k and b k in LDS in fragment layout, from which every wave computes its score
+// tiles over the pass's k blocks (the accumulators carry across passes, so each tile's chain is
+// the one-pass chain: k blocks in ascending order).
 // ------------------------------------------------------------------------------------
 template <int D>
 struct WyLayout {
-  static constexpr int LD = D + 4, LT = T + 4;
-  // gc | b*k (later X = b*k*e^gc) | w*v | S (scores, then merge temp, then transposes) | Akk | inverse
-  static constexpr int OFF_G = 0, OFF_BK = T * LD, OFF_Y = 2 * T * LD;
-  static constexpr int OFF_S = 3 * T * LD, OFF_K = OFF_S + T * LT, OFF_I = OFF_K + T * LT;
-  static constexpr int TOTAL = OFF_I + T * LT;
-  static_assert(T * LT >= 8 * 16 * 20, "transpose scratch must fit in S");
+  static constexpr int DC = 32, NPASS = D / DC, NKBP = DC / 16, LT = T + 4;
+  static constexpr int TILE = T * DC;
+  // a pass: gc | q | k | b k, each T x DC in fragment layout; the cumsum's run totals use the
+  // q slot before the elementwise step fills it
+  static constexpr int OFF_G = 0, OFF_Q = TILE, OFF_K = 2 * TILE, OFF_BK = 3 * TILE;
+  // after the scores: (1 - eps) Akk and the inverse (row-major, ld LT); after the inverse the
+  // Akk slot takes X^T, then Y^T, four 16-channel strips at a time (fragment layout, 64 x T)
+  static constexpr int OFF_S = 0, OFF_I = T * LT, OFF_X = 0;
+  // per-wave 16 x 16 transpose tiles; during the inverse, the scalar doubling temp
+  static constexpr int OFF_TR = (4 * TILE > 2 * T * LT) ? 4 * TILE : 2 * T * LT;
+  static constexpr int TOTAL = OFF_TR + 4 * 16 * TRP;
+  static_assert(D % DC == 0 && D % 64 == 0 || D == 64, "whole passes");
+  static_assert(64 * T <= T * LT, "a strip group of X^T fits in the Akk slot");
 };
 
-// One 16x16 tile position of a score piece, both matrices at once (they share the legs and
-// the B operand): accq += sum_d (q[i][d] ra) (k[j][d] cb), acck += sum_d (bk[i][d] ra) (k[j][d] cb),
-// where i (j) is the A row (B column) of the calling lane.  Legs (fwd/scores.py:42-75):
+// Score tile (ti, tj) of piece pc over the k blocks of one pass, both matrices at once (they share
+// the legs and the k operand), from the pass's staged gc, q, k, b k (fragment layout, T x DC):
+//   accq += sum_d (q[i][d] ra) (k[j][d] cb),  acck += sum_d (bk[i][d] ra) (k[j][d] cb)
+// with i = 16 ti + (lane's row), j = 16 tj + (lane's row).  Legs (fwd/scores.py:16-22, 39-65):
 //   KIND 0 (off-diagonal, anchor a): ra = e^{min(gc_i - gc_a, 0)}, cb = e^{min(gc_a - gc_j, 0)}
 //   KIND 1 (BTL diagonal block [s0, s1)): r = gc_s0, half = (gc_s0 - gc_{s1-1}) / 2,
 //          ra = e^{(gc_i - r) + half}, cb = e^{(r - gc_j) - half}
-template <int D, int LD, int DOT, int KIND, typename TIn>
-__device__ __forceinline__ void score_pair(f4& accq, f4& acck, const TIn* __restrict__ q, const float* sBK,
-                                           const TIn* __restrict__ kk, const float* sG, const Piece& pc, int i,
-                                           int j) {
-  const int g = lane_id() >> 4;
-  const float* gi = sG + i * LD;
-  const float* gj = sG + j * LD;
-  const float* ga = sG + (KIND == 0 ? pc.anchor : pc.s0) * LD;
-  const float* gz = sG + (KIND == 0 ? pc.anchor : pc.s1 - 1) * LD;
-  const TIn* qi = q + i * D;
-  const float* bi = sBK + i * LD;
-  const TIn* kj = kk + j * D;
-  // the raw q / k operands of the whole chain are loaded first (one memory round trip)
-  float4 qa[D / 16], ka[D / 16];
-#pragma unroll
-  for (int kb = 0; kb < D / 16; ++kb) {
-    qa[kb] = in_ld4(qi + 16 * kb + 4 * g);
-    ka[kb] = in_ld4(kj + 16 * kb + 4 * g);
-  }
-  // the operands of k block kb with the legs applied: q ra, (b k) ra, k cb
-  auto operands = [&](int kb, float4& aq, float4& ak, float4& bv) __attribute__((always_inline)) {
-    const int d = 16 * kb + 4 * g;
-    const float4 vi = ld4(gi + d), vj = ld4(gj + d), va = ld4(ga + d);
+// The k operand is the A operand (mma16_tr), so the accumulators hold Aqk / Akk tile (ti, tj)
+// in the operand layout: lane (r, g) has row 16 ti + r, columns 16 tj + 4 g .. + 3, which is
+// block (ti, tj) of FRAG(Aqk) and a float4 of a row-major tile.
+template <int DC, int DOT, int KIND>
+__device__ __forceinline__ void score_tile_pass(f4& accq, f4& acck, const float* sG, const float* sQ, const float* sKs,
+                                                const float* sBK, const Piece& pc, int ti, int tj) {
+  constexpr int NKBP = DC / 16;
+  const int l = lane_id(), g = l >> 4;
+  const int ra_row = KIND == 0 ? pc.anchor : pc.s0, rz_row = KIND == 0 ? pc.anchor : pc.s1 - 1;
+  auto operands = [&](int kb, float4& bv, float4& aq, float4& ak) __attribute__((always_inline)) {
+    const int oi = frag_blk(ti, kb, DC) + 4 * l, oj = frag_blk(tj, kb, DC) + 4 * l;
+    const float4 vi = ld4(sG + oi), vj = ld4(sG + oj), va = ld4(sG + frag_off(ra_row, 16 * kb + 4 * g, DC));
     float4 ra, cb;
     if constexpr (KIND == 0) {
-      ra = make_float4(fast_exp(min0(vi.x - va.x)), fast_exp(min0(vi.y - va.y)),
-                       fast_exp(min0(vi.z - va.z)), fast_exp(min0(vi.w - va.w)));
-      cb = make_float4(fast_exp(min0(va.x - vj.x)), fast_exp(min0(va.y - vj.y)),
-                       fast_exp(min0(va.z - vj.z)), fast_exp(min0(va.w - vj.w)));
+      ra = make_float4(fast_exp(min0(vi.x - va.x)), fast_exp(min0(vi.y - va.y)), fast_exp(min0(vi.z - va.z)),
+                       fast_exp(min0(vi.w - va.w)));
+      cb = make_float4(fast_exp(min0(va.x - vj.x)), fast_exp(min0(va.y - vj.y)), fast_exp(min0(va.z - vj.z)),
+                       fast_exp(min0(va.w - vj.w)));
     } else {
-      const float4 h = scale4(sub4(va, ld4(gz + d)), 0.5f);
+      const float4 h = scale4(sub4(va, ld4(sG + frag_off(rz_row, 16 * kb + 4 * g, DC))), 0.5f);
       ra = make_float4(fast_exp((vi.x - va.x) + h.x), fast_exp((vi.y - va.y) + h.y), fast_exp((vi.z - va.z) + h.z),
                        fast_exp((vi.w - va.w) + h.w));
       cb = make_float4(fast_exp((va.x - vj.x) - h.x), fast_exp((va.y - vj.y) - h.y), fast_exp((va.z - vj.z) - h.z),
                        fast_exp((va.w - vj.w) - h.w));
     }
-    bv = mul4(ka[kb], cb);
-    aq = mul4(qa[kb], ra);
-    ak = mul4(ld4(bi + d), ra);
+    bv = mul4(ld4(sKs + oj), cb);
+    aq = mul4(ld4(sQ + oi), ra);
+    ak = mul4(ld4(sBK + oi), ra);
   };
   if constexpr (DOT == DOT_HIGHEST) {
 #pragma unroll
-    for (int kb = 0; kb < D / 16; ++kb) {
-      float4 aq, ak, bv;
-      operands(kb, aq, ak, bv);
-      mma16<DOT>(accq, aq, bv);
-      mma16<DOT>(acck, ak, bv);
+    for (int kb = 0; kb < NKBP; ++kb) {
+      float4 bv, aq, ak;
+      operands(kb, bv, aq, ak);
+      mma16_tr<DOT>(accq, bv, aq);
+      mma16_tr<DOT>(acck, bv, ak);
     }
   } else {
-    // bf16 modes: two k blocks per 32-deep MFMA
+    // bf16 modes: two k blocks per 32-deep MFMA (pairs never straddle a pass: DC / 16 is even)
 #pragma unroll
-    for (int kb = 0; kb < D / 16; kb += 2) {
-      float4 aq0, ak0, bv0, aq1, ak1, bv1;
-      operands(kb, aq0, ak0, bv0);
-      operands(kb + 1, aq1, ak1, bv1);
-      mma32<DOT>(accq, aq0, bv0, aq1, bv1);
-      mma32<DOT>(acck, ak0, bv0, ak1, bv1);
+    for (int kb = 0; kb < NKBP; kb += 2) {
+      float4 bv0, aq0, ak0, bv1, aq1, ak1;
+      operands(kb, bv0, aq0, ak0);
+      operands(kb + 1, bv1, aq1, ak1);
+      mma32_tr<DOT>(accq, bv0, aq0, bv1, aq1);
+      mma32_tr<DOT>(acck, bv0, ak0, bv1, ak1);
     }
   }
   drain(accq, acck);
@@ -119,10 +124,11 @@ __device__ __forceinline__ void leaf_solve(const float* sSe, float* sI, int tid)
 }
 
 // One doubling level with blocks of 2 BB, BB < 16, as scalar dot products in two passes:
-// M = S21 X11 into sM, then X21 = -X22 M.  Every dot runs over the whole block width: X11 is
-// zero above its diagonal and X22 above its diagonal (the solve writes only the lower part of
-// sI, zeroed beforehand), so the added terms are exact zeros and the sums are those of the
-// triangular ranges; with compile-time bounds the operand reads are issued together.
+// M = S21 X11 into sM (BB x BB per block m, packed), then X21 = -X22 M.  Every dot runs over the
+// whole block width: X11 is zero above its diagonal and X22 above its diagonal (the solve writes
+// only the lower part of sI, zeroed beforehand), so the added terms are exact zeros and the sums
+// are those of the triangular ranges; with compile-time bounds the operand reads are issued
+// together.
 template <int LT, int NT, int BB>
 __device__ __forceinline__ void doubling_level_scalar(int smode, const float* sK, float* sI, float* sM, int tid) {
   constexpr int NM = T / (2 * BB), PER = BB * BB;
@@ -130,18 +136,18 @@ __device__ __forceinline__ void doubling_level_scalar(int smode, const float* sK
     const int m = e / PER, i = (e % PER) / BB, j = e % BB, i0 = m * 2 * BB;
     const float* srow = sK + (i0 + BB + i) * LT + i0;
     const float* tcol = sI + i0 * LT + i0 + j;
-    sM[(i0 + BB + i) * LT + i0 + j] =
-        dot_mode_scalar(smode, 0, BB, [&](int kk) { return srow[kk]; }, [&](int kk) { return tcol[kk * LT]; });
+    sM[e] = dot_mode_scalar(smode, 0, BB, [&](int kk) { return srow[kk]; }, [&](int kk) { return tcol[kk * LT]; });
   }
   __syncthreads();
   for (int e = tid; e < NM * PER; e += NT) {
     const int m = e / PER, i = (e % PER) / BB, j = e % BB, i0 = m * 2 * BB;
     const float* brow = sI + (i0 + BB + i) * LT + i0 + BB;
-    const float* mcol = sM + (i0 + BB) * LT + i0 + j;
+    const float* mcol = sM + m * PER + j;
     sI[(i0 + BB + i) * LT + i0 + j] =
-        -dot_mode_scalar(smode, 0, BB, [&](int kk) { return brow[kk]; }, [&](int kk) { return mcol[kk * LT]; });
+        -dot_mode_scalar(smode, 0, BB, [&](int kk) { return brow[kk]; }, [&](int kk) { return mcol[kk * BB]; });
   }
 }
+constexpr int WY_SM_FLOATS = 256;   // the largest scalar level's temp: T / 16 blocks of 8 x 8
 
 // One doubling level (blocks of 2 BB, BB = 16 or 32) on MFMA: wave w takes block m = w / NTL
 // and column strip tj = w % NTL (NTL = BB / 16) and computes the strip of M = S21 X11 (tiles
@@ -187,12 +193,12 @@ __device__ __forceinline__ void doubling_level_mfma(const float* sK, float* sI, 
 }
 
 // The WY inverse A = (I + Se)^-1 (fwd/solve.py:9-59) of Se = (1-eps) Akk, strictly lower in
-// sK, into sI (zero on entry): leaf inverses by forward substitution, block doubling with sM as
-// the temp (T x LT), then A = san(A) in place and, if A_out is given, row-major to A_out.
-// Starts with the leaf solves and ends with a barrier.
+// sK, into sI (zero on entry): leaf inverses by forward substitution, block doubling with sM
+// (WY_SM_FLOATS) as the scalar levels' temp, then A = san(A) in place and, if A_out is given,
+// row-major to A_out.  Starts with the leaf solves and ends with a barrier.
 // `during_leaves` runs in every thread before the barrier that ends the leaf solves (one wave
 // solves; the others are otherwise idle there).
-template <int LT, int NT, int NW, class F>
+template <int LT, int NT, class F>
 __device__ __forceinline__ void wy_inverse(const Cfg& cf, const float* sK, float* sI, float* sM, float* A_out,
                                            int tid, int wv, int r, int g, F&& during_leaves) {
   const int smode = cf.solve_mode;
@@ -217,12 +223,11 @@ __device__ __forceinline__ void wy_inverse(const Cfg& cf, const float* sK, float
   during_leaves();
   __syncthreads();
 
-  // 5b. block doubling X <- [[X11, 0], [-X22 (S21 X11), X22]] (solve.py:30-43), products in the
-  //     solve dot mode: scalar below blocks of 16 (two passes), on MFMA from 16 up (one pass:
-  //     each column strip of a block computed by one wave, which keeps M = S21 X11 to itself
-  //     between the two products).
+  // block doubling X <- [[X11, 0], [-X22 (S21 X11), X22]] (solve.py:30-43), products in the
+  // solve dot mode: scalar below blocks of 16 (two passes), on MFMA from 16 up (one pass: each
+  // column strip of a block computed by one wave, which keeps M = S21 X11 to itself between the
+  // two products).
   for (int bb = cf.mb; bb < T; bb *= 2) {
-    const int nm = T / (2 * bb);
     if (bb < 16) {
       switch (bb) {
         case 1: doubling_level_scalar<LT, NT, 1>(smode, sK, sI, sM, tid); break;
@@ -239,7 +244,7 @@ __device__ __forceinline__ void wy_inverse(const Cfg& cf, const float* sK, float
     }
     __syncthreads();
   }
-  // 5c. A = san(inverse)
+  // A = san(inverse)
   for (int f = tid; f < T * T / 4; f += NT) {
     const int i = f / (T / 4), j = 4 * (f % (T / 4));
     const float4 x = san4(ld4(sI + i * LT + j), cf.clip);
@@ -249,17 +254,26 @@ __device__ __forceinline__ void wy_inverse(const Cfg& cf, const float* sK, float
   __syncthreads();
 }
 
-template <int D, int DOT, typename TIn>
-__global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
+// Lower-triangle score tile position t (0..9) -> (ti, tj), rows in order: wave w takes t = w,
+// w + 4, w + 8, which gives the four waves 3, 3, 2, 2 tiles.
+constexpr int WY_NTL = T / 16 * (T / 16 + 1) / 2;
+__device__ __forceinline__ int tri_row(int t) { return t >= 6 ? 3 : t >= 3 ? 2 : t >= 1 ? 1 : 0; }
+
+// LEAN: the diagonal pieces exactly (fwd/scores.py:31-36), per element by the workgroup's threads.
+template <int D, int DOT, bool LEAN, typename TIn>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void wy_fwd_kernel(WyFwdArgs a) {
   using Lay = WyLayout<D>;
-  constexpr int LD = Lay::LD, LT = Lay::LT, NT = 512, NW = NT / WAVE, NKB = D / 16;
+  constexpr int NT = 256, DC = Lay::DC, NPASS = Lay::NPASS, NKBP = Lay::NKBP, LT = Lay::LT, NKB = D / 16;
+  constexpr int NSLOT = (WY_NTL + 3) / 4;
   __shared__ __attribute__((aligned(16))) float smem[Lay::TOTAL];
   float* sG = smem + Lay::OFF_G;
+  float* sQ = smem + Lay::OFF_Q;
+  float* sKs = smem + Lay::OFF_K;
   float* sBK = smem + Lay::OFF_BK;
-  float* sY = smem + Lay::OFF_Y;
-  float* sS = smem + Lay::OFF_S;
-  float* sK = smem + Lay::OFF_K;
+  float* sK = smem + Lay::OFF_S;
   float* sI = smem + Lay::OFF_I;
+  float* sX = smem + Lay::OFF_X;
+  float* sM = smem + Lay::OFF_TR;
   const Cfg& cf = a.cfg;
   const float clip = cf.clip;
   const int chunk = blockIdx.x;
@@ -270,235 +284,243 @@ __global__ __launch_bounds__(512) void wy_fwd_kernel(WyFwdArgs a) {
   const TIn* __restrict__ b = static_cast<const TIn*>(a.b) + tio;
   const TIn* __restrict__ w = static_cast<const TIn*>(a.w) + tio;
   const TIn* __restrict__ v = static_cast<const TIn*>(a.v) + tio;
+  const TIn* __restrict__ gg = static_cast<const TIn*>(a.g) + tio;
   const int tid = threadIdx.x, wv = wave_id(), l = lane_id(), r = l & 15, g = l >> 4;
+  float* tr = smem + Lay::OFF_TR + wv * 16 * TRP;
+  // elementwise steps: wave wv owns token tile wv, lane (r, g) row 16 wv + r, columns 16 kb + 4 g
+  const int row = 16 * wv + r;
 
-  // row-fragment items of this thread (item f is lane f%64 of 16x16 block f/64, so fragment
-  // stores are contiguous); all raw inputs are loaded up front, before the cumsum's g
-  constexpr int NIT = T * D / 4 / NT;
-  float4 xk[NIT], xb[NIT], xq[NIT];
+  // the pieces of this wave's score tiles t = wv + 4 s (scalar reads, before any memory traffic)
+  Piece pcs[NSLOT];
 #pragma unroll
-  for (int it = 0; it < NIT; ++it) {
-    const int f = tid + it * NT, blk = f >> 6, ln = f & 63;
-    const int o = (16 * (blk / NKB) + (ln & 15)) * D + 16 * (blk % NKB) + 4 * (ln >> 4);
-    xk[it] = in_ld4(k + o);
-    xb[it] = in_ld4(b + o);
-    xq[it] = in_ld4(q + o);
+  for (int s = 0; s < NSLOT; ++s) {
+    const int t = wv + 4 * s < WY_NTL ? wv + 4 * s : 0, ti = tri_row(t), tj = t - ti * (ti + 1) / 2;
+    pcs[s] = piece_at(cf.pieces, cf.tile_piece[4 * ti + tj]);
   }
 
-  // 1. gc = cumsum(g) inside the chunk
-  chunk_cumsum<D, LD, NT>(static_cast<const TIn*>(a.g) + tio, sG);
-
-  // 2a. row fragments (cd_slim.py:17-21): FA(Kg) with kg = san(k e^{min(gl-gc,0)}),
-  //     FA(Qg) with qg = san(q e^{min(gc,0)}); b*k and w*v into LDS.
-  // 2b. column fragments FA(Kg^T) (D x T): the wave holds one whole 16x16 block of k per item
-  //     (block wv + 8 it), which a per-wave LDS transpose (in S, free until the scores) turns
-  //     into lane l of the transposed block: 4 consecutive tokens of one channel.
-  // The fragments stay in registers until the scores are done and the w / v loads issued: the
-  // vector memory counter is in order and counts stores, so stores issued here would hold back
-  // the score phase's q / k loads until they drained.
-  float* tr = sS + wv * 16 * TRP;
-  const bool colf = a.kgT_f != nullptr;
-  float4 kgv[NIT], qgv[NIT], ktv[NIT];
+  // this pass's inputs: the cumsum's g runs, and q, k, b as the wave's row fragments
+  CumsumPass<D, 512, NT, DC / 4> cs;
+  float4 xq[NKBP], xk[NKBP], xb[NKBP];
+  auto load_pass = [&](int p) __attribute__((always_inline)) {
+    cs.load(gg, DC * p);
 #pragma unroll
-  for (int it = 0; it < NIT; ++it) {
-    const int f = tid + it * NT, blk = f >> 6, ln = f & 63;
-    const int i = 16 * (blk / NKB) + (ln & 15), d = 16 * (blk % NKB) + 4 * (ln >> 4);
-    const float4 gc = ld4(sG + i * LD + d);
-    st4(sBK + i * LD + d, mul4(xb[it], xk[it]));
-    kgv[it] = san4(mul4(xk[it], expnp4(sub4(ld4(sG + (T - 1) * LD + d), gc))), clip);
-    qgv[it] = san4(mul4(xq[it], expnp4(gc)), clip);
-    ktv[it] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (colf) {
-      // lane (r, g): channel dc = 16 bj + r at tokens i0 + e, e = 0..3
-      const int bi = blk / NKB, bj = blk % NKB, dc = 16 * bj + r, i0 = 16 * bi + 4 * g;
-      const float4 kc = wave_transpose16(tr, xk[it], r, g);
-      const float gl = sG[(T - 1) * LD + dc];
-      const float kv4[4] = {kc.x, kc.y, kc.z, kc.w};
-      float kt[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) kt[e] = sanitize(kv4[e] * exp_nonpos(gl - sG[(i0 + e) * LD + dc]), clip);
-      ktv[it] = make_float4(kt[0], kt[1], kt[2], kt[3]);
+    for (int kb = 0; kb < NKBP; ++kb) {
+      const int o = row * D + DC * p + 16 * kb + 4 * g;
+      xq[kb] = in_ld4(q + o);
+      xk[kb] = in_ld4(k + o);
+      xb[kb] = in_ld4(b + o);
     }
-  }
-  __syncthreads();
+  };
+  load_pass(0);
 
-  // 3. scores, all pieces at once (scores.py:42-75): Aqk = s (q ra)(k cb)^T, Akk = (bk ra)(k cb)^T
-  {
-    const int np = cf.pieces.n, P = cf.pieces.p[0].P, nb = P / 16, tpp = nb * nb;
-    const bool lean = cf.diag == DIAG_LEAN;
-    for (int t = wv; t < np * tpp; t += NW) {
-      const Piece pc = cf.pieces.p[t / tpp];
-      if (pc.kind == 1 && lean) continue;
-      const int rem = t % tpp, ti = rem / nb, tj = rem % nb;
-      const int i = pc.row0 + 16 * ti + r, j = pc.col0 + 16 * tj + r;
-      f4 accq = {0.f, 0.f, 0.f, 0.f}, acck = {0.f, 0.f, 0.f, 0.f};
-      if (pc.kind == 0) score_pair<D, LD, DOT, 0, TIn>(accq, acck, q, sBK, k, sG, pc, i, j);
-      else score_pair<D, LD, DOT, 1, TIn>(accq, acck, q, sBK, k, sG, pc, i, j);
+  f4 accq[NSLOT], acck[NSLOT];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int o = (pc.row0 + 16 * ti + 4 * g + e) * LT + pc.col0 + 16 * tj + r;
-        sS[o] = cf.scale * accq[e];
-        sK[o] = acck[e];
+  for (int s = 0; s < NSLOT; ++s) accq[s] = acck[s] = f4{0.f, 0.f, 0.f, 0.f};
+  float4 xT[NKB];     // X^T = (b k e^gc)^T, fragment blocks (kb, wv), staged for Wp after the scores
+  // LEAN: this thread's diagonal-piece elements (element m = tid + NT m of the diagonal pieces
+  // taken in order), their running sums over d
+  constexpr int NLEAN = LEAN ? 12 : 1;
+  float lq[NLEAN], lk[NLEAN];
+#pragma unroll
+  for (int m = 0; m < NLEAN; ++m) lq[m] = lk[m] = 0.f;
+  // element m of the diagonal pieces -> (row, col), or false past their end
+  auto lean_elem = [&](int m, int& er, int& ec) -> bool {
+    int e = tid + NT * m;
+    for (int pi = 0; pi < cf.pieces.n; ++pi) {
+      const Piece pc = piece_at(cf.pieces, pi);
+      if (pc.kind != 1) continue;
+      if (e < pc.P * pc.P) {
+        er = pc.row0 + e / pc.P;
+        ec = pc.col0 + e % pc.P;
+        return true;
       }
+      e -= pc.P * pc.P;
     }
-    if (lean) {
-      // lean diagonal (scores.py:34-39): exact exp(clip(gc_i - gc_j, +-diff_clip)) per element
-      const float dc = cf.diff_clip;
-      for (int pi = 0; pi < np; ++pi) {
-        const Piece pc = cf.pieces.p[pi];
-        if (pc.kind != 1) continue;
-        for (int e = tid; e < P * P; e += NT) {
-          const int row = pc.row0 + e / P, col = pc.col0 + e % P;
-          float sq = 0.f, sk = 0.f;
-          for (int d = 0; d < D; ++d) {
-            const float E = expf(clip_nan(sG[row * LD + d] - sG[col * LD + d], -dc, dc));
-            const float kj = in_val(k + col * D + d);
-            sq += (in_val(q + row * D + d) * E) * kj;
-            sk += (sBK[row * LD + d] * E) * kj;
-          }
-          sS[row * LT + col] = cf.scale * sq;
-          sK[row * LT + col] = sk;
+    return false;
+  };
+
+#pragma unroll
+  for (int p = 0; p < NPASS; ++p) {
+    // 1. gc = cumsum(g) inside the chunk, this pass's columns (fragment layout)
+    cs.run(sG, reinterpret_cast<float4*>(sQ));
+
+    // 2. gated fragments (cd_slim.py:17-21): Kg = san(k e^{min(gl - gc, 0)}) as FRAG(Kg) and,
+    //    through the wave's transpose tile, FRAG(Kg^T); Qg = san(q e^{min(gc, 0)}); X = b k e^{min(gc, 0)}
+    //    (transposed, kept for Wp).  Staged for the scores: gc (already), q, k, b k.
+    float4 kgv[NKBP], qgv[NKBP], bkv[NKBP];
+#pragma unroll
+    for (int kb = 0; kb < NKBP; ++kb) {
+      const int o = frag_blk(wv, kb, DC) + 4 * l;
+      const float4 gc = ld4(sG + o), gl = ld4(sG + frag_off(T - 1, 16 * kb + 4 * g, DC));
+      kgv[kb] = san4(mul4(xk[kb], expnp4(sub4(gl, gc))), clip);
+      const float4 eg = expnp4(gc);
+      qgv[kb] = san4(mul4(xq[kb], eg), clip);
+      bkv[kb] = mul4(xb[kb], xk[kb]);
+      st4(sQ + o, xq[kb]);
+      st4(sKs + o, xk[kb]);
+      st4(sBK + o, bkv[kb]);
+      xT[NKBP * p + kb] = wave_transpose16(tr, mul4(bkv[kb], eg), r, g);
+    }
+    // the next pass's loads go out before this pass's stores (the memory counter is in order)
+    if (p + 1 < NPASS) load_pass(p + 1);
+#pragma unroll
+    for (int kb = 0; kb < NKBP; ++kb) {
+      const int kg = NKBP * p + kb, d = DC * p + 16 * kb + 4 * g;
+      if (a.kg_f) stg4(a.kg_f + tb + frag_blk(wv, kg, D) + 4 * l, kgv[kb]);
+      if (a.kg) stg4(a.kg + tb + row * D + d, kgv[kb]);
+      if (a.qg_f) stg4(a.qg_f + tb + frag_blk(wv, kg, D) + 4 * l, qgv[kb]);
+      if (a.qg) stg4(a.qg + tb + row * D + d, qgv[kb]);
+      if (a.kgT_f) stg4(a.kgT_f + tb + frag_blk(kg, wv, T) + 4 * l, wave_transpose16(tr, kgv[kb], r, g));
+    }
+    if (a.gl && tid < DC) a.gl[(size_t)chunk * D + DC * p + tid] = sG[frag_off(T - 1, tid, DC)];
+    __syncthreads();
+
+    // 3. scores over this pass's k blocks (scores.py:39-84): tiles t = wv + 4 s
+#pragma unroll
+    for (int s = 0; s < NSLOT; ++s) {
+      const int t = wv + 4 * s;
+      if (t >= WY_NTL) continue;
+      const int ti = tri_row(t), tj = t - ti * (ti + 1) / 2;
+      const Piece& pc = pcs[s];
+      if (pc.kind == 0) score_tile_pass<DC, DOT, 0>(accq[s], acck[s], sG, sQ, sKs, sBK, pc, ti, tj);
+      else if (!LEAN) score_tile_pass<DC, DOT, 1>(accq[s], acck[s], sG, sQ, sKs, sBK, pc, ti, tj);
+    }
+    if constexpr (LEAN) {
+      // exact diagonal: exp(clip(gc_i - gc_j, +-diff_clip)) per element and channel, summed over
+      // the channels in order (the pass's channels continue the previous pass's sums)
+      const float dcl = cf.diff_clip;
+#pragma unroll
+      for (int m = 0; m < NLEAN; ++m) {
+        int er, ec;
+        if (!lean_elem(m, er, ec)) continue;
+        for (int d = 0; d < DC; ++d) {
+          const int oi = frag_off(er, d, DC), oj = frag_off(ec, d, DC);
+          const float E = expf(clip_nan(sG[oi] - sG[oj], -dcl, dcl));
+          const float kj = sKs[oj];
+          lq[m] += (sQ[oi] * E) * kj;
+          lk[m] += (sBK[oi] * E) * kj;
         }
       }
     }
+    __syncthreads();
   }
-  __syncthreads();
 
-  // w and v for U (items as in the prologue); they arrive during the masks and the inverse
-  float4 xw[NIT], xv[NIT];
+  // 4. masks + sanitize (scores.py:83-84); Se = (1-eps) Akk for the solve (solve.py:25).  Aqk
+  //    goes out as FRAG(Aqk) (the upper blocks as zeros), Akk into LDS row-major.
+  const float ome = cf.ome, scale = cf.scale;
 #pragma unroll
-  for (int it = 0; it < NIT; ++it) {
-    const int f = tid + it * NT, blk = f >> 6, ln = f & 63;
-    const int o = (16 * (blk / NKB) + (ln & 15)) * D + 16 * (blk % NKB) + 4 * (ln >> 4);
-    xw[it] = in_ld4(w + o);
-    xv[it] = in_ld4(v + o);
-  }
-  // the fragment stores of step 2 (behind the w / v loads in the memory counter's order)
-#pragma unroll
-  for (int it = 0; it < NIT; ++it) {
-    const int f = tid + it * NT, blk = f >> 6, ln = f & 63;
-    const int i = 16 * (blk / NKB) + (ln & 15), d = 16 * (blk % NKB) + 4 * (ln >> 4);
-    if (a.kg_f) stg4(a.kg_f + tb + 4 * f, kgv[it]);
-    if (a.kg) stg4(a.kg + tb + i * D + d, kgv[it]);
-    if (a.qg_f) stg4(a.qg_f + tb + 4 * f, qgv[it]);
-    if (a.qg) stg4(a.qg + tb + i * D + d, qgv[it]);
-    if (colf) stg4(a.kgT_f + tb + frag_blk(blk % NKB, blk / NKB, T) + 4 * l, ktv[it]);
-  }
-  if (a.gl && tid < D) a.gl[(size_t)chunk * D + tid] = sG[(T - 1) * LD + tid];
-
-  // 4. masks + sanitize (scores.py:84-87); Se = (1-eps) Akk for the solve (solve.py:25)
-  for (int f = tid; f < T * T / 4; f += NT) {
-    const int i = f / (T / 4), j = 4 * (f % (T / 4));
-    const float4 s4v = ld4(sS + i * LT + j), k4v = ld4(sK + i * LT + j);
-    const float sv[4] = {s4v.x, s4v.y, s4v.z, s4v.w}, kv[4] = {k4v.x, k4v.y, k4v.z, k4v.w};
+  for (int s = 0; s < NSLOT; ++s) {
+    const int t = wv + 4 * s;
+    if (t >= WY_NTL) continue;
+    const int ti = tri_row(t), tj = t - ti * (ti + 1) / 2;
+    if (LEAN && pcs[s].kind == 1) continue;
+    const int i = 16 * ti + r, j0 = 16 * tj + 4 * g;
     float aq[4], ak[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      aq[e] = j + e <= i ? sanitize(sv[e], clip) : 0.f;
-      ak[e] = j + e < i ? sanitize(kv[e], clip) : 0.f;
+      aq[e] = j0 + e <= i ? sanitize(scale * accq[s][e], clip) : 0.f;
+      ak[e] = j0 + e < i ? sanitize(acck[s][e], clip) : 0.f;
     }
     const float4 aq4 = make_float4(aq[0], aq[1], aq[2], aq[3]), ak4 = make_float4(ak[0], ak[1], ak[2], ak[3]);
-    st4(sS + i * LT + j, aq4);
-    st4(sK + i * LT + j, scale4(ak4, cf.ome));
-    st4(sI + i * LT + j, make_float4(0.f, 0.f, 0.f, 0.f));
-    if (a.aqk) stg4(a.aqk + sb + i * T + j, aq4);
-    if (a.akk) stg4(a.akk + sb + i * T + j, ak4);
+    st4(sK + i * LT + j0, scale4(ak4, ome));
+    if (a.aqk_f) stg4(a.aqk_f + sb + frag_blk(ti, tj, T) + 4 * l, aq4);
+    if (a.aqk) stg4(a.aqk + sb + i * T + j0, aq4);
+    if (a.akk) stg4(a.akk + sb + i * T + j0, ak4);
   }
+  // upper tiles (tj > ti): zeros
+  for (int t = wv; t < 16; t += 4) {
+    const int ti = t / 4, tj = t % 4;
+    if (tj <= ti) continue;
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (a.aqk_f) stg4(a.aqk_f + sb + frag_blk(ti, tj, T) + 4 * l, z);
+    if (a.aqk) stg4(a.aqk + sb + (16 * ti + r) * T + 16 * tj + 4 * g, z);
+    if (a.akk) stg4(a.akk + sb + (16 * ti + r) * T + 16 * tj + 4 * g, z);
+  }
+  if constexpr (LEAN) {
+#pragma unroll
+    for (int m = 0; m < NLEAN; ++m) {
+      int er, ec;
+      if (!lean_elem(m, er, ec)) continue;
+      const float aq = ec <= er ? sanitize(scale * lq[m], clip) : 0.f;
+      const float ak = ec < er ? sanitize(lk[m], clip) : 0.f;
+      sK[er * LT + ec] = ak * ome;
+      if (a.aqk_f) a.aqk_f[sb + frag_off(er, ec, T)] = aq;
+      if (a.aqk) a.aqk[sb + er * T + ec] = aq;
+      if (a.akk) a.akk[sb + er * T + ec] = ak;
+    }
+  }
+  for (int f = tid; f < T * T / 4; f += NT) st4(sI + (f / (T / 4)) * LT + 4 * (f % (T / 4)), make_float4(0.f, 0.f, 0.f, 0.f));
   __syncthreads();
 
-  // 5a. FA(Aqk); X = b k e^{min(gc,0)} in place (cd_slim.py:17); leaf inverses
-  if (a.aqk_f) {
-    for (int f = tid; f < T * T / 4; f += NT) {
-      const int blk = f >> 6, ln = f & 63, bi = blk >> 2, bj = blk & 3, rr = ln & 15, gg = ln >> 4;
-      stg4(a.aqk_f + sb + 4 * f, ld4(sS + (16 * bi + rr) * LT + 16 * bj + 4 * gg));
-    }
-  }
-  for (int f = tid; f < T * D / 4; f += NT) {
-    const int i = f / (D / 4), d = 4 * (f % (D / 4));
-    st4(sBK + i * LD + d, mul4(ld4(sBK + i * LD + d), expnp4(ld4(sG + i * LD + d))));
-  }
-  // w v is needed only by U at the end: its loads were issued after the scores, so that they
-  // stream in during the masks and the inverse instead of adding to the load burst at the start
-  wy_inverse<LT, NT, NW>(cf, sK, sI, sS, a.A ? a.A + sb : nullptr, tid, wv, r, g, [&]() {
-#pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-      const int f = tid + it * NT, blk = f >> 6, ln = f & 63;
-      const int i = 16 * (blk / NKB) + (ln & 15), d = 16 * (blk % NKB) + 4 * (ln >> 4);
-      st4(sY + i * LD + d, mul4(xw[it], xv[it]));
-    }
-  });
+  // 5. the WY inverse
+  wy_inverse<LT, NT>(cf, sK, sI, sM, a.A ? a.A + sb : nullptr, tid, wv, r, g, [] {});
 
   // 6. Wp = san(A X), U = san(A (w v)); A is unit lower triangular, so row tile ti only needs
   //    k blocks 0..ti.  Lane l's accumulator is lane l of FA(P^T) block (tj, ti); FA(Wp) goes
-  //    through a per-wave 16x16 transpose in LDS.
-  {
-    float* sW = sS + wv * (16 * 20);
-    constexpr int NTJ = D / 16, NTM = (T / 16) * NTJ;
-    const bool want_w = a.wp_f || a.wpT_f || a.wp, want_u = a.uT_f || a.u;
-    // the epilogue of tile (mat, ti, tj): sanitize, then the requested layouts
-    auto store_tile = [&](int mat, int ti, int tj, const f4& acc) __attribute__((always_inline)) {
-      const float4 p = san4(f4_to_float4(acc), clip);     // p.e = P[16 ti + 4 g + e][16 tj + r]
-      float* rowmaj = mat ? a.u : a.wp;
-      if (rowmaj) {
-        float* o = rowmaj + tb + (size_t)(16 * ti + 4 * g) * D + 16 * tj + r;
-        o[0] = p.x; o[D] = p.y; o[2 * D] = p.z; o[3 * D] = p.w;
-      }
-      float* fT = mat ? a.uT_f : a.wpT_f;
-      if (fT) stg4(fT + tb + frag_blk(tj, ti, T) + 4 * l, p);
-      if (mat == 0 && a.wp_f) {
-        sW[(4 * g + 0) * 20 + r] = p.x;
-        sW[(4 * g + 1) * 20 + r] = p.y;
-        sW[(4 * g + 2) * 20 + r] = p.z;
-        sW[(4 * g + 3) * 20 + r] = p.w;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        stg4(a.wp_f + tb + frag_blk(ti, tj, D) + 4 * l, ld4(sW + r * 20 + 4 * g));
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      }
-    };
-    if constexpr (NTJ == NW) {
-      // wave w owns column strip tj = w of both products: the strip's B operands (k blocks
-      // 0..3) are read once, and the four row tiles' chains (lengths 1..4) are interleaved
-      // k-block-major; each tile still accumulates its k blocks in ascending order
-      const int tj = wv;
+  //    through the wave's transpose tile.  Wave wv owns column strips wv, wv + 4, ...: each
+  //    strip's B operands (FRAG(X^T) blocks (tj, kb)) are read once and the four row tiles'
+  //    chains (lengths 1..4) interleaved k-block-major; each tile accumulates its k blocks in
+  //    ascending order.
+  const bool want_w = a.wp_f || a.wpT_f || a.wp, want_u = a.uT_f || a.u;
+  auto store_tile = [&](int mat, int ti, int tj, const f4& acc) __attribute__((always_inline)) {
+    const float4 pv = san4(f4_to_float4(acc), clip);     // pv.e = P[16 ti + 4 g + e][16 tj + r]
+    float* rowmaj = mat ? a.u : a.wp;
+    if (rowmaj) {
+      float* o = rowmaj + tb + (size_t)(16 * ti + 4 * g) * D + 16 * tj + r;
+      o[0] = pv.x; o[D] = pv.y; o[2 * D] = pv.z; o[3 * D] = pv.w;
+    }
+    float* fT = mat ? a.uT_f : a.wpT_f;
+    if (fT) stg4(fT + tb + frag_blk(tj, ti, T) + 4 * l, pv);
+    if (mat == 0 && a.wp_f) stg4(a.wp_f + tb + frag_blk(ti, tj, D) + 4 * l, wave_transpose16(tr, pv, r, g));
+  };
+  // strips of four channel tiles at a time (group m): the group's B operands (blocks (tj, kb) of
+  // X^T or Y^T) staged in the Akk slot, wave wv computes strip tj = 4 m + wv
+  auto products = [&](int mat, int m, const float4* opT) __attribute__((always_inline)) {
+    {
 #pragma unroll
-      for (int mat = 0; mat < 2; ++mat) {
-        if (mat ? !want_u : !want_w) continue;
-        const float* X = mat ? sY : sBK;
-        float4 xb[4];
+      for (int c = 0; c < 4; ++c) st4(sX + frag_blk(c, wv, T) + 4 * l, opT[c]);
+      __syncthreads();
+      const int tj = 4 * m + wv;
+      float4 xbv[4];
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-          const float* xc = X + (16 * kb + 4 * g) * LD + 16 * tj + r;
-          xb[kb] = make_float4(xc[0], xc[LD], xc[2 * LD], xc[3 * LD]);
-        }
-        f4 acc[4];
+      for (int kb = 0; kb < 4; ++kb) xbv[kb] = ld4(sX + frag_blk(wv, kb, T) + 4 * l);
+      __syncthreads();
+      f4 acc[4];
 #pragma unroll
-        for (int ti = 0; ti < 4; ++ti) acc[ti] = f4{0.f, 0.f, 0.f, 0.f};
+      for (int ti = 0; ti < 4; ++ti) acc[ti] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
+      for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-          for (int ti = kb; ti < 4; ++ti) mma16<DOT>(acc[ti], ld4(sI + (16 * ti + r) * LT + 16 * kb + 4 * g), xb[kb]);
-        drain(acc[0], acc[1], acc[2], acc[3]);
+        for (int ti = kb; ti < 4; ++ti) mma16<DOT>(acc[ti], ld4(sI + (16 * ti + r) * LT + 16 * kb + 4 * g), xbv[kb]);
+      drain(acc[0], acc[1], acc[2], acc[3]);
 #pragma unroll
-        for (int ti = 0; ti < 4; ++ti) store_tile(mat, ti, tj, acc[ti]);
-      }
-    } else {
-      for (int t = wv; t < 2 * NTM; t += NW) {
-        const int mat = t / NTM, ti = (t % NTM) / NTJ, tj = t % NTJ;
-        if (mat ? !want_u : !want_w) continue;
-        const float* X = mat ? sY : sBK;
-        f4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (int kb = 0; kb <= ti; ++kb) {
-          const float4 av = ld4(sI + (16 * ti + r) * LT + 16 * kb + 4 * g);
-          const float* xb = X + (16 * kb + 4 * g) * LD + 16 * tj + r;
-          mma16<DOT>(acc, av, make_float4(xb[0], xb[LD], xb[2 * LD], xb[3 * LD]));
-        }
-        drain(acc);
-        store_tile(mat, ti, tj, acc);
-      }
+      for (int ti = 0; ti < 4; ++ti) store_tile(mat, ti, tj, acc[ti]);
+    }
+  };
+  // w and v of one strip group (the wave's row fragments), for Y = w v: group 0's loads go out
+  // before the Wp products, each next group's before the current group's U products
+  float4 xw[4], xv[4];
+  auto load_wv = [&](int m) __attribute__((always_inline)) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int o = row * D + 64 * m + 16 * c + 4 * g;
+      xw[c] = in_ld4(w + o);
+      xv[c] = in_ld4(v + o);
+    }
+  };
+  if (want_u) load_wv(0);
+  if (want_w) {
+#pragma unroll
+    for (int m = 0; m < NKB / 4; ++m) products(0, m, xT + 4 * m);
+  }
+  if (want_u) {
+#pragma unroll
+    for (int m = 0; m < NKB / 4; ++m) {
+      float4 yT[4];     // blocks (4 m + c, wv) of Y^T
+#pragma unroll
+      for (int c = 0; c < 4; ++c) yT[c] = wave_transpose16(tr, mul4(xw[c], xv[c]), r, g);
+      if (m + 1 < NKB / 4) load_wv(m + 1);
+      products(1, m, yT);
     }
   }
 }
@@ -629,14 +651,16 @@ hipError_t launch_stream_probe(int mode, const void* src, void* dst, size_t n4, 
 }
 
 hipError_t launch_wy_fwd(int D, const WyFwdArgs& a, hipStream_t s, bool bf16_inputs) {
+  const bool lean = a.cfg.diag == DIAG_LEAN;
   dispatch_mode(a.cfg.dot_mode, [&](auto m) {
     constexpr int M = decltype(m)::value;
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, dim3(a.n_chunks), dim3(256), 0, s, a); };
     if (bf16_inputs) {
-      if (D == 128) hipLaunchKernelGGL((wy_fwd_kernel<128, M, uint16_t>), dim3(a.n_chunks), dim3(512), 0, s, a);
-      else hipLaunchKernelGGL((wy_fwd_kernel<64, M, uint16_t>), dim3(a.n_chunks), dim3(512), 0, s, a);
+      if (D == 128) lean ? go(wy_fwd_kernel<128, M, true, uint16_t>) : go(wy_fwd_kernel<128, M, false, uint16_t>);
+      else lean ? go(wy_fwd_kernel<64, M, true, uint16_t>) : go(wy_fwd_kernel<64, M, false, uint16_t>);
     } else {
-      if (D == 128) hipLaunchKernelGGL((wy_fwd_kernel<128, M, float>), dim3(a.n_chunks), dim3(512), 0, s, a);
-      else hipLaunchKernelGGL((wy_fwd_kernel<64, M, float>), dim3(a.n_chunks), dim3(512), 0, s, a);
+      if (D == 128) lean ? go(wy_fwd_kernel<128, M, true, float>) : go(wy_fwd_kernel<128, M, false, float>);
+      else lean ? go(wy_fwd_kernel<64, M, true, float>) : go(wy_fwd_kernel<64, M, false, float>);
     }
     return 0;
   });

@@ -55,7 +55,29 @@ struct Cfg {
   // wy_eps = 0 every chunk size is the 64-chunk operator).
   int group;
   PieceList pieces;
+  // the piece that covers 16 x 16 score tile (ti, tj), at [4 ti + tj], for ti >= tj (pieces are
+  // squares of side 16 or 32 on multiples of their side, so a tile lies in exactly one).  32-bit
+  // entries: a kernel reads them with a wave-uniform index as scalar loads (there is no scalar
+  // byte load, and a vector load of kernel arguments would make its wait cover every memory
+  // operation in flight).
+  int32_t tile_piece[16];
 };
+
+// Piece i of a piece list held in the kernel arguments, read as two scalar dwords (i wave-uniform)
+__device__ __forceinline__ Piece piece_at(const PieceList& pl, int i) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(&pl.p[i]);
+  const uint32_t w0 = w[0], w1 = w[1];
+  Piece p;
+  p.row0 = (int8_t)(w0 & 0xff);
+  p.col0 = (int8_t)((w0 >> 8) & 0xff);
+  p.P = (int8_t)((w0 >> 16) & 0xff);
+  p.kind = (int8_t)(w0 >> 24);
+  p.anchor = (int8_t)(w1 & 0xff);
+  p.s0 = (int8_t)((w1 >> 8) & 0xff);
+  p.s1 = (int8_t)((w1 >> 16) & 0xff);
+  p.pad = (int8_t)(w1 >> 24);
+  return p;
+}
 
 // Offset in floats of a chunk (index (b, h) * nc + chunk of the segment) in a raw operator
 // tensor -- q..g, o, dO and the input gradients, (B, H, seq_ld, D) with the segment starting at
