@@ -17,16 +17,16 @@ LIB_PATH = Path(os.environ.get("GDN2_LIB", Path(__file__).resolve().parent / "_l
 
 DOT_IDS = {"highest": 0, "bf16x3": 1, "default": 2}
 DIAG_IDS = {"btl": 0, "lean": 1}
-RES_NAMES = ("aqk", "A", "h_pre", "v_new", "wpT", "kg", "qg", "gl")
+RES_NAMES = ("aqk", "A", "h_pre", "v_new", "wp", "kg", "qg", "gl")
 # per residual: (rows, cols) of the stored matrix per chunk (T = bt, D = head dim), whether it
 # is stored in fragment layout, and whether it is the transpose of the named quantity
 RES_STORAGE = {"aqk": ("T", "T", True, False), "A": ("T", "T", False, False),
                "h_pre": ("D", "D", True, True), "v_new": ("D", "T", True, True),
-               "wpT": ("D", "T", True, True), "kg": ("T", "D", True, False),
+               "wp": ("T", "D", True, False), "kg": ("T", "D", True, False),
                "qg": ("T", "D", True, False), "gl": (None, "D", False, False)}
 KERNEL_NAMES = ("wy_fwd", "scan_fwd", "scan_bwd", "bwd_state", "bwd_wy", "out_fwd", "bwd_pre", "bwd_state_rc",
                 "decode")
-ABI_VERSION = 2
+ABI_VERSION = 3
 STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported configuration", 3: "HIP error"}
 
 _c_int, _c_dbl, _c_size, _vp = ctypes.c_int32, ctypes.c_double, ctypes.c_size_t, ctypes.c_void_p
@@ -116,7 +116,7 @@ def residual_layout(desc: Gdn2Desc):
 
 def decode_residual(name, flat, B, H, nc, T, D):
     """Row-major (B, H, nc, rows, cols) tensor of one residual sub-buffer (``flat`` float32),
-    un-transposed: wpT -> Wp, h_pre / v_new in their natural layout."""
+    un-transposed: h_pre / v_new in their natural layout."""
     from .layout import from_frag
     R, C, frag, transposed = RES_STORAGE[name]
     dim = {"T": T, "D": D}

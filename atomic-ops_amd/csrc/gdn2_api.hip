@@ -23,7 +23,7 @@ bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
 
 gdn2::Cfg make_cfg(const gdn2_desc* d);
 
-// Validation mirrors BLRConfig.__post_init__ (atomic_gdn2/config.py:62-75) plus this
+// Validation mirrors BLRConfig.__post_init__ (atomic_gdn2/config.py:52-65) plus this
 // build's supported geometry.
 int validate(const gdn2_desc* d) {
   if (!d) return fail(GDN2_ERR_INVALID, "null descriptor");
@@ -151,7 +151,7 @@ void residual_sizes(const gdn2_desc* d, size_t sz[GDN2_RES_COUNT]) {
   const size_t nck = (size_t)gdn2::CkptBlocks((int)x.nc, eff_ckpt(d), damped_group(d)).nblk;
   sz[GDN2_RES_HPRE] = x.n_bh * nck * x.DD * 4;
   sz[GDN2_RES_VNEW] = x.n_chunks * x.tD * 4;
-  sz[GDN2_RES_WPT] = x.n_chunks * x.tD * 4;
+  sz[GDN2_RES_WP] = x.n_chunks * x.tD * 4;
   sz[GDN2_RES_KG] = x.n_chunks * x.tD * 4;
   sz[GDN2_RES_QG] = x.n_chunks * x.tD * 4;
   sz[GDN2_RES_GL] = x.n_chunks * x.D * 4;
@@ -218,14 +218,14 @@ int gdn2_residual_layout(const gdn2_desc* d, size_t offsets[GDN2_RES_COUNT], siz
   return GDN2_OK;
 }
 
-// forward workspace (fragment layouts): [Wp | U^T | Kg^T], and without a residual also
-// [Qg | Aqk | gl] (with a residual those live in it).
+// forward workspace (fragment layouts): [U^T | Kg^T], and without a residual also
+// [Wp | Qg | Aqk | gl] (with a residual those live in it).
 size_t gdn2_fwd_workspace_bytes(const gdn2_desc* d, int with_residual) {
   if (with_residual ? validate_residual(d) : validate(d)) return 0;
   const Dims x = dims(d);
-  size_t n = 3 * align_up(x.n_chunks * x.tD * 4);
+  size_t n = 2 * align_up(x.n_chunks * x.tD * 4);
   if (!with_residual)
-    n += align_up(x.n_chunks * x.tD * 4) + align_up(x.n_chunks * x.tT * 4) + align_up(x.n_chunks * x.D * 4);
+    n += 2 * align_up(x.n_chunks * x.tD * 4) + align_up(x.n_chunks * x.tT * 4) + align_up(x.n_chunks * x.D * 4);
   return n;
 }
 
@@ -258,12 +258,13 @@ int fwd_impl(const gdn2_desc* d, const void* q, const void* k, const void* v, co
   // operands of the scan and the output kernel, all in fragment layout
   size_t o2 = 0;
   auto take = [&](size_t bytes) { float* p = at<float>(workspace, o2); o2 += align_up(bytes); return p; };
-  float* wp = take(x.n_chunks * x.tD * 4);
   float* uT = take(x.n_chunks * x.tD * 4);
   float* kgT = take(x.n_chunks * x.tD * 4);
-  // residuals for the backward -- training only; otherwise Qg / Aqk / gl live in the workspace
-  // and h_pre / v_new are not stored at all (the scan consumes them itself)
-  float *A = nullptr, *wpT = nullptr, *kg = nullptr, *qg, *aqk, *gl, *hpre = nullptr, *vnew = nullptr;
+  // residuals for the backward -- training only; otherwise Wp / Qg / Aqk / gl live in the
+  // workspace and Kg, h_pre and v_new are not stored at all (the scan consumes h_pre and v_new
+  // itself).  Wp is kept in the orientation the forward scan contracts over keys; the reverse
+  // scan, which contracts it over tokens, transposes it in LDS (gdn2_scan.hip).
+  float *A = nullptr, *wp, *kg = nullptr, *qg, *aqk, *gl, *hpre = nullptr, *vnew = nullptr;
   if (residual) {
     size_t off[GDN2_RES_COUNT], tot;
     residual_offsets(d, off, &tot);
@@ -271,11 +272,12 @@ int fwd_impl(const gdn2_desc* d, const void* q, const void* k, const void* v, co
     A = at<float>(residual, off[GDN2_RES_A]);
     hpre = at<float>(residual, off[GDN2_RES_HPRE]);
     vnew = at<float>(residual, off[GDN2_RES_VNEW]);
-    wpT = at<float>(residual, off[GDN2_RES_WPT]);
+    wp = at<float>(residual, off[GDN2_RES_WP]);
     kg = at<float>(residual, off[GDN2_RES_KG]);
     qg = at<float>(residual, off[GDN2_RES_QG]);
     gl = at<float>(residual, off[GDN2_RES_GL]);
   } else {
+    wp = take(x.n_chunks * x.tD * 4);
     qg = take(x.n_chunks * x.tD * 4);
     aqk = take(x.n_chunks * x.tT * 4);
     gl = take(x.n_chunks * x.D * 4);
@@ -283,7 +285,7 @@ int fwd_impl(const gdn2_desc* d, const void* q, const void* k, const void* v, co
 
   gdn2::WyFwdArgs wa{};
   wa.q = q; wa.k = k; wa.v = v; wa.w = w; wa.b = b; wa.g = g;
-  wa.wp_f = wp; wa.wpT_f = wpT; wa.uT_f = uT; wa.kg_f = kg; wa.kgT_f = kgT; wa.qg_f = qg;
+  wa.wp_f = wp; wa.uT_f = uT; wa.kg_f = kg; wa.kgT_f = kgT; wa.qg_f = qg;
   wa.aqk_f = aqk; wa.A = A; wa.gl = gl;
   wa.n_chunks = (int)x.n_chunks;
   wa.cfg = cfg;
@@ -425,7 +427,7 @@ int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v,
   const float* A = at<float>(res, off[GDN2_RES_A]);
   const float* hpre = at<float>(res, off[GDN2_RES_HPRE]);
   const float* vnew = at<float>(res, off[GDN2_RES_VNEW]);
-  const float* wpT = at<float>(res, off[GDN2_RES_WPT]);
+  const float* wp = at<float>(res, off[GDN2_RES_WP]);
   const float* kg = at<float>(res, off[GDN2_RES_KG]);
   const float* qg = at<float>(res, off[GDN2_RES_QG]);
   const float* gl = at<float>(res, off[GDN2_RES_GL]);
@@ -445,7 +447,7 @@ int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v,
   hipError_t e = timed(6, s, [&] { return gdn2::launch_bwd_pre(d->D, pa, s); });
   if (e != hipSuccess) return hip_fail(e, "bwd_pre launch");
 
-  gdn2::ScanBwdArgs sa{wpT, kg, gl, xo, yo, d_hf, dvn, dhn, dh0, ez, (int)x.nc, (int)x.n_bh, cfg};
+  gdn2::ScanBwdArgs sa{wp, kg, gl, xo, yo, d_hf, dvn, dhn, dh0, ez, (int)x.nc, (int)x.n_bh, cfg};
   e = timed(2, s, [&] { return gdn2::launch_scan_bwd(d->D, sa, s); });
   if (e != hipSuccess) return hip_fail(e, "scan_bwd launch");
 

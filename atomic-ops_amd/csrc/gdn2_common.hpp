@@ -491,6 +491,22 @@ __device__ __forceinline__ float4 wave_transpose16(float* tr, const float4 x, in
                      tr[(4 * g + 3) * TRP + r]);
 }
 
+// N tiles at once: x[i] (MFMA result / operand layout) -> y[i], the transposed tile, through N
+// per-wave LDS tiles of 16 x TRP floats at tr: every write, one wave barrier, every read.
+template <int N>
+__device__ __forceinline__ void wave_transpose16_n(float* tr, const float4* x, float4* y, int r, int g) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) st4(tr + i * 16 * TRP + r * TRP + 4 * g, x[i]);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float* t = tr + i * 16 * TRP;
+    y[i] = make_float4(t[(4 * g) * TRP + r], t[(4 * g + 1) * TRP + r], t[(4 * g + 2) * TRP + r], t[(4 * g + 3) * TRP + r]);
+  }
+}
+
 // In-chunk cumulative sum of g over the T rows of a (T x D) tile, into LDS sG (ld = LD).
 // Thread t owns float4 column t % (D/4) over a run of RUN consecutive rows: it sums its run,
 // then adds the totals of the runs above it in order.  Same code in every kernel, so every

@@ -456,26 +456,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void w
   wy_inverse<LT, NT>(cf, sK, sI, sM, a.A ? a.A + sb : nullptr, tid, wv, r, g, [] {});
 
   // 6. Wp = san(A X), U = san(A (w v)); A is unit lower triangular, so row tile ti only needs
-  //    k blocks 0..ti.  Lane l's accumulator is lane l of FA(P^T) block (tj, ti); FA(Wp) goes
-  //    through the wave's transpose tile.  Wave wv owns column strips wv, wv + 4, ...: each
-  //    strip's B operands (FRAG(X^T) blocks (tj, kb)) are read once and the four row tiles'
-  //    chains (lengths 1..4) interleaved k-block-major; each tile accumulates its k blocks in
-  //    ascending order.
-  const bool want_w = a.wp_f || a.wpT_f || a.wp, want_u = a.uT_f || a.u;
-  auto store_tile = [&](int mat, int ti, int tj, const f4& acc) __attribute__((always_inline)) {
-    const float4 pv = san4(f4_to_float4(acc), clip);     // pv.e = P[16 ti + 4 g + e][16 tj + r]
-    float* rowmaj = mat ? a.u : a.wp;
-    if (rowmaj) {
-      float* o = rowmaj + tb + (size_t)(16 * ti + 4 * g) * D + 16 * tj + r;
-      o[0] = pv.x; o[D] = pv.y; o[2 * D] = pv.z; o[3 * D] = pv.w;
+  //    k blocks 0..ti.  U: lane l's accumulator is lane l of FA(U^T) block (tj, ti).  Wp: the
+  //    transposed chains (mma16_tr, the A operand X^T), whose accumulator is lane l of FA(Wp)
+  //    block (ti, tj) -- the orientation the forward scan contracts over keys.  Wave wv owns
+  //    column strips wv, wv + 4, ...: each strip's FRAG(X^T) / FRAG(Y^T) blocks (tj, kb) are
+  //    read once and the four row tiles' chains (lengths 1..4) interleaved k-block-major; each
+  //    tile accumulates its k blocks in ascending order.
+  const bool want_w = a.wp_f || a.wp, want_u = a.uT_f || a.u;
+  auto store_tile = [&](auto matc, int ti, int tj, const f4& acc) __attribute__((always_inline)) {
+    const float4 pv = san4(f4_to_float4(acc), clip);
+    if constexpr (decltype(matc)::value == 0) {
+      // pv = Wp[16 ti + r][16 tj + 4 g .. + 3]
+      if (a.wp_f) stg4(a.wp_f + tb + frag_blk(ti, tj, D) + 4 * l, pv);
+      if (a.wp) stg4(a.wp + tb + (size_t)(16 * ti + r) * D + 16 * tj + 4 * g, pv);
+    } else {
+      // pv.e = U[16 ti + 4 g + e][16 tj + r]
+      if (a.uT_f) stg4(a.uT_f + tb + frag_blk(tj, ti, T) + 4 * l, pv);
+      if (a.u) {
+        float* o = a.u + tb + (size_t)(16 * ti + 4 * g) * D + 16 * tj + r;
+        o[0] = pv.x; o[D] = pv.y; o[2 * D] = pv.z; o[3 * D] = pv.w;
+      }
     }
-    float* fT = mat ? a.uT_f : a.wpT_f;
-    if (fT) stg4(fT + tb + frag_blk(tj, ti, T) + 4 * l, pv);
-    if (mat == 0 && a.wp_f) stg4(a.wp_f + tb + frag_blk(ti, tj, D) + 4 * l, wave_transpose16(tr, pv, r, g));
   };
   // strips of four channel tiles at a time (group m): the group's B operands (blocks (tj, kb) of
   // X^T or Y^T) staged in the Akk slot, wave wv computes strip tj = 4 m + wv
-  auto products = [&](int mat, int m, const float4* opT) __attribute__((always_inline)) {
+  auto products = [&](auto matc, int m, const float4* opT) __attribute__((always_inline)) {
+    constexpr int mat = decltype(matc)::value;     // 0: Wp, 1: U (compile-time: no branch in a chain)
     {
 #pragma unroll
       for (int c = 0; c < 4; ++c) st4(sX + frag_blk(c, wv, T) + 4 * l, opT[c]);
@@ -491,10 +497,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void w
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int ti = kb; ti < 4; ++ti) mma16<DOT>(acc[ti], ld4(sI + (16 * ti + r) * LT + 16 * kb + 4 * g), xbv[kb]);
+        for (int ti = kb; ti < 4; ++ti) {
+          const float4 av = ld4(sI + (16 * ti + r) * LT + 16 * kb + 4 * g);
+          if constexpr (mat == 0) mma16_tr<DOT>(acc[ti], xbv[kb], av);
+          else mma16<DOT>(acc[ti], av, xbv[kb]);
+        }
       drain(acc[0], acc[1], acc[2], acc[3]);
 #pragma unroll
-      for (int ti = 0; ti < 4; ++ti) store_tile(mat, ti, tj, acc[ti]);
+      for (int ti = 0; ti < 4; ++ti) store_tile(matc, ti, tj, acc[ti]);
     }
   };
   // w and v of one strip group (the wave's row fragments), for Y = w v: group 0's loads go out
@@ -511,7 +521,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void w
   if (want_u) load_wv(0);
   if (want_w) {
 #pragma unroll
-    for (int m = 0; m < NKB / 4; ++m) products(0, m, xT + 4 * m);
+    for (int m = 0; m < NKB / 4; ++m) products(std::integral_constant<int, 0>{}, m, xT + 4 * m);
   }
   if (want_u) {
 #pragma unroll
@@ -520,7 +530,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void w
 #pragma unroll
       for (int c = 0; c < 4; ++c) yT[c] = wave_transpose16(tr, mul4(xw[c], xv[c]), r, g);
       if (m + 1 < NKB / 4) load_wv(m + 1);
-      products(1, m, yT);
+      products(std::integral_constant<int, 1>{}, m, yT);
     }
   }
 }

@@ -89,14 +89,14 @@ __device__ __forceinline__ size_t io_off(const C& c, int chunk) {
 }
 
 // Per-chunk outputs of the WY build.  "_f" outputs are in fragment layout (gdn2_common.hpp):
-//   wp_f FA(Wp) (T x D), wpT_f FA(Wp^T) (D x T), uT_f FA(U^T) (D x T), kg_f FA(Kg) (T x D),
-//   kgT_f FA(Kg^T) (D x T), qg_f FA(Qg) (T x D), aqk_f FA(Aqk) (T x T).  A (T x T) and gl (D)
-//   are row-major.  The plain row-major
+//   wp_f FA(Wp) (T x D), uT_f FA(U^T) (D x T), kg_f FA(Kg) (T x D), kgT_f FA(Kg^T) (D x T),
+//   qg_f FA(Qg) (T x D), aqk_f FA(Aqk) (T x T).  A (T x T) and gl (D) are row-major.  The plain
+//   row-major
 //   aqk / akk / wp / u / kg / qg are written only for the stage-level entry point.  Any
 //   pointer may be null (not written).
 struct WyFwdArgs {
   const void *q, *k, *v, *w, *b, *g;   // fp32, or bfloat16 bits for the bf16-input variant
-  float *wp_f, *wpT_f, *uT_f, *kg_f, *kgT_f, *qg_f, *aqk_f;
+  float *wp_f, *uT_f, *kg_f, *kgT_f, *qg_f, *aqk_f;
   float *A, *gl;
   float *aqk, *akk, *wp, *u, *kg, *qg;
   int n_chunks;
@@ -166,13 +166,13 @@ struct BwdPreArgs {
   Cfg cfg;
 };
 
-// Reverse state scan: reads FA(Wp^T), FA(Kg), gl, X, Y; writes dv_new as FA(dv_new) (T x D),
+// Reverse state scan: reads FA(Wp), FA(Kg), gl, X, Y; writes dv_new as FA(dv_new) (T x D),
 // dh_next as FA(dh_next) (D x D), dh0 row-major.
-// With Cfg::pair the cotangent of the damped state of each pair's second half reaches the
-// first half's Kg v_new term as eps Wp_b^T dv_new_b: added to dh there, and written per pair as
+// With Cfg::group = G > 1 the cotangent of the damping correction of each part j >= 1 reaches
+// part j - 1's Kg v_new term (EZ, Cfg::group): added to dh there, and written per part as
 // FA(ez) (D x D, the dh_next layout) for bwd_state_rc's dKg.
 struct ScanBwdArgs {
-  const float *wpT_f, *kg_f, *gl, *x_f, *y_f, *dhf;
+  const float *wp_f, *kg_f, *gl, *x_f, *y_f, *dhf;
   float *dv_new_f, *dh_next_f, *dh0, *ez_f;
   int nc, n_bh;
   Cfg cfg;

@@ -217,10 +217,12 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
       drain(hn);
       const float gmv[4] = {op.gm.x, op.gm.y, op.gm.z, op.gm.w};
       if (part < G - 1) {
-        // h_d(part + 1) = san(e^gamma h_d(part) + (1 - eps) Kg^T v_new), h_d(0) = h(0)
+        // h_d(part + 1) = san(e^gamma h_d(part) + (1 - eps) Kg^T v_new), h_d(0) = h(0); a reset
+        // byte on the next part zeroes it with the state (the rest of the big chunk then starts
+        // from zero, damped and true state alike)
         const f4 hb0 = part == 0 ? h : hdr;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) hdr[e] = state_update(hb0[e], gmv[e], ome * hn[e], clip);
+        for (int e = 0; e < 4; ++e) hdr[e] = rst_next ? 0.f : state_update(hb0[e], gmv[e], ome * hn[e], clip);
         sHd[w * WAVE + l] = f4_to_float4(hdr);   // read in the next step's window A, after its barrier
       }
 #pragma unroll
@@ -322,40 +324,51 @@ __device__ __forceinline__ float4 frag_transpose_lds(const float4* xs, int u, in
 template <int NH>
 struct BwdOps {
   float4 kg[NH];   // dv waves: FA(Kg) block (tp, kb):  Kg[16 tp + r][16 kb + 4 g .. +3]
-  float4 wpT[4];   // FA(Wp^T) block (w, u):   Wp^T[16w + r][16u + 4g .. +3]
+  float4 wr[NH];   // waves 4-7: FA(Wp) blocks (u, kt), transposed into sWT in window A
   float4 xx;       // dv waves: FA(X^T) block (slice, tp), lane lp: X = Aqk^T dO
   float4 yy;       // FA(Y^T) block (slice, w): Y = s Qg^T dO, this lane's 4 state rows
   float4 gm;       // gamma[16w + 4g .. +3]
 };
 
 // Reverse scan, chain only: the dO terms X = Aqk^T dO and Y = s Qg^T dO do not depend on dh and
-// come precomputed per chunk (bwd_pre_kernel).  D/16 waves; wave w keeps key rows 16 w .. + 15
-// of the dh slice in registers.  Per chunk, two barriers:
+// come precomputed per chunk (bwd_pre_kernel).  Eight waves; wave w < D/16 keeps key rows
+// 16 w .. + 15 of the dh slice in registers.  Per chunk, two barriers:
 //   window A  dv waves 0..3 (token tile tp = w): dv_new = san(X + Kg (dh + EZ)) over all D
 //             keys, dh read from LDS (sDH, written by every wave at the end of the previous
-//             step), the tile to LDS (sDB) and, transposed, to dv_new_f;
-//   window B  every wave: z = Wp^T dv_new (its key rows, over the chunk's tokens from sDB),
-//             dh = san(Y + e^gamma dh - z), then dh (+ the next chunk's EZ) to sDH.
-// RED: a dv wave (waves 0..3): the role is a compile-time parameter, so that each role's code
-// is straight-line and its prefetch loads unconditional.
-template <int D, int MODE, bool RED>
-__device__ __forceinline__ void scan_bwd_role(const ScanBwdArgs& a, float4* sDH, float4* sDB, float* sTr) {
-  constexpr int NW = D / 16, NVB = D / 16, NH = D / 16;
-  (void)NW;
+//             step), the tile to LDS (sDB) and, transposed, to dv_new_f; waves 4..7 (idle
+//             otherwise) transpose the chunk's FA(Wp) blocks into sWT = FA(Wp^T) (the residual
+//             keeps Wp in the orientation the forward scan contracts over keys);
+//   window B  every state wave: z = Wp^T dv_new (its key rows, over the chunk's tokens from
+//             sDB, Wp^T from sWT), dh = san(Y + e^gamma dh - z), then dh (+ the next chunk's EZ)
+//             to sDH.
+// RED: a dv wave (waves 0..3); HELP: a transposing wave (waves 4..7), which also keeps state
+// rows when D = 128.  The roles are compile-time parameters, so that each role's code is
+// straight-line and its prefetch loads unconditional.
+template <int D, int MODE, bool RED, bool HELP>
+__device__ __forceinline__ void scan_bwd_role(const ScanBwdArgs& a, float4* sDH, float4* sDB, float* sTr,
+                                              float4* sWT, float* sTrs) {
+  constexpr int NVB = D / 16, NH = D / 16;
+  constexpr bool OWN = RED || NH == 8;     // keeps key tile w of dh
   const float clip = a.cfg.clip;
   const int nc = a.nc;
   const int lin = xcd_remap(gridDim.x);
   const int vb = lin % NVB, bh = lin / NVB, c0 = 16 * vb;
   const int tid = threadIdx.x, l = lane_id(), r = l & 15, g = l >> 4, w = wave_id();
   const int tp = (tid & 255) >> 6, lp = tid & 63;
+  const int J = w & 3;                      // HELP: wave 4 + J
 
-  f4 dh;
+  f4 dh = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (OWN) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) dh[e] = a.dhf[(size_t)bh * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r];
-  sDH[w * WAVE + l] = f4_to_float4(dh);
+    for (int e = 0; e < 4; ++e) dh[e] = a.dhf[(size_t)bh * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r];
+    sDH[w * WAVE + l] = f4_to_float4(dh);
+  }
 
   // step s processes chunk nc-1-s; steps past the last are clamped to chunk 0 (loads only)
   auto chunk = [&](int s) { return (size_t)bh * nc + (s < nc ? nc - 1 - s : 0); };
+  // wave 4 + J transposes the FA(Wp) blocks m = 0 .. NH - 1 of index J NH + m: key tile
+  // (J NH + m) / 4, token tile (J NH + m) % 4
+  auto wr_blk = [&](int m) { const int i = J * NH + m; return frag_blk(i % 4, i / 4, D); };
   auto load_all = [&](BwdOps<NH>& op, int s) {
     const size_t ch = chunk(s), tb = ch * T * D;
     if constexpr (RED) {
@@ -363,10 +376,14 @@ __device__ __forceinline__ void scan_bwd_role(const ScanBwdArgs& a, float4* sDH,
       for (int kb = 0; kb < NH; ++kb) op.kg[kb] = ld4(a.kg_f + tb + frag_blk(tp, kb, D) + 4 * lp);
       op.xx = ld4(a.x_f + tb + frag_blk(vb, tp, T) + 4 * lp);
     }
+    if constexpr (HELP) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) op.wpT[i] = ld4(a.wpT_f + tb + frag_blk(w, i, T) + 4 * l);
-    op.yy = ld4(a.y_f + ch * D * D + frag_blk(vb, w, D) + 4 * l);
-    op.gm = ld4(a.gl + ch * D + 16 * w + 4 * g);
+      for (int m = 0; m < NH; ++m) op.wr[m] = ld4(a.wp_f + tb + wr_blk(m) + 4 * l);
+    }
+    if constexpr (OWN) {
+      op.yy = ld4(a.y_f + ch * D * D + frag_blk(vb, w, D) + 4 * l);
+      op.gm = ld4(a.gl + ch * D + 16 * w + 4 * g);
+    }
   };
 
   // Cfg::group = G > 1: chunk c = nc - 1 - s is part c % G of a damped big chunk, and the parts
@@ -412,57 +429,80 @@ __device__ __forceinline__ void scan_bwd_role(const ScanBwdArgs& a, float4* sDH,
       sDB[tid] = san4(add4(op.xx, f4_to_float4(acc)), clip);
       nx.xx = ld4(a.x_f + tbn + frag_blk(vb, tp, T) + 4 * lp);
     }
-    // dh entering this chunk's step (mega.py:35) as FA(dh_next) block (w, slice)
-    const float4 dhv = wave_transpose16(sTr + w * 16 * TRP, db, r, g);
-    if (carries_ez(c))
-      stg4(a.ez_f + ch * D * D + frag_blk(w, vb, D) + 4 * l, wave_transpose16(sTr + w * 16 * TRP, ez, r, g));
-    nx.yy = ld4(a.y_f + chn * D * D + frag_blk(vb, w, D) + 4 * l);
-    nx.gm = ld4(a.gl + chn * D + 16 * w + 4 * g);
+    if constexpr (HELP) {
+      float4 wt[NH];
+      wave_transpose16_n<NH>(sTrs + J * NH * 16 * TRP, op.wr, wt, r, g);
+#pragma unroll
+      for (int m = 0; m < NH; ++m) sWT[(J * NH + m) * WAVE + l] = wt[m];
+      if constexpr (!OWN) {
+#pragma unroll
+        for (int m = 0; m < NH; ++m) nx.wr[m] = ld4(a.wp_f + tbn + wr_blk(m) + 4 * l);
+      }
+    }
+    float4 dhv = db;
+    if constexpr (OWN) {
+      // dh entering this chunk's step (mega.py:35) as FA(dh_next) block (w, slice)
+      dhv = wave_transpose16(sTr + w * 16 * TRP, db, r, g);
+      if (carries_ez(c))
+        stg4(a.ez_f + ch * D * D + frag_blk(w, vb, D) + 4 * l, wave_transpose16(sTr + w * 16 * TRP, ez, r, g));
+      nx.yy = ld4(a.y_f + chn * D * D + frag_blk(vb, w, D) + 4 * l);
+      nx.gm = ld4(a.gl + chn * D + 16 * w + 4 * g);
+    }
     __syncthreads();
     // ---- window B: this wave's key rows of dh ----
-    float4 db4[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) db4[u] = sDB[u * WAVE + l];
-    f4 z = {0.f, 0.f, 0.f, 0.f};
-    if constexpr (MODE == DOT_HIGHEST) {
+    if constexpr (OWN) {
+      float4 db4[4], wpt[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        mma16<MODE>(z, op.wpT[u], db4[u]);
-        GDN2_SCHED_FENCE();
-        nx.wpT[u] = ld4(a.wpT_f + tbn + frag_blk(w, u, T) + 4 * l);
-        GDN2_SCHED_FENCE();
+        db4[u] = sDB[u * WAVE + l];
+        wpt[u] = sWT[(4 * w + u) * WAVE + l];
       }
-    } else {
+      f4 z = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (MODE == DOT_HIGHEST) {
 #pragma unroll
-      for (int u = 0; u < 4; u += 2) {
-        mma32<MODE>(z, op.wpT[u], db4[u], op.wpT[u + 1], db4[u + 1]);
-        GDN2_SCHED_FENCE();
-        nx.wpT[u] = ld4(a.wpT_f + tbn + frag_blk(w, u, T) + 4 * l);
-        nx.wpT[u + 1] = ld4(a.wpT_f + tbn + frag_blk(w, u + 1, T) + 4 * l);
-        GDN2_SCHED_FENCE();
+        for (int u = 0; u < 4; ++u) {
+          mma16<MODE>(z, wpt[u], db4[u]);
+          GDN2_SCHED_FENCE();
+          if constexpr (HELP) {
+#pragma unroll
+            for (int m = 2 * u; m < 2 * u + 2; ++m) nx.wr[m] = ld4(a.wp_f + tbn + wr_blk(m) + 4 * l);
+          }
+          GDN2_SCHED_FENCE();
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; u += 2) {
+          mma32<MODE>(z, wpt[u], db4[u], wpt[u + 1], db4[u + 1]);
+          GDN2_SCHED_FENCE();
+          if constexpr (HELP) {
+#pragma unroll
+            for (int m = 2 * u; m < 2 * u + 4; ++m) nx.wr[m] = ld4(a.wp_f + tbn + wr_blk(m) + 4 * l);
+          }
+          GDN2_SCHED_FENCE();
+        }
       }
-    }
-    float4 dvv = db;
-    if constexpr (RED) dvv = frag_transpose_lds(sDB, tp, lp);     // FA(dv_new) block (tp, slice)
-    drain(z);
-    const float gmv[4] = {op.gm.x, op.gm.y, op.gm.z, op.gm.w};
-    if (G > 1) {
-      if (part > 0)
-        ez = make_float4(fmaf(exp_nonpos(gmv[0]), ez.x, eps * z[0]), fmaf(exp_nonpos(gmv[1]), ez.y, eps * z[1]),
-                         fmaf(exp_nonpos(gmv[2]), ez.z, eps * z[2]), fmaf(exp_nonpos(gmv[3]), ez.w, eps * z[3]));
-      else
-        ez = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    const float yv[4] = {op.yy.x, op.yy.y, op.yy.z, op.yy.w};
+      float4 dvv = db;
+      if constexpr (RED) dvv = frag_transpose_lds(sDB, tp, lp);     // FA(dv_new) block (tp, slice)
+      drain(z);
+      const float gmv[4] = {op.gm.x, op.gm.y, op.gm.z, op.gm.w};
+      if (G > 1) {
+        if (part > 0)
+          ez = make_float4(fmaf(exp_nonpos(gmv[0]), ez.x, eps * z[0]), fmaf(exp_nonpos(gmv[1]), ez.y, eps * z[1]),
+                           fmaf(exp_nonpos(gmv[2]), ez.z, eps * z[2]), fmaf(exp_nonpos(gmv[3]), ez.w, eps * z[3]));
+        else
+          ez = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+      const float yv[4] = {op.yy.x, op.yy.y, op.yy.z, op.yy.w};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) dh[e] = sanitize((yv[e] + dh[e] * exp_nonpos(gmv[e])) - z[e], clip);
-    // every dv wave has read sDH (window A) before the first barrier: the next chunk's rows
-    // may overwrite it here
-    const float4 dn = f4_to_float4(dh);
-    sDH[w * WAVE + l] = carries_ez(c - 1) ? add4(dn, ez) : dn;
-    // stores last: the next step's waits for the prefetch loads above then do not also cover them
-    stg4(a.dh_next_f + ch * D * D + frag_blk(w, vb, D) + 4 * l, dhv);
-    if constexpr (RED) stg4(a.dv_new_f + tb + frag_blk(tp, vb, D) + 4 * lp, dvv);
+      for (int e = 0; e < 4; ++e) dh[e] = sanitize((yv[e] + dh[e] * exp_nonpos(gmv[e])) - z[e], clip);
+      // every dv wave has read sDH (window A) before the first barrier: the next chunk's rows
+      // may overwrite it here
+      const float4 dn = f4_to_float4(dh);
+      sDH[w * WAVE + l] = carries_ez(c - 1) ? add4(dn, ez) : dn;
+      // stores last: the next step's waits for the prefetch loads above then do not also cover them
+      stg4(a.dh_next_f + ch * D * D + frag_blk(w, vb, D) + 4 * l, dhv);
+      if constexpr (RED) stg4(a.dv_new_f + tb + frag_blk(tp, vb, D) + 4 * lp, dvv);
+    }
     __syncthreads();
   };
 
@@ -475,18 +515,22 @@ __device__ __forceinline__ void scan_bwd_role(const ScanBwdArgs& a, float4* sDH,
     step(B, s + 1, A, s + 2, std::true_type{});
   }
   if (s < nc) step(A, s, B, s + 1, std::false_type{});
+  if constexpr (OWN) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) a.dh0[(size_t)bh * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r] = dh[e];
+    for (int e = 0; e < 4; ++e) a.dh0[(size_t)bh * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r] = dh[e];
+  }
 }
 
 template <int D, int MODE>
-__global__ __launch_bounds__(D / 16 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) {
-  constexpr int NW = D / 16;
-  __shared__ float4 sDH[NW * WAVE];        // dh (+ EZ) rows of every wave, B-operand layout, [w][lane]
+__global__ __launch_bounds__(8 * WAVE) void scan_bwd_kernel(ScanBwdArgs a) {
+  constexpr int NH = D / 16;
+  __shared__ float4 sDH[NH * WAVE];        // dh (+ EZ) rows of every state wave, B-operand layout, [w][lane]
   __shared__ float4 sDB[4 * WAVE];         // dv_new tiles in B-operand layout, [u][lane]
-  __shared__ __attribute__((aligned(16))) float sTr[NW * 16 * TRP];   // per-wave transpose tiles
-  if (wave_id() < 4) scan_bwd_role<D, MODE, true>(a, sDH, sDB, sTr);
-  else scan_bwd_role<D, MODE, false>(a, sDH, sDB, sTr);
+  __shared__ __attribute__((aligned(16))) float sTr[8 * 16 * TRP];   // per-wave transpose tiles
+  __shared__ float4 sWT[NH * 4 * WAVE];    // FA(Wp^T) of the current chunk, [key tile][token tile][lane]
+  __shared__ __attribute__((aligned(16))) float sTrs[4 * NH * 16 * TRP];   // transpose tiles of waves 4-7
+  if (wave_id() < 4) scan_bwd_role<D, MODE, true, false>(a, sDH, sDB, sTr, sWT, sTrs);
+  else scan_bwd_role<D, MODE, false, true>(a, sDH, sDB, sTr, sWT, sTrs);
 }
 
 hipError_t launch_scan_fwd(int D, const ScanFwdArgs& a, hipStream_t s) {
@@ -508,7 +552,7 @@ hipError_t launch_scan_bwd(int D, const ScanBwdArgs& a, hipStream_t s) {
   dispatch_mode(a.cfg.b3_mode, [&](auto m) {
     constexpr int M = decltype(m)::value;
     if (D == 128) hipLaunchKernelGGL((scan_bwd_kernel<128, M>), dim3(a.n_bh * 8), dim3(512), 0, s, a);
-    else hipLaunchKernelGGL((scan_bwd_kernel<64, M>), dim3(a.n_bh * 4), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((scan_bwd_kernel<64, M>), dim3(a.n_bh * 4), dim3(512), 0, s, a);
     return 0;
   });
   return hipGetLastError();

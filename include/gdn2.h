@@ -15,13 +15,13 @@
  *
  * Reference interfaces replaced (paths relative to the reference repository):
  *   gdn2_fwd  : the custom_vjp forward of one segment, `_fwd` + `core_fwd`
- *               (atomic_gdn2/pipeline.py:20-36), i.e. build_scores (fwd/scores.py:90-100),
+ *               (atomic_gdn2/pipeline.py:20-36), i.e. build_scores (fwd/scores.py:87-97),
  *               wy_solve_leafbatched (fwd/solve.py:51-59) and recompute_and_scan_slim
  *               (fwd/cd_slim.py:34-51).
  *   gdn2_bwd  : the custom_vjp backward of one segment, `core_bwd` (pipeline.py:38-47),
  *               i.e. backward_mega (bwd/mega.py:61-79) before `_fin`.
  *   gdn2_wy_stage : the chunk-parallel stages alone (scores, WY inverse, W/U recompute),
- *               for stage-level checks (fwd/scores.py:90, fwd/solve.py:51, cd_slim.py:17-21).
+ *               for stage-level checks (fwd/scores.py:87, fwd/solve.py:51, cd_slim.py:17-21).
  */
 #ifndef GDN2_H_
 #define GDN2_H_
@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define GDN2_ABI_VERSION 2
+#define GDN2_ABI_VERSION 3
 
 /* Matmul precision modes (atomic_gdn2/precision.py:27-31; config.py:51-53). */
 enum { GDN2_DOT_HIGHEST = 0, GDN2_DOT_BF16X3 = 1, GDN2_DOT_DEFAULT = 2 };
@@ -66,24 +66,29 @@ typedef struct gdn2_desc {
 } gdn2_desc;
 
 /* Residual buffer written by gdn2_fwd and read by gdn2_bwd: sub-buffers at the offsets
- * reported by gdn2_residual_layout (bytes, 256-aligned), float32, per chunk:
- *   AQK   (B,H,nc, bt*bt)  gated q.k scores, FRAG(Aqk)                         (pipeline.py:25)
- *   A     (B,H,nc,bt,bt)   the WY inverse (I + (1-eps) Akk)^-1, row-major        (pipeline.py:25)
- *   HPRE  (B,H,nck, D*D)   state entering each chunk (nck = nc, state_ckpt 0 or 1) or only
- *                          the first chunk of each checkpoint block (state_ckpt = K: chunks
- *                          0, K, .., K (nc / K - 1), then the nc % K chunks left over as one
- *                          block, or as blocks of bt / 64 chunks -- single chunks without
- *                          damping -- when those are at most two), FRAG(h_pre^T)  (cd_slim.py:22)
- *   VNEW  (B,H,nc, D*bt)   v_new of each chunk, FRAG(v_new^T)                    (cd_slim.py:23)
- *   WPT   (B,H,nc, D*bt)   W = A (b k e^gc), FRAG(W^T)                           (cd_slim.py:17)
- *   KG    (B,H,nc, bt*D)   gated k, FRAG(Kg)                                     (cd_slim.py:20)
- *   QG    (B,H,nc, bt*D)   gated q, FRAG(Qg)                                     (cd_slim.py:21)
- *   GL    (B,H,nc,D)       gc of the chunk's last row                            (cd_slim.py:19)
+ * reported by gdn2_residual_layout (bytes, 256-aligned), float32.  Whatever bt is, the kernels
+ * work on parts of 64 tokens (bt = 128 / 256 is 2 / 4 consecutive parts), so every per-chunk
+ * entry below is per 64-token part: n64 = L / 64 parts per (b, h) of the segment, p = part.
+ *   AQK   (B,H,n64, 64*64)  gated q.k scores of the part, FRAG(Aqk)            (pipeline.py:25)
+ *   A     (B,H,n64,64,64)   the part's own WY inverse (I + (1-eps) Akk_pp)^-1, row-major; at
+ *                           bt = 64 the reference's A, at bt > 64 the diagonal blocks of the
+ *                           reference's bt x bt inverse (the off-diagonal blocks are carried
+ *                           by the states, gdn2_kernels.hpp Cfg::group)         (pipeline.py:25)
+ *   HPRE  (B,H,nck, D*D)    state entering each part (nck = n64, state_ckpt 0 or 1) or only
+ *                           the first part of each checkpoint block (state_ckpt = K: parts
+ *                           0, K, .., K (n64 / K - 1), then the n64 % K parts left over as one
+ *                           block, or as blocks of bt / 64 parts -- single parts without
+ *                           damping -- when those are at most two), FRAG(h_pre^T) (cd_slim.py:22)
+ *   VNEW  (B,H,n64, D*64)   v_new of each part, FRAG(v_new^T)                  (cd_slim.py:23)
+ *   WP    (B,H,n64, 64*D)   W = A (b k e^gc) of each part, FRAG(W)              (cd_slim.py:17)
+ *   KG    (B,H,n64, 64*D)   gated k, FRAG(Kg)                                   (cd_slim.py:20)
+ *   QG    (B,H,n64, 64*D)   gated q, FRAG(Qg)                                   (cd_slim.py:21)
+ *   GL    (B,H,n64,D)       gc (within the part) of the part's last row         (cd_slim.py:19)
  * FRAG(M) of an R x C matrix M is the MFMA fragment order the kernels load with one
  * coalesced float4 per lane: 16x16 blocks in row-major block order (C/16 blocks per block
  * row, 256 floats each); inside a block, floats [4 l, 4 l + 4) with l = r + 16 c hold
  * M[16 bi + r][16 bj + 4 c + e], e = 0..3 (r = 0..15, c = 0..3). */
-enum { GDN2_RES_AQK = 0, GDN2_RES_A, GDN2_RES_HPRE, GDN2_RES_VNEW, GDN2_RES_WPT, GDN2_RES_KG,
+enum { GDN2_RES_AQK = 0, GDN2_RES_A, GDN2_RES_HPRE, GDN2_RES_VNEW, GDN2_RES_WP, GDN2_RES_KG,
        GDN2_RES_QG, GDN2_RES_GL, GDN2_RES_COUNT };
 
 int gdn2_abi_version(void);
@@ -118,8 +123,11 @@ int gdn2_fwd_bf16(const gdn2_desc* d, const uint16_t* q, const uint16_t* k, cons
  * state entering that chunk is zero (its first token starts a new document; at chunk 0 it
  * replaces h0).  Replaces the chunkwise part of chunk_forward_inference in the reference's
  * inference module (notebooks/gdn2_v031_stage2_tpu.ipynb, cell 1, INFERENCE_V031: the
- * _cd_inference_body call with per-row segment resets).  With bt = 128 only even 64-token
- * chunks may carry a reset.  workspace holds gdn2_fwd_workspace_bytes(d, 0). */
+ * _cd_inference_body call with per-row segment resets).  At bt = 128 / 256 with wy_eps > 0 a
+ * reset on a 64-token part that does not start a bt chunk zeroes the damped state with the
+ * true one, so the remaining parts of that chunk run as a damped chunk of their own (the
+ * reference's inference API places document starts only at bt boundaries, and
+ * atomic_gdn2.inference flags only those).  workspace holds gdn2_fwd_workspace_bytes(d, 0). */
 int gdn2_fwd_reset(const gdn2_desc* d, int in_dtype, const void* q, const void* k, const void* v,
                    const void* w, const void* b, const void* g, const float* h0,
                    const uint8_t* chunk_reset, float* o, float* h_final, void* workspace,

@@ -1,7 +1,7 @@
 """GPU checks at the benchmark configurations' full sizes, and the failure path.
 
-* config 3 at B4 H6 L4096 (two internal segments): every output and gradient finite, one
-  (batch, head) sequence against the float64 oracle run on it alone;
+* config 3 at B4 H6 L4096 (two internal segments), B4 H2 L4096 and B4 H4 L2048: every output
+  and gradient finite, one (batch, head) sequence against the float64 oracle run on it alone;
 * config 4 at B8 H16 L32768 D128 with bf16 inputs as 8 calls of 4096 tokens (h0 = previous
   h_final): bit-equal to one call over the whole length, finite, one sequence against the
   float64 token recurrence;
@@ -31,18 +31,23 @@ def _need_gpu():
         pytest.skip("no ROCm GPU")
 
 
-def test_config3_b4_h6_l4096_full_size():
+@pytest.mark.parametrize("H,L", [(6, 4096), (2, 4096), (4, 2048)])
+def test_config3_cells_full_size(H, L):
+    """Config 3's cells at their own shapes (B4 D128; L4096 is two internal segments; the grids
+    of the scans, 8 H workgroups per batch row, and of the chunk-parallel kernels differ by
+    cell): every output and gradient finite, one (batch, head) sequence against the float64
+    oracle run on it alone."""
     from atomic_gdn2.synthetic import make_inputs_np
-    banner("config3 B4 H6 L4096 full size")
-    arrs, scale = make_inputs_np(4, 6, 4096, 128, seed=3)
+    banner(f"config3 B4 H{H} L{L} full size")
+    arrs, scale = make_inputs_np(4, H, L, 128, seed=3)
     cfg = base_cfg()
     hip = hip_grad(cfg, scale, arrs)
     for n, t in hip.items():
         assert torch.isfinite(t).all(), n
-    bi, hi = 2, 4
+    bi, hi = 2, H - 1
     ref = oracle_grad(cfg, scale, [a[bi:bi + 1, hi:hi + 1] for a in arrs])
     errs = {n: rel_l2(hip[n][bi:bi + 1, hi:hi + 1], ref[n]) for n in ("o", "h_final") + NAMES}
-    banner(f"config3 L4096 slice {(bi, hi)} rel-L2 {errs}")
+    banner(f"config3 H{H} L{L} slice {(bi, hi)} rel-L2 {errs}")
     assert max(errs.values()) <= GATE, errs
 
 

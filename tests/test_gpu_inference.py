@@ -376,3 +376,75 @@ def test_prefill_pairs_with_resets_across_flag_blocks():
     ro, rh = O.chunk_forward_inference_ref(*(x[:, :1].double() for x in xs), scale, O.OracleCfg.from_cfg(cfg),
                                            segment_ids=ids)
     assert rel_l2(o[:, :1], ro) <= GATE and rel_l2(h[:, :1], rh) <= GATE
+
+
+@pytest.mark.parametrize("bt,D", [(256, 64), (256, 128), (128, 128)])
+def test_reset_on_a_non_leading_part_of_a_damped_chunk(bt, D):
+    """gdn2_fwd_reset at bt = 128 / 256 with wy_eps > 0 and reset bytes on 64-token parts that
+    do not start a big chunk: the true and the damped state are both zero entering that part, so
+    the remaining parts of the big chunk run as a damped chunk of their own and the following big
+    chunks as usual.  Checked against the float64 oracle run piecewise with those chunk sizes
+    (parts before a reset are the first parts of their big chunk, whose outputs do not depend on
+    the parts after them)."""
+    from atomic_gdn2 import _lib
+    import ctypes
+    O = _oracle()
+    eps, B, H, nbig = 0.02, 1, 2, 5
+    G = bt // 64
+    L = bt * nbig
+    banner(f"damped non-leading reset bt={bt} D={D}")
+    xs, scale = _inputs(B, H, L, D, seed=23)
+    # row (0, 0): resets at part G/2 of big chunks 1 and 3 (bt 256: parts 2; bt 128: parts 1)
+    jr = G // 2
+    parts = [G * 1 + jr, G * 3 + jr]
+    rst = torch.zeros(B * H, L // 64, dtype=torch.uint8)
+    rst[0, parts] = 1
+    cfg = _cfg(bt, wy_eps=eps)
+    desc = _lib.make_desc(cfg, B, H, L, D, scale)
+    L_ = _lib.lib()
+    xd = [x.cuda() for x in xs]
+    o = torch.empty(B, H, L, D, device="cuda")
+    hf = torch.empty(B, H, D, D, device="cuda")
+    ws = torch.empty(L_.gdn2_fwd_workspace_bytes(ctypes.byref(desc), 0), dtype=torch.uint8, device="cuda")
+    _lib.check(L_.gdn2_fwd_reset(ctypes.byref(desc), 0, *map(_lib.ptr, xd), None, _lib.ptr(rst.cuda()),
+                                 _lib.ptr(o), _lib.ptr(hf), _lib.ptr(ws), _lib.stream_handle()), "gdn2_fwd_reset")
+    torch.cuda.synchronize()
+    oc = O.OracleCfg.from_cfg(cfg)
+
+    def run(seq, t0, t1, chunk, h0):
+        c = oc.with_(bt=chunk, score_bs=min(oc.score_bs, chunk), mb=min(oc.mb, chunk))
+        return O.forward_ref(*(x[:, seq:seq + 1, t0:t1].double() for x in xs), scale, h0, c)
+
+    # row (0, 0): pieces between the resets, each a run of whole (possibly shortened) chunks
+    cut = [p * 64 for p in parts]
+    pieces = []          # (t0, t1, chunk, fresh)
+    t = 0
+    for c in cut:
+        big0 = (c // bt) * bt
+        if big0 > t:
+            pieces.append((t, big0, bt, False))
+        pieces.append((big0, c, c - big0, False))       # the parts before the reset
+        t = c
+        pieces.append((t, big0 + bt, big0 + bt - t, True))   # the remaining parts, from zero
+        t = big0 + bt
+    pieces.append((t, L, bt, False))
+    h = None
+    outs = []
+    for t0, t1, chunk, fresh in pieces:
+        if fresh:
+            h = None
+        ro, rh = run(0, t0, t1, chunk, h)
+        outs.append(ro)
+        h = rh
+    ro0 = torch.cat(outs, dim=2)
+    e0 = rel_l2(o[:, :1], ro0)
+    eh0 = rel_l2(hf[:, :1], h)
+    # row (0, 1): no resets
+    ro1, rh1 = run(1, 0, L, bt, None)
+    e1, eh1 = rel_l2(o[:, 1:], ro1), rel_l2(hf[:, 1:], rh1)
+    banner(f"  rel-L2 o {e0:.2e} h {eh0:.2e} | no-reset row o {e1:.2e} h {eh1:.2e}")
+    assert max(e0, eh0, e1, eh1) <= GATE
+    # the part right after each reset, chunk by chunk (an error there hides in the aggregate)
+    for p in parts:
+        sl = slice(64 * p, 64 * (p + 1))
+        assert rel_l2(o[:, :1, sl], ro0[:, :, sl]) <= 1e-4, p

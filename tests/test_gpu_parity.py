@@ -104,7 +104,7 @@ def base_cfg(**kw):
 def test_library_is_the_in_tree_hip_build():
     from atomic_gdn2 import _lib
     L = _lib.lib()
-    assert L.gdn2_abi_version() == 2
+    assert L.gdn2_abi_version() == 3
     repo = Path(__file__).resolve().parents[1]
     assert Path(L._name).resolve().is_relative_to(repo), L._name
     maps = Path("/proc/self/maps").read_text()

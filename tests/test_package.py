@@ -53,7 +53,7 @@ def test_library_exports_every_header_symbol():
     assert len(names) >= 10, names
     missing = [n for n in names if not hasattr(L, n)]
     assert not missing, missing
-    assert L.gdn2_abi_version() == 2
+    assert L.gdn2_abi_version() == 3
 
 
 def test_descriptor_struct_matches_header():
@@ -83,8 +83,9 @@ def test_residual_layout_and_workspaces():
         assert nxt - o >= s
     L = _lib.lib()
     d = _desc()
-    # [Wp | U^T | Kg^T], without a residual also [Qg | Aqk | gl] (h_pre / v_new never leave the scan)
-    assert L.gdn2_fwd_workspace_bytes(ctypes.byref(d), 1) == N * 3 * 64 * 128 * 4
+    # [U^T | Kg^T], without a residual also [Wp | Qg | Aqk | gl] (with one they are residuals;
+    # h_pre / v_new never leave the scan)
+    assert L.gdn2_fwd_workspace_bytes(ctypes.byref(d), 1) == N * 2 * 64 * 128 * 4
     assert L.gdn2_fwd_workspace_bytes(ctypes.byref(d), 0) == N * (4 * 64 * 128 + 64 * 64 + 128) * 4
     assert L.gdn2_bwd_workspace_bytes(ctypes.byref(d)) >= N * (4 * 64 * 128 + 128 * 128 + 128) * 4
 
@@ -204,11 +205,14 @@ def test_fragment_layout_roundtrip_and_definition():
     off = lambda i, j, C: ((i // 16) * (C // 16) + j // 16) * 256 + 4 * ((i % 16) + 16 * ((j % 16) // 4)) + j % 4
     for i, j in [(0, 0), (5, 7), (17, 33), (63, 127), (40, 90)]:
         assert f[1, 2, off(i, j, 128)] == m[1, 2, i, j]
-    # residual decoding: a transposed fragment sub-buffer comes back as the named quantity
+    # residual decoding: a fragment sub-buffer comes back as the named quantity, a transposed
+    # one (v_new is stored as FRAG(v_new^T)) un-transposed
     B, H, nc, T, D = 1, 2, 3, 64, 128
     wp = torch.randn(B, H, nc, T, D)
-    flat = to_frag(wp.transpose(-1, -2).contiguous()).reshape(-1)
-    assert torch.equal(_lib.decode_residual("wpT", flat, B, H, nc, T, D), wp)
+    assert torch.equal(_lib.decode_residual("wp", to_frag(wp).reshape(-1), B, H, nc, T, D), wp)
+    vn = torch.randn(B, H, nc, T, D)
+    flat = to_frag(vn.transpose(-1, -2).contiguous()).reshape(-1)
+    assert torch.equal(_lib.decode_residual("v_new", flat, B, H, nc, T, D), vn)
 
 
 def test_golden_fixture_inputs_are_reproduced():
