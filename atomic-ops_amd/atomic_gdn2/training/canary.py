@@ -1,6 +1,6 @@
 """Runtime canary: BTL scores against exact (lean) scores on a sample of chunks (reference
 ``atomic_gdn2/training/canary.py:12-23``).  Both score sets come from the HIP kernels
-(``gdn2_wy_stage`` with ``diag='btl'`` and ``diag='lean'``); the alarm fires when their Akk
+(``build_scores`` with ``diag='btl'`` and ``diag='lean'`` on the same gc); the alarm fires when their Akk
 differ by more than ``thresh`` in relative L2, which flags a gate whose half span has left the
 BTL factorisation's domain."""
 from __future__ import annotations
@@ -29,7 +29,7 @@ def btl_vs_lean_canary(cfg, q=None, k=None, b=None, g=None, D=64, g_level=None, 
         g = torch.full(sh, -float(g_level), dtype=torch.float32, device=device)
     gc = torch.cumsum(g.float(), dim=-2)
     scale = 1.0 / np.sqrt(q.shape[-1])
-    _, Ab = build_scores(q, k, b, g, scale, cfg.with_(diag="btl"))
-    _, Al = build_scores(q, k, b, g, scale, cfg.with_(diag="lean"))
+    _, Ab = build_scores(q, k, b, gc, scale, cfg.with_(diag="btl"))
+    _, Al = build_scores(q, k, b, gc, scale, cfg.with_(diag="lean"))
     err = _rel(Ab, Al)
     return dict(rel_err=err, half_span=float(half_span_max(gc, cfg.bs2)), alarm=err > thresh)

@@ -37,12 +37,20 @@ def _operator(config: KernelConfig, scale: float):
 
 
 def operator_cfg(config: KernelConfig):
-    """The operator configuration that stands in for ``config`` (see the module docstring)."""
+    """The operator configuration that stands in for ``config`` (see the module docstring).
+
+    Scores: the legacy Kernel A forms every score pair exactly, exp(clip(gc_i - gc_j, -20, 20))
+    per channel over the whole chunk (atomic_ops/gdn2_fwd.py:60-65, and the same in its off-TPU
+    reference, reference.py:73-74), so the operator runs the exact ('lean') diagonal with
+    diff_clip 20 on the largest diagonal block the kernels take: bs2 = 64.  At bt = 64 that is
+    the whole chunk, as in the legacy kernel; at bt = 128 / 256 the pairs in different 64-token
+    parts are carried by the state, exactly and without the clip (the two differ only where
+    gc_i - gc_j < -20 across parts, i.e. for pair weights below e^-20)."""
     bt = config.bt if kernels_support(config.bt, config.wy_eps) else 64
     eps = config.wy_eps if bt == config.bt else 0.0
-    return make_cfg(bt=bt, bc=bt // 2, score_bs=bt, bs2=32, mb=min(config.mb, bt), diag="btl",
-                    clip=config.clip, wy_eps=eps, dot_mode="highest", solve_dot_mode="highest",
-                    b3_dot_mode="highest")
+    return make_cfg(bt=bt, bc=bt // 2, score_bs=bt, bs2=64, mb=min(config.mb, bt),
+                    diag="lean", diff_clip=20.0, clip=config.clip, wy_eps=eps, dot_mode="highest",
+                    solve_dot_mode="highest", b3_dot_mode="highest")
 
 
 def _run(q, k, v, w, b, g, scale, h0, config):

@@ -491,6 +491,27 @@ int gdn2_wy_stage(const gdn2_desc* d, const float* q, const float* k, const floa
   return GDN2_OK;
 }
 
+int gdn2_scores(const gdn2_desc* d, const float* q, const float* k, const float* b, const float* gc, float* aqk,
+                float* akk, void* stream) {
+  int st = validate(d);
+  if (st) return st;
+  if (d->bt != gdn2::T)
+    return fail(GDN2_ERR_UNSUPPORTED, "gdn2_scores reports chunks of 64 tokens: use bt == 64");
+  if (!q || !k || !b || !gc || !aqk || !akk) return fail(GDN2_ERR_INVALID, "null tensor pointer");
+  const Dims x = dims(d);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  gdn2::WyFwdArgs wa{};
+  // v and w are not read (no U is requested); they point at q so that no pointer is null
+  wa.q = q; wa.k = k; wa.v = q; wa.w = q; wa.b = b; wa.g = gc;
+  wa.g_is_gc = 1;
+  wa.aqk = aqk; wa.akk = akk;
+  wa.n_chunks = (int)x.n_chunks;
+  wa.cfg = make_cfg(d);
+  hipError_t e = timed(0, s, [&] { return gdn2::launch_wy_fwd(d->D, wa, s); });
+  if (e != hipSuccess) return hip_fail(e, "wy_fwd launch");
+  return GDN2_OK;
+}
+
 int gdn2_debug_gemm(int mode, const float* A, const float* B, float* C, int M, int N, int K, void* stream) {
   if (mode < 0 || mode > 2) return fail(GDN2_ERR_INVALID, "unknown dot mode");
   if (M <= 0 || N <= 0 || K <= 0 || M > 64 || N > 64 || K > 128 || M % 16 || N % 16 || K % 16)

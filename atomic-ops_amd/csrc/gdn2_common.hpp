@@ -562,6 +562,16 @@ struct CumsumPass {
         for (int i = 0; i < RUN; ++i) x[m][i] = in_ld4(g + (seg(m) * RUN + i) * D + c0 + 4 * col(m));
       }
   }
+  // the loaded rows are gc already (the caller's in-chunk cumsum): store them as they are
+  __device__ __forceinline__ void store_as_is(float* sGf) {
+#pragma unroll
+    for (int m = 0; m < NV; ++m)
+      if (active(m)) {
+#pragma unroll
+        for (int i = 0; i < RUN; ++i) st4(sGf + frag_off(seg(m) * RUN + i, 4 * col(m), 4 * NQP), x[m][i]);
+      }
+    __syncthreads();
+  }
   __device__ __forceinline__ void run(float* sGf, float4* sTot) {
 #pragma unroll
     for (int m = 0; m < NV; ++m)

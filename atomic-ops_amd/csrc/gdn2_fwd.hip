@@ -342,7 +342,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void w
 #pragma unroll
   for (int p = 0; p < NPASS; ++p) {
     // 1. gc = cumsum(g) inside the chunk, this pass's columns (fragment layout)
-    cs.run(sG, reinterpret_cast<float4*>(sQ));
+    if (a.g_is_gc) cs.store_as_is(sG);
+    else cs.run(sG, reinterpret_cast<float4*>(sQ));
 
     // 2. gated fragments (cd_slim.py:17-21): Kg = san(k e^{min(gl - gc, 0)}) as FRAG(Kg) and,
     //    through the wave's transpose tile, FRAG(Kg^T); Qg = san(q e^{min(gc, 0)}); X = b k e^{min(gc, 0)}

@@ -100,6 +100,7 @@ struct WyFwdArgs {
   float *A, *gl;
   float *aqk, *akk, *wp, *u, *kg, *qg;
   int n_chunks;
+  int g_is_gc;     // nonzero: g holds the in-chunk cumulative sum gc itself (the stage entry points)
   Cfg cfg;
 };
 

@@ -22,6 +22,7 @@
  *               i.e. backward_mega (bwd/mega.py:61-79) before `_fin`.
  *   gdn2_wy_stage : the chunk-parallel stages alone (scores, WY inverse, W/U recompute),
  *               for stage-level checks (fwd/scores.py:87, fwd/solve.py:51, cd_slim.py:17-21).
+ *   gdn2_scores : build_scores itself, gc given (fwd/scores.py:87-97).
  */
 #ifndef GDN2_H_
 #define GDN2_H_
@@ -190,6 +191,14 @@ int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v,
 int gdn2_wy_stage(const gdn2_desc* d, const float* q, const float* k, const float* v,
                   const float* w, const float* b, const float* g, float* aqk, float* akk,
                   float* A, float* wp, float* u, float* kg, float* qg, float* gl, void* stream);
+
+/* Kernel A alone with the reference's signature: build_scores(q, k, b, gc, scale, cfg) ->
+ * (Aqk, Akk) (atomic_gdn2/fwd/scores.py:87-97).  gc (B,H,L,D) is the caller's in-chunk
+ * cumulative gate (cumsum of g within each 64-token chunk), used as given; aqk, akk
+ * (B,H,nc,64,64) row-major, masked and sanitized, akk before the (1 - wy_eps) factor.
+ * bt == 64 only (the scores of a chunk of 64 tokens). */
+int gdn2_scores(const gdn2_desc* d, const float* q, const float* k, const float* b, const float* gc,
+                float* aqk, float* akk, void* stream);
 
 /* Diagnostics: C[M,N] = A[M,K] B[K,N] (row-major float32) through the kernels' MFMA tile
  * routine in the given dot mode.  M, N <= 64, K <= 128, all multiples of 16. */

@@ -60,7 +60,8 @@ def _akk(cfg, c):
                for s in (0.3, 0.3, 0.5))
     b = b.abs()
     g = torch.full((1, 1, 1, T, D), -c, device="cuda")
-    return build_scores(q, k, b, g, 1 / 8.0, cfg)[1], torch.cumsum(g, dim=-2)
+    gc = torch.cumsum(g, dim=-2)
+    return build_scores(q, k, b, gc, 1 / 8.0, cfg)[1], gc
 
 
 @pytest.mark.gpu

@@ -198,6 +198,32 @@ def test_wy_stage_config1(cfg1):
     assert float((M @ A.double() - I).abs().max()) < 1e-4
 
 
+@pytest.mark.parametrize("diag,bs2", [("btl", 32), ("btl", 16), ("lean", 32)])
+def test_build_scores_takes_gc(cfg1, diag, bs2):
+    """stages.build_scores(q, k, b, gc, scale, cfg), the reference's Kernel A signature
+    (fwd/scores.py:87-97): gc is the caller's in-chunk cumulative gate, used as given.  Against
+    the kernel-semantics oracle on the same gc (float64), and equal to the scores of
+    gdn2_wy_stage, which forms gc from g itself (same in-chunk cumsum up to its rounding).
+    Passing the raw g where gc belongs gives different scores (the argument is gc, not g)."""
+    from atomic_gdn2.stages import build_scores, wy_stage
+    from oracle import gdn2_oracle as O
+    arrs, scale, _ = cfg1
+    banner(f"build_scores(gc) {diag} bs2={bs2}")
+    cfg = base_cfg().with_(diag=diag, bs2=bs2)
+    q, k, v, w, b, g = (torch.from_numpy(a) for a in arrs)
+    ch = lambda t: O.to_chunks(t, 64)
+    gc = torch.cumsum(ch(g), dim=-2)                                   # float32, the caller's
+    aqk, akk = build_scores(*(x.cuda() for x in (ch(q), ch(k), ch(b), gc)), scale, cfg)
+    ra, rk = O.btl_scores(*(x.double() for x in (ch(q), ch(k), ch(b), gc)), scale, O.OracleCfg.from_cfg(cfg))
+    ea, ek = rel_l2(aqk, ra), rel_l2(akk, rk)
+    banner(f"  vs oracle on the same gc: aqk {ea:.2e} akk {ek:.2e}")
+    assert ea < 1e-5 and ek < 1e-5
+    st = wy_stage(*(x.cuda() for x in (q, k, v, w, b, g)), scale, cfg)
+    assert rel_l2(st["aqk"], aqk) < 1e-5 and rel_l2(st["akk"], akk) < 1e-5
+    _, akk_g = build_scores(*(x.cuda() for x in (ch(q), ch(k), ch(b), ch(g))), scale, cfg)
+    assert rel_l2(akk_g, akk) > 1e-3
+
+
 def test_forward_residuals_config1(cfg1):
     """gdn2_fwd through the C ABI: every residual sub-buffer and o / h_final per chunk vs
     the kernel-semantics oracle (localises a forward error to a stage and a chunk)."""

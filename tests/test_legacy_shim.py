@@ -96,10 +96,47 @@ def test_legacy_entry_points_match_oracle(preset):
     o2, hf2 = atomic_ops.gdn2_forward_trainable(*xs, scale, config=config)
     ((o2 * o2).sum() + (hf2 * hf2).sum()).backward()
     ref = grad_ref(q, k, v, w, b, g, scale, None,
-                   OracleCfg(bt=config.bt, score_bs=config.bt, bs2=32, mb=config.mb, wy_eps=config.wy_eps,
-                             clip=config.clip))
+                   OracleCfg(bt=config.bt, score_bs=config.bt, bs2=64, mb=config.mb, wy_eps=config.wy_eps,
+                             clip=config.clip, diag="lean", diff_clip=20.0))
     for x, n in zip(xs, ("dq", "dk", "dv", "dw", "db", "dg")):
         assert rel_l2(x.grad, sw(ref[n])) < 2e-3, n
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("g_rate", [8.0, 30.0])
+def test_legacy_strong_decay_beyond_the_btl_span(g_rate):
+    """Gates far beyond BTL's span (|g| = 8 and 30 per token: half spans 128 and 480 over a
+    32-token block, past the 88 at which the BTL legs overflow): the legacy operator forms every
+    pair exactly with its decay clipped at e^-20 (atomic_ops/gdn2_fwd.py:60-65), and so does the
+    shim (the exact diagonal over the whole 64-token chunk).  Forward against the float64 oracle
+    with the same exact scores; the BTL operator on the same inputs does not match it."""
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm GPU")
+    import sys
+    from pathlib import Path
+    sys.path.insert(0, str(Path(__file__).resolve().parents[1]))
+    from atomic_gdn2 import make_blr_trainable
+    from atomic_ops.fallback import operator_cfg
+    from oracle.gdn2_oracle import OracleCfg, forward_ref
+    from conftest import mk_inputs
+    print(f"[gpu-test] legacy strong decay g={g_rate}", flush=True)
+    config = KernelConfig(bt=64, bc=32, mb=8, clip=1e4, wy_eps=0.0)
+    arrs = mk_inputs(1, 256, 2, 128, seed=5, g=1.0)                 # (B, L, H, D)
+    arrs = arrs[:5] + (np.full_like(arrs[5], -g_rate),)
+    scale = 128 ** -0.5
+    dev = [torch.from_numpy(a).cuda() for a in arrs]
+    o, hf = atomic_ops.gdn2_forward(*dev, scale, config=config)
+    sw = lambda x: x.transpose(1, 2)
+    t = [sw(torch.from_numpy(a).double()) for a in arrs]
+    oc = OracleCfg(bt=64, score_bs=64, bs2=64, mb=8, wy_eps=0.0, diag="lean", diff_clip=20.0)
+    ro, rh = forward_ref(*t, scale, None, oc)
+    eo, eh = rel_l2(sw(o), ro), rel_l2(hf, rh)
+    print(f"[gpu-test]   rel-L2 o {eo:.2e} h_final {eh:.2e}", flush=True)
+    assert torch.isfinite(o).all() and eo < 2e-3 and eh < 2e-3
+    cb = operator_cfg(config).with_(diag="btl", bs2=32)
+    with torch.no_grad():
+        ob, _ = make_blr_trainable(cb, scale)(*(sw(x) for x in dev))
+    assert rel_l2(ob, ro) > 1e-2
 
 
 @pytest.mark.gpu
@@ -127,6 +164,8 @@ def test_operator_cfg_follows_the_reference_dispatch():
         c = operator_cfg(preset)
         assert (c.bt, c.wy_eps, c.clip) == (preset.bt, preset.wy_eps, preset.clip)
         assert c.mb == min(preset.mb, preset.bt)
+        # the legacy Kernel A's exact pairs (gdn2_fwd.py:60-65): the exact diagonal, clip 20
+        assert (c.diag, c.bs2, c.diff_clip) == ("lean", 64, 20.0)
     c = operator_cfg(KernelConfig(bt=512, bc=256, mb=8, clip=1e4, wy_eps=1e-3))
     assert c.bt == 64 and c.wy_eps == 0.0
     c = operator_cfg(KernelConfig(bt=64, bc=32, mb=8, clip=1e4, wy_eps=1e-3))
