@@ -25,7 +25,7 @@ RES_STORAGE = {"aqk": ("T", "T", True, False), "A": ("T", "T", False, False),
                "wp": ("T", "D", True, False), "kg": ("T", "D", True, False),
                "qg": ("T", "D", True, False), "gl": (None, "D", False, False)}
 KERNEL_NAMES = ("wy_fwd", "scan_fwd", "scan_bwd", "bwd_state", "bwd_wy", "out_fwd", "bwd_pre", "bwd_state_rc",
-                "decode")
+                "decode", "anchors")
 ABI_VERSION = 3
 STATUS = {0: "ok", 1: "invalid argument", 2: "unsupported configuration", 3: "HIP error"}
 

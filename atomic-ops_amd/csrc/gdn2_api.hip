@@ -42,10 +42,8 @@ int validate(const gdn2_desc* d) {
   // size is the 64-token operator
   if (d->bt != gdn2::T && d->bt != 2 * gdn2::T && d->bt != 4 * gdn2::T)
     return fail(GDN2_ERR_UNSUPPORTED, "this build supports bt in {64, 128, 256}");
-  if (d->bt > gdn2::T && d->bs2 > gdn2::T)
-    return fail(GDN2_ERR_UNSUPPORTED, "this build supports bs2 <= 64 at bt >= 128");
   if (d->D != 64 && d->D != 128) return fail(GDN2_ERR_UNSUPPORTED, "this build supports D in {64, 128}");
-  if (d->bs2 < 16) return fail(GDN2_ERR_UNSUPPORTED, "this build supports bs2 >= 16");
+  if (d->bs2 < 8) return fail(GDN2_ERR_UNSUPPORTED, "this build supports bs2 >= 8");
   if (d->seq_ld != 0 && d->seq_ld < d->L) return fail(GDN2_ERR_INVALID, "seq_ld must be 0 or >= L");
   if (d->state_ckpt < 0) return fail(GDN2_ERR_INVALID, "state_ckpt must be >= 0");
   // the score pieces partition the lower triangle, so every 16 x 16 tile on or below the
@@ -75,9 +73,11 @@ int eff_ckpt(const gdn2_desc* d) {
   return (G > 1 && k % G) ? k + (G - k % G) : k;
 }
 
-// Pieces of the two-level block-local rescaling (fwd/scores.py:42-75): for each row block
+// Pieces of the two-level block-local rescaling (fwd/scores.py:39-72): for each row block
 // [q0, q0+bs2) of outer block p0: its diagonal block, the level-2 part [p0, q0) with anchor
-// q0 and the level-1 part [0, p0) with anchor p0, cut into squares of side min(bs2, 32).
+// q0 and the level-1 part [0, p0) with anchor p0, cut into squares of side min(bs2, 32).  A
+// diagonal block wider than the part (bs2 > T) covers the whole part: kind-2 pieces, whose
+// block ends come from the anchor buffer.
 void make_pieces(int T, int sbs, int bs2, gdn2::PieceList* out) {
   const int P = bs2 < 32 ? bs2 : 32;
   int n = 0;
@@ -86,6 +86,12 @@ void make_pieces(int T, int sbs, int bs2, gdn2::PieceList* out) {
     p.row0 = (int8_t)r; p.col0 = (int8_t)c; p.P = (int8_t)P; p.kind = (int8_t)kind;
     p.anchor = (int8_t)anchor; p.s0 = (int8_t)s0; p.s1 = (int8_t)s1; p.pad = 0;
   };
+  if (bs2 > T) {
+    for (int r = 0; r < T; r += P)
+      for (int c = 0; c <= r; c += P) add(r, c, 2, 0, 0, 0);
+    out->n = n;
+    return;
+  }
   for (int q0 = 0; q0 < T; q0 += bs2) {
     const int q1 = q0 + bs2, p0 = (q0 / sbs) * sbs;
     for (int r = q0; r < q1; r += P)
@@ -117,6 +123,8 @@ gdn2::Cfg make_cfg(const gdn2_desc* d) {
   // geometry that lie inside a half are the 64 geometry's with the outer block capped at 64
   // (the pieces crossing the halves are carried by the state, see Cfg::group)
   make_pieces(gdn2::T, d->score_bs < gdn2::T ? d->score_bs : gdn2::T, d->bs2, &c.pieces);
+  // (the kernels cut the chunk into 64-token parts; score_bs and bs2 above 64 act through the
+  // anchors of the kind-2 pieces and, between parts, through the state)
   for (int t = 0; t < 16; ++t) {
     const int ti = t / 4, tj = t % 4;
     c.tile_piece[t] = -1;
@@ -193,8 +201,26 @@ hipError_t timed(int kid, hipStream_t s, F&& launch) {
   return e;
 }
 
+// The anchor buffer of the kind-2 pieces (bs2 > 64): two rows of D floats per 64-token part.
+size_t anchor_bytes(const gdn2_desc* d) {
+  return d->bs2 > gdn2::T ? align_up((size_t)d->B * d->H * (d->L / gdn2::T) * 2 * d->D * 4) : 0;
+}
 int hip_fail(hipError_t e, const char* what) {
   return fail(GDN2_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// Fills it (anchor_kernel) from the raw gate g into buf; *anc = buf, or null when no piece is of
+// kind 2 or the pieces are formed exactly (nothing is launched then).
+int fill_anchors(const gdn2_desc* d, const gdn2::Cfg& cfg, const void* g, bool bf16, void* buf, hipStream_t s,
+                 const float** anc) {
+  *anc = nullptr;
+  // (the lean diagonal forms its kind-2 pieces exactly, without anchors)
+  if (d->bs2 <= gdn2::T || d->diag == GDN2_DIAG_LEAN) return GDN2_OK;
+  gdn2::AnchorArgs aa{g, static_cast<float*>(buf), (int)((size_t)d->B * d->H * (d->L / gdn2::T)), d->bs2 / gdn2::T, cfg};
+  const hipError_t e = timed(9, s, [&] { return gdn2::launch_anchors(d->D, aa, s, bf16); });
+  if (e != hipSuccess) return hip_fail(e, "anchors launch");
+  *anc = aa.anc;
+  return GDN2_OK;
 }
 
 template <class T>
@@ -218,23 +244,24 @@ int gdn2_residual_layout(const gdn2_desc* d, size_t offsets[GDN2_RES_COUNT], siz
   return GDN2_OK;
 }
 
-// forward workspace (fragment layouts): [U^T | Kg^T], and without a residual also
-// [Wp | Qg | Aqk | gl] (with a residual those live in it).
+// forward workspace (fragment layouts): [U^T | Kg^T | anchors (bs2 > 64 only)], and without a
+// residual also [Wp | Qg | Aqk | gl] (with a residual those live in it).
 size_t gdn2_fwd_workspace_bytes(const gdn2_desc* d, int with_residual) {
   if (with_residual ? validate_residual(d) : validate(d)) return 0;
   const Dims x = dims(d);
-  size_t n = 2 * align_up(x.n_chunks * x.tD * 4);
+  size_t n = 2 * align_up(x.n_chunks * x.tD * 4) + anchor_bytes(d);
   if (!with_residual)
     n += 2 * align_up(x.n_chunks * x.tD * 4) + align_up(x.n_chunks * x.tT * 4) + align_up(x.n_chunks * x.D * 4);
   return n;
 }
 
-// backward workspace: [dv_new | dh_next | dqg | dwp | dkg | dlast | X | Y]
+// backward workspace: [dv_new | dh_next | dqg | dwp | dkg | dlast | X | Y | EZ (damped) |
+// anchors (bs2 > 64)]
 size_t gdn2_bwd_workspace_bytes(const gdn2_desc* d) {
   if (validate_residual(d)) return 0;
   const Dims x = dims(d);
   size_t n = 5 * align_up(x.n_chunks * x.tD * 4) + 2 * align_up(x.n_chunks * x.DD * 4) +
-             align_up(x.n_chunks * x.D * 4);
+             align_up(x.n_chunks * x.D * 4) + anchor_bytes(d);
   if (damped_group(d) > 1) n += align_up(x.n_chunks * x.DD * 4);     // EZ(j + 1) per 64-token part j
   return n;
 }
@@ -260,6 +287,7 @@ int fwd_impl(const gdn2_desc* d, const void* q, const void* k, const void* v, co
   auto take = [&](size_t bytes) { float* p = at<float>(workspace, o2); o2 += align_up(bytes); return p; };
   float* uT = take(x.n_chunks * x.tD * 4);
   float* kgT = take(x.n_chunks * x.tD * 4);
+  void* anc_buf = take(anchor_bytes(d));
   // residuals for the backward -- training only; otherwise Wp / Qg / Aqk / gl live in the
   // workspace and Kg, h_pre and v_new are not stored at all (the scan consumes h_pre and v_new
   // itself).  Wp is kept in the orientation the forward scan contracts over keys; the reverse
@@ -283,8 +311,11 @@ int fwd_impl(const gdn2_desc* d, const void* q, const void* k, const void* v, co
     gl = take(x.n_chunks * x.D * 4);
   }
 
+  const float* anc = nullptr;
+  st = fill_anchors(d, cfg, g, bf16, anc_buf, s, &anc);
+  if (st) return st;
   gdn2::WyFwdArgs wa{};
-  wa.q = q; wa.k = k; wa.v = v; wa.w = w; wa.b = b; wa.g = g;
+  wa.q = q; wa.k = k; wa.v = v; wa.w = w; wa.b = b; wa.g = g; wa.anc = anc;
   wa.wp_f = wp; wa.uT_f = uT; wa.kg_f = kg; wa.kgT_f = kgT; wa.qg_f = qg;
   wa.aqk_f = aqk; wa.A = A; wa.gl = gl;
   wa.n_chunks = (int)x.n_chunks;
@@ -441,7 +472,14 @@ int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v,
   float* dlast = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.D * 4);
   float* xo = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.tD * 4);
   float* yo = at<float>(workspace, o2); o2 += align_up(x.n_chunks * x.DD * 4);
-  float* ez = damped_group(d) > 1 ? at<float>(workspace, o2) : nullptr;
+  float* ez = nullptr;
+  if (damped_group(d) > 1) {
+    ez = at<float>(workspace, o2);
+    o2 += align_up(x.n_chunks * x.DD * 4);
+  }
+  const float* anc = nullptr;
+  st = fill_anchors(d, cfg, g, false, at<float>(workspace, o2), s, &anc);
+  if (st) return st;
 
   gdn2::BwdPreArgs pa{aqk, qg, d_o, xo, yo, (int)x.n_chunks, cfg};
   hipError_t e = timed(6, s, [&] { return gdn2::launch_bwd_pre(d->D, pa, s); });
@@ -463,7 +501,7 @@ int gdn2_bwd(const gdn2_desc* d, const float* q, const float* k, const float* v,
     if (e != hipSuccess) return hip_fail(e, "bwd_state launch");
   }
 
-  gdn2::BwdWyArgs wa{q, k, v, w, b, g, A, d_o, vnew, dvn, dqg, dwp, dkg, dlast,
+  gdn2::BwdWyArgs wa{q, k, v, w, b, g, A, d_o, vnew, dvn, anc, dqg, dwp, dkg, dlast,
                      dq, dk, dv, dw, db, dg, (int)x.n_chunks, cfg};
   e = timed(4, s, [&] { return gdn2::launch_bwd_wy(d->D, wa, s); });
   if (e != hipSuccess) return hip_fail(e, "bwd_wy launch");

@@ -424,11 +424,17 @@ __device__ __forceinline__ float4 pick4(const float4 (&x)[4], int t) {
 }
 
 // STD: the pieces are the standard geometry's (bt = score_bs = 64, bs2 = 32), see std_pieces().
-// LEAN: the lean diagonal (cfg.diag); a compile-time choice, so that the BTL kernels carry no
-// trace of the lean loops (whose live ranges otherwise push registers into scratch).
-template <int D, int B3, bool STD, bool LEAN>
+// EM: elementwise pieces, a compile-time choice, so that the other kernels carry no trace of
+// the elementwise loops (whose live ranges otherwise push registers into scratch):
+//   EM_NONE  every piece on MFMA;
+//   EM_LEAN  the lean diagonal (cfg.diag): its diagonal-block pieces elementwise and exact;
+//   EM_MIX   pieces narrower than a 16 x 16 tile (bs2 = 8): every piece elementwise, with its
+//            legs (or, with the lean diagonal, the diagonal blocks exactly).
+enum { EM_NONE = 0, EM_LEAN = 1, EM_MIX = 2 };
+template <int D, int B3, bool STD, int EM>
 __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
-  static_assert(!(STD && LEAN), "the standard piece list is the BTL one");
+  constexpr bool ELEM = EM != EM_NONE;
+  static_assert(!(STD && ELEM), "the standard piece list is the BTL one");
   using Lay = BwdWyLayout<D>;
   using St = Strip<D>;
   constexpr int LD = Lay::LD, LT = Lay::LT, NT = 512, NW = 8, NTW = St::NTW, NKB = D / 16;
@@ -436,7 +442,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   // PERSIST: one workgroup per CU walks the chunks blockIdx.x, + gridDim.x, ...; the next
   // chunk's prologue operands are fetched during this chunk's B4 and gate phase (below).
   // Other instantiations run the body once (one workgroup per chunk).
-  constexpr bool RT_STATIC = St::NS == NW, PERSIST = RT_STATIC && !LEAN;
+  constexpr bool RT_STATIC = St::NS == NW, PERSIST = RT_STATIC && !ELEM;
   // X2 as DMA windows of 256 floats, a whole number per wave (the tail past T x LD is slack)
   constexpr int X2_WIN = PERSIST ? (T * LD / 256 + NW - 1) / NW * NW : (T * LD + 255) / 256;
   __shared__ __attribute__((aligned(16))) float smem[Lay::TOTAL];
@@ -835,7 +841,14 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     dk4[m] = dq4[m];
     dgc4[m] = dq4[m];
   }
-  constexpr bool lean = LEAN;
+  const bool lean = ELEM && cf.diag == DIAG_LEAN;
+  auto elementwise = [&](const Piece& pc) { return ELEM && ((lean && pc.kind != 0) || pc.P < 16); };
+  // this lane's block anchors of the kind-2 pieces (bs2 > 64), in this part's gc frame
+  float ar = 0.f, az = 0.f;
+  if (a.anc) {
+    ar = a.anc[(size_t)chunk * 2 * D + dcol];
+    az = a.anc[(size_t)chunk * 2 * D + D + dcol];
+  }
   // One piece of the two-level score factorisation; with the standard geometry the three
   // pieces are compile-time constants, so every branch and index below folds away.
   auto b4_piece = [&](const Piece pc) __attribute__((always_inline)) {
@@ -849,8 +862,8 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
       float rv[4], cv[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        rv[e] = piece_row_leg(pc, sG, LD, 16 * ti + 4 * g + e, dcol);
-        cv[e] = piece_col_leg(pc, sG, LD, 16 * tj + 4 * g + e, dcol);
+        rv[e] = piece_row_leg(pc, sG, LD, 16 * ti + 4 * g + e, dcol, ar, az);
+        cv[e] = piece_col_leg(pc, sG, LD, 16 * tj + 4 * g + e, dcol, ar, az);
       }
       ra[kb] = make_float4(rv[0], rv[1], rv[2], rv[3]);
       cbl[kb] = make_float4(cv[0], cv[1], cv[2], cv[3]);
@@ -935,24 +948,25 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   };
   if constexpr (STD) {
     constexpr Piece P0{0, 0, 32, 1, 0, 0, 32, 0}, P1{32, 32, 32, 1, 32, 32, 64, 0}, P2{32, 0, 32, 0, 32, 0, 0, 0};
-    if (!lean) {
-      b4_piece(P0);
-      b4_piece(P1);
-    }
+    b4_piece(P0);
+    b4_piece(P1);
     b4_piece(P2);
   } else {
     for (int pi = 0; pi < cf.pieces.n; ++pi) {
       const Piece pc = load_piece(cf.pieces.p[pi]);
-      if (pc.kind == 1 && lean) continue;
+      if (elementwise(pc)) continue;
       b4_piece(pc);
     }
   }
 
-  // lean diagonal blocks (b4.py:20-30): exact E = exp(clip(gc_i - gc_j, +-diff_clip)) per element
-  if constexpr (LEAN) {
+  // Elementwise pieces: the lean diagonal's (b4.py:20-30) with the exact
+  // E = exp(clip(gc_i - gc_j, +-diff_clip)), the others with E = row leg x column leg (the
+  // factorised form above, one element at a time).  In both, dE/dgc_i = E = -dE/dgc_j.
+  if constexpr (ELEM) {
     for (int pi = 0; pi < cf.pieces.n; ++pi) {
       const Piece pc = load_piece(cf.pieces.p[pi]);
-      if (pc.kind != 1) continue;
+      if (!elementwise(pc)) continue;
+      const bool exact = EM == EM_LEAN || (lean && pc.kind != 0);
       const float dc = cf.diff_clip;
 #pragma unroll
       for (int m = 0; m < NTW; ++m) {
@@ -963,9 +977,11 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
           const float gx = sG[x * LD + dcol];
           if (x >= pc.row0 && x < pc.row0 + pc.P) {
             float sq = 0.f, sbk = 0.f;
+            const float rl = exact ? 0.f : piece_row_leg(pc, sG, LD, x, dcol, ar, az);
             for (int jl = 0; jl < pc.P; ++jl) {
               const int j = pc.col0 + jl;
-              const float E = expf(clip_nan(gx - sG[j * LD + dcol], -dc, dc));
+              const float E = exact ? expf(clip_nan(gx - sG[j * LD + dcol], -dc, dc))
+                                    : rl * piece_col_leg(pc, sG, LD, j, dcol, ar, az);
               const float ek = E * k[j * D + dcol];
               sq += sDAq[x * LT + j] * ek;
               sbk += sDA[x * LT + j] * ek;
@@ -977,9 +993,11 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
           }
           if (x >= pc.col0 && x < pc.col0 + pc.P) {
             float s2 = 0.f;
+            const float cl = exact ? 0.f : piece_col_leg(pc, sG, LD, x, dcol, ar, az);
             for (int il = 0; il < pc.P; ++il) {
               const int i = pc.row0 + il;
-              const float E = expf(clip_nan(sG[i * LD + dcol] - gx, -dc, dc));
+              const float E = exact ? expf(clip_nan(sG[i * LD + dcol] - gx, -dc, dc))
+                                    : piece_row_leg(pc, sG, LD, i, dcol, ar, az) * cl;
               const float M = sDAq[i * LT + x] * (scale * q[i * D + dcol]) + sDA[i * LT + x] * (b[i * D + dcol] * k[i * D + dcol]);
               s2 += M * E;
             }
@@ -1285,7 +1303,11 @@ static bool std_pieces(const PieceList& pl) {
 }
 
 hipError_t launch_bwd_wy(int D, const BwdWyArgs& a, hipStream_t s) {
-  const bool lean = a.cfg.diag == DIAG_LEAN, std_geom = !lean && std_pieces(a.cfg.pieces);
+  // elementwise pieces: pieces of side 8 (every piece has side min(bs2, 32)), or the lean diagonal
+  const bool mix = a.cfg.pieces.p[0].P < 16, elem = mix || a.cfg.diag == DIAG_LEAN;
+  const bool std_geom = !elem && std_pieces(a.cfg.pieces);
+  // kind-2 pieces on the factorised path read the anchor buffer
+  if (!elem && a.cfg.pieces.p[0].kind == 2 && !a.anc) return hipErrorInvalidValue;
   // D = 128 BTL kernels are persistent: one workgroup per CU (their LDS admits no second).
   dim3 pgrid;
   const hipError_t e = persistent_grid(a.n_chunks, &pgrid);
@@ -1294,13 +1316,15 @@ hipError_t launch_bwd_wy(int D, const BwdWyArgs& a, hipStream_t s) {
     constexpr int M = decltype(m)::value;
     const dim3 grid(a.n_chunks), block(512);
     if (D == 128) {
-      if (lean) hipLaunchKernelGGL((bwd_wy_kernel<128, M, false, true>), grid, block, 0, s, a);
-      else if (std_geom) hipLaunchKernelGGL((bwd_wy_kernel<128, M, true, false>), pgrid, block, 0, s, a);
-      else hipLaunchKernelGGL((bwd_wy_kernel<128, M, false, false>), pgrid, block, 0, s, a);
+      if (mix) hipLaunchKernelGGL((bwd_wy_kernel<128, M, false, EM_MIX>), grid, block, 0, s, a);
+      else if (elem) hipLaunchKernelGGL((bwd_wy_kernel<128, M, false, EM_LEAN>), grid, block, 0, s, a);
+      else if (std_geom) hipLaunchKernelGGL((bwd_wy_kernel<128, M, true, EM_NONE>), pgrid, block, 0, s, a);
+      else hipLaunchKernelGGL((bwd_wy_kernel<128, M, false, EM_NONE>), pgrid, block, 0, s, a);
     } else {
-      if (lean) hipLaunchKernelGGL((bwd_wy_kernel<64, M, false, true>), grid, block, 0, s, a);
-      else if (std_geom) hipLaunchKernelGGL((bwd_wy_kernel<64, M, true, false>), grid, block, 0, s, a);
-      else hipLaunchKernelGGL((bwd_wy_kernel<64, M, false, false>), grid, block, 0, s, a);
+      if (mix) hipLaunchKernelGGL((bwd_wy_kernel<64, M, false, EM_MIX>), grid, block, 0, s, a);
+      else if (elem) hipLaunchKernelGGL((bwd_wy_kernel<64, M, false, EM_LEAN>), grid, block, 0, s, a);
+      else if (std_geom) hipLaunchKernelGGL((bwd_wy_kernel<64, M, true, EM_NONE>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((bwd_wy_kernel<64, M, false, EM_NONE>), grid, block, 0, s, a);
     }
     return 0;
   });

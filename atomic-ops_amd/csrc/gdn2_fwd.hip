@@ -42,7 +42,9 @@ struct WyLayout {
   static constexpr int OFF_S = 0, OFF_I = T * LT, OFF_X = 0;
   // per-wave 16 x 16 transpose tiles; during the inverse, the scalar doubling temp
   static constexpr int OFF_TR = (4 * TILE > 2 * T * LT) ? 4 * TILE : 2 * T * LT;
-  static constexpr int TOTAL = OFF_TR + 4 * 16 * TRP;
+  // the pass's kind-2 anchors: first row | last row of the diagonal block, DC channels each
+  static constexpr int OFF_ANC = OFF_TR + 4 * 16 * TRP;
+  static constexpr int TOTAL = OFF_ANC + 2 * DC;
   static_assert(D % DC == 0 && D % 64 == 0 || D == 64, "whole passes");
   static_assert(64 * T <= T * LT, "a strip group of X^T fits in the Akk slot");
 };
@@ -54,18 +56,21 @@ struct WyLayout {
 //   KIND 0 (off-diagonal, anchor a): ra = e^{min(gc_i - gc_a, 0)}, cb = e^{min(gc_a - gc_j, 0)}
 //   KIND 1 (BTL diagonal block [s0, s1)): r = gc_s0, half = (gc_s0 - gc_{s1-1}) / 2,
 //          ra = e^{(gc_i - r) + half}, cb = e^{(r - gc_j) - half}
+//   KIND 2 (BTL block wider than the part): as KIND 1 with r and gc_{s1-1} from sAnc (the
+//          block's first and last rows in this part's gc frame, DC channels each)
 // The k operand is the A operand (mma16_tr), so the accumulators hold Aqk / Akk tile (ti, tj)
 // in the operand layout: lane (r, g) has row 16 ti + r, columns 16 tj + 4 g .. + 3, which is
 // block (ti, tj) of FRAG(Aqk) and a float4 of a row-major tile.
 template <int DC, int DOT, int KIND>
 __device__ __forceinline__ void score_tile_pass(f4& accq, f4& acck, const float* sG, const float* sQ, const float* sKs,
-                                                const float* sBK, const Piece& pc, int ti, int tj) {
+                                                const float* sBK, const float* sAnc, const Piece& pc, int ti, int tj) {
   constexpr int NKBP = DC / 16;
   const int l = lane_id(), g = l >> 4;
   const int ra_row = KIND == 0 ? pc.anchor : pc.s0, rz_row = KIND == 0 ? pc.anchor : pc.s1 - 1;
   auto operands = [&](int kb, float4& bv, float4& aq, float4& ak) __attribute__((always_inline)) {
     const int oi = frag_blk(ti, kb, DC) + 4 * l, oj = frag_blk(tj, kb, DC) + 4 * l;
-    const float4 vi = ld4(sG + oi), vj = ld4(sG + oj), va = ld4(sG + frag_off(ra_row, 16 * kb + 4 * g, DC));
+    const float4 vi = ld4(sG + oi), vj = ld4(sG + oj);
+    const float4 va = KIND == 2 ? ld4(sAnc + 16 * kb + 4 * g) : ld4(sG + frag_off(ra_row, 16 * kb + 4 * g, DC));
     float4 ra, cb;
     if constexpr (KIND == 0) {
       ra = make_float4(fast_exp(min0(vi.x - va.x)), fast_exp(min0(vi.y - va.y)), fast_exp(min0(vi.z - va.z)),
@@ -73,7 +78,8 @@ __device__ __forceinline__ void score_tile_pass(f4& accq, f4& acck, const float*
       cb = make_float4(fast_exp(min0(va.x - vj.x)), fast_exp(min0(va.y - vj.y)), fast_exp(min0(va.z - vj.z)),
                        fast_exp(min0(va.w - vj.w)));
     } else {
-      const float4 h = scale4(sub4(va, ld4(sG + frag_off(rz_row, 16 * kb + 4 * g, DC))), 0.5f);
+      const float4 vz = KIND == 2 ? ld4(sAnc + DC + 16 * kb + 4 * g) : ld4(sG + frag_off(rz_row, 16 * kb + 4 * g, DC));
+      const float4 h = scale4(sub4(va, vz), 0.5f);
       ra = make_float4(fast_exp((vi.x - va.x) + h.x), fast_exp((vi.y - va.y) + h.y), fast_exp((vi.z - va.z) + h.z),
                        fast_exp((vi.w - va.w) + h.w));
       cb = make_float4(fast_exp((va.x - vj.x) - h.x), fast_exp((va.y - vj.y) - h.y), fast_exp((va.z - vj.z) - h.z),
@@ -259,9 +265,17 @@ __device__ __forceinline__ void wy_inverse(const Cfg& cf, const float* sK, float
 constexpr int WY_NTL = T / 16 * (T / 16 + 1) / 2;
 __device__ __forceinline__ int tri_row(int t) { return t >= 6 ? 3 : t >= 3 ? 2 : t >= 1 ? 1 : 0; }
 
-// LEAN: the diagonal pieces exactly (fwd/scores.py:31-36), per element by the workgroup's threads.
-template <int D, int DOT, bool LEAN, typename TIn>
+// Piece modes (PM), one instantiation each so that no kernel carries another mode's registers:
+//   PM_TILES  every piece on MFMA, kinds 0 and 1 (bs2 = 16 .. 64, BTL);
+//   PM_LEAN   the lean diagonal: the diagonal-block pieces (kinds 1 and 2) formed per element by
+//             the workgroup's threads, exactly (fwd/scores.py:31-36), the others on MFMA;
+//   PM_ELEM   pieces narrower than an MFMA tile (bs2 = 8): every piece per element, with its
+//             legs (or, with the lean diagonal, the diagonal blocks exactly);
+//   PM_WIDE   every piece of kind 2 on MFMA (bs2 = 128 / 256, BTL), legs from the anchor buffer.
+enum { PM_TILES = 0, PM_ELEM = 1, PM_WIDE = 2, PM_LEAN = 3 };
+template <int D, int DOT, int PM, typename TIn>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void wy_fwd_kernel(WyFwdArgs a) {
+  constexpr bool ELEM = PM == PM_ELEM || PM == PM_LEAN, WIDE = PM == PM_WIDE;
   using Lay = WyLayout<D>;
   constexpr int NT = 256, DC = Lay::DC, NPASS = Lay::NPASS, NKBP = Lay::NKBP, LT = Lay::LT, NKB = D / 16;
   constexpr int NSLOT = (WY_NTL + 3) / 4;
@@ -274,6 +288,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void w
   float* sI = smem + Lay::OFF_I;
   float* sX = smem + Lay::OFF_X;
   float* sM = smem + Lay::OFF_TR;
+  float* sAnc = smem + Lay::OFF_ANC;
   const Cfg& cf = a.cfg;
   const float clip = cf.clip;
   const int chunk = blockIdx.x;
@@ -317,21 +332,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void w
 #pragma unroll
   for (int s = 0; s < NSLOT; ++s) accq[s] = acck[s] = f4{0.f, 0.f, 0.f, 0.f};
   float4 xT[NKB];     // X^T = (b k e^gc)^T, fragment blocks (kb, wv), staged for Wp after the scores
-  // LEAN: this thread's diagonal-piece elements (element m = tid + NT m of the diagonal pieces
-  // taken in order), their running sums over d
-  constexpr int NLEAN = LEAN ? 12 : 1;
+  // ELEM: this thread's elementwise score elements (element m = tid + NT m of the elementwise
+  // pieces taken in order), their running sums over d.  At most 12 per thread: the diagonal
+  // pieces of bs2 = 64 (3 x 32 x 32) or every piece of bs2 = 8 (36 x 8 x 8).
+  const bool lean = cf.diag == DIAG_LEAN;
+  auto elementwise = [&](const Piece& pc) {
+    return PM == PM_LEAN ? pc.kind != 0 : (lean && pc.kind != 0) || pc.P < 16;
+  };
+  constexpr int NLEAN = ELEM ? 12 : 1;
   float lq[NLEAN], lk[NLEAN];
 #pragma unroll
   for (int m = 0; m < NLEAN; ++m) lq[m] = lk[m] = 0.f;
-  // element m of the diagonal pieces -> (row, col), or false past their end
-  auto lean_elem = [&](int m, int& er, int& ec) -> bool {
+  // element m of the elementwise pieces -> (row, col, piece), or false past their end
+  auto lean_elem = [&](int m, int& er, int& ec, Piece& pe) -> bool {
     int e = tid + NT * m;
     for (int pi = 0; pi < cf.pieces.n; ++pi) {
       const Piece pc = piece_at(cf.pieces, pi);
-      if (pc.kind != 1) continue;
+      if (!elementwise(pc)) continue;
       if (e < pc.P * pc.P) {
         er = pc.row0 + e / pc.P;
         ec = pc.col0 + e % pc.P;
+        pe = pc;
         return true;
       }
       e -= pc.P * pc.P;
@@ -374,6 +395,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void w
       if (a.kgT_f) stg4(a.kgT_f + tb + frag_blk(kg, wv, T) + 4 * l, wave_transpose16(tr, kgv[kb], r, g));
     }
     if (a.gl && tid < DC) a.gl[(size_t)chunk * D + DC * p + tid] = sG[frag_off(T - 1, tid, DC)];
+    // kind-2 anchors of this pass's channels (first row | last row of the diagonal block)
+    if (WIDE && tid < DC / 2) {
+      const int h = tid / (DC / 4), c4 = 4 * (tid % (DC / 4));
+      st4(sAnc + h * DC + c4, ld4(a.anc + ((size_t)chunk * 2 + h) * D + DC * p + c4));
+    }
     __syncthreads();
 
     // 3. scores over this pass's k blocks (scores.py:39-84): tiles t = wv + 4 s
@@ -383,23 +409,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void w
       if (t >= WY_NTL) continue;
       const int ti = tri_row(t), tj = t - ti * (ti + 1) / 2;
       const Piece& pc = pcs[s];
-      if (pc.kind == 0) score_tile_pass<DC, DOT, 0>(accq[s], acck[s], sG, sQ, sKs, sBK, pc, ti, tj);
-      else if (!LEAN) score_tile_pass<DC, DOT, 1>(accq[s], acck[s], sG, sQ, sKs, sBK, pc, ti, tj);
+      if (ELEM && elementwise(pc)) continue;
+      if constexpr (WIDE) score_tile_pass<DC, DOT, 2>(accq[s], acck[s], sG, sQ, sKs, sBK, sAnc, pc, ti, tj);
+      else if (pc.kind == 0) score_tile_pass<DC, DOT, 0>(accq[s], acck[s], sG, sQ, sKs, sBK, sAnc, pc, ti, tj);
+      else score_tile_pass<DC, DOT, 1>(accq[s], acck[s], sG, sQ, sKs, sBK, sAnc, pc, ti, tj);
     }
-    if constexpr (LEAN) {
-      // exact diagonal: exp(clip(gc_i - gc_j, +-diff_clip)) per element and channel, summed over
-      // the channels in order (the pass's channels continue the previous pass's sums)
+    if constexpr (ELEM) {
+      // per element and channel, summed over the channels in order (the pass's channels continue
+      // the previous pass's sums): the lean diagonal's exact exp(clip(gc_i - gc_j, +-diff_clip)),
+      // or the piece's legs ra_i cb_j applied to the operands as on the MFMA path
       const float dcl = cf.diff_clip;
 #pragma unroll
       for (int m = 0; m < NLEAN; ++m) {
         int er, ec;
-        if (!lean_elem(m, er, ec)) continue;
+        Piece pe;
+        if (!lean_elem(m, er, ec, pe)) continue;
+        const bool exact = PM == PM_LEAN || (lean && pe.kind != 0);
+        // (a kind-2 piece is elementwise only with the lean diagonal, hence exact)
+        const int ra_row = pe.kind == 0 ? pe.anchor : pe.s0, rz_row = pe.kind == 0 ? pe.anchor : pe.s1 - 1;
         for (int d = 0; d < DC; ++d) {
           const int oi = frag_off(er, d, DC), oj = frag_off(ec, d, DC);
-          const float E = expf(clip_nan(sG[oi] - sG[oj], -dcl, dcl));
           const float kj = sKs[oj];
-          lq[m] += (sQ[oi] * E) * kj;
-          lk[m] += (sBK[oi] * E) * kj;
+          if (exact) {
+            const float E = expf(clip_nan(sG[oi] - sG[oj], -dcl, dcl));
+            lq[m] += (sQ[oi] * E) * kj;
+            lk[m] += (sBK[oi] * E) * kj;
+          } else {
+            const float ga = sG[frag_off(ra_row, d, DC)], gz = sG[frag_off(rz_row, d, DC)];
+            const float ra = leg_row(pe.kind, sG[oi], ga, gz), bv = kj * leg_col(pe.kind, sG[oj], ga, gz);
+            lq[m] += (sQ[oi] * ra) * bv;
+            lk[m] += (sBK[oi] * ra) * bv;
+          }
         }
       }
     }
@@ -414,8 +454,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void w
     const int t = wv + 4 * s;
     if (t >= WY_NTL) continue;
     const int ti = tri_row(t), tj = t - ti * (ti + 1) / 2;
-    if (LEAN && pcs[s].kind == 1) continue;
     const int i = 16 * ti + r, j0 = 16 * tj + 4 * g;
+    if (ELEM && elementwise(pcs[s])) {
+      // the pieces write their own elements below; a diagonal tile cut into 8 x 8 pieces has
+      // no piece over its upper right quarter (rows 0-7, columns 8-15), which is zero
+      if (PM == PM_ELEM && ti == tj && r < 8 && g >= 2) {
+        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+        st4(sK + i * LT + j0, z);
+        if (a.aqk_f) stg4(a.aqk_f + sb + frag_blk(ti, tj, T) + 4 * l, z);
+        if (a.aqk) stg4(a.aqk + sb + i * T + j0, z);
+        if (a.akk) stg4(a.akk + sb + i * T + j0, z);
+      }
+      continue;
+    }
     float aq[4], ak[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -437,11 +488,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void w
     if (a.aqk) stg4(a.aqk + sb + (16 * ti + r) * T + 16 * tj + 4 * g, z);
     if (a.akk) stg4(a.akk + sb + (16 * ti + r) * T + 16 * tj + 4 * g, z);
   }
-  if constexpr (LEAN) {
+  if constexpr (ELEM) {
 #pragma unroll
     for (int m = 0; m < NLEAN; ++m) {
       int er, ec;
-      if (!lean_elem(m, er, ec)) continue;
+      Piece pe;
+      if (!lean_elem(m, er, ec, pe)) continue;
       const float aq = ec <= er ? sanitize(scale * lq[m], clip) : 0.f;
       const float ak = ec < er ? sanitize(lk[m], clip) : 0.f;
       sK[er * LT + ec] = ak * ome;
@@ -661,17 +713,79 @@ hipError_t launch_stream_probe(int mode, const void* src, void* dst, size_t n4, 
   return hipGetLastError();
 }
 
+// ------------------------------------------------------------------------------------
+// Anchors of the diagonal blocks wider than a part (AnchorArgs): one workgroup per block of B
+// parts; each part's gc by chunk_cumsum (the arithmetic of every other kernel), its last row gl
+// kept per channel, then the anchors in each part's frame.
+// ------------------------------------------------------------------------------------
+template <int D, typename TIn>
+__global__ __launch_bounds__(512) void anchor_kernel(AnchorArgs a) {
+  constexpr int LD = D + 4, BMAX = 4;
+  __shared__ __attribute__((aligned(16))) float sG[T * LD];
+  const int blk = blockIdx.x, B = a.B, t = threadIdx.x;
+  float g00 = 0.f, gl[BMAX];
+#pragma unroll
+  for (int j = 0; j < BMAX; ++j) {
+    gl[j] = 0.f;
+    if (j < B) {
+      chunk_cumsum<D, LD, 512>(static_cast<const TIn*>(a.g) + io_off<D>(a.cfg, blk * B + j), sG);
+      if (t < D) {
+        if (j == 0) g00 = sG[t];
+        gl[j] = sG[(T - 1) * LD + t];
+      }
+      __syncthreads();     // the next part's cumsum overwrites sG
+    }
+  }
+  if (t >= D) return;
+#pragma unroll
+  for (int j = 0; j < BMAX; ++j) {
+    if (j >= B) break;
+    float before = 0.f, from = 0.f;
+#pragma unroll
+    for (int i = 0; i < BMAX; ++i) {
+      if (i < j) before += gl[i];
+      else if (i < B) from += gl[i];
+    }
+    float* o = a.anc + (size_t)(blk * B + j) * 2 * D;
+    o[t] = g00 - before;
+    o[D + t] = from;
+  }
+}
+
+hipError_t launch_anchors(int D, const AnchorArgs& a, hipStream_t s, bool bf16_inputs) {
+  const dim3 grid(a.n_chunks / a.B), block(512);
+  if (bf16_inputs) {
+    if (D == 128) hipLaunchKernelGGL((anchor_kernel<128, uint16_t>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((anchor_kernel<64, uint16_t>), grid, block, 0, s, a);
+  } else {
+    if (D == 128) hipLaunchKernelGGL((anchor_kernel<128, float>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((anchor_kernel<64, float>), grid, block, 0, s, a);
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_wy_fwd(int D, const WyFwdArgs& a, hipStream_t s, bool bf16_inputs) {
-  const bool lean = a.cfg.diag == DIAG_LEAN;
+  // every piece has side min(bs2, 32) and, past bs2 = 64, kind 2
+  const Piece& p0 = a.cfg.pieces.p[0];
+  const int pm = p0.P < 16 ? PM_ELEM : a.cfg.diag == DIAG_LEAN ? PM_LEAN : p0.kind == 2 ? PM_WIDE : PM_TILES;
+  if (pm == PM_WIDE && !a.anc) return hipErrorInvalidValue;
   dispatch_mode(a.cfg.dot_mode, [&](auto m) {
     constexpr int M = decltype(m)::value;
     auto go = [&](auto kern) { hipLaunchKernelGGL(kern, dim3(a.n_chunks), dim3(256), 0, s, a); };
+    auto by_pm = [&](auto d, auto tin) {
+      constexpr int DD = decltype(d)::value;
+      using TI = decltype(tin);
+      if (pm == PM_ELEM) go(wy_fwd_kernel<DD, M, PM_ELEM, TI>);
+      else if (pm == PM_LEAN) go(wy_fwd_kernel<DD, M, PM_LEAN, TI>);
+      else if (pm == PM_WIDE) go(wy_fwd_kernel<DD, M, PM_WIDE, TI>);
+      else go(wy_fwd_kernel<DD, M, PM_TILES, TI>);
+    };
     if (bf16_inputs) {
-      if (D == 128) lean ? go(wy_fwd_kernel<128, M, true, uint16_t>) : go(wy_fwd_kernel<128, M, false, uint16_t>);
-      else lean ? go(wy_fwd_kernel<64, M, true, uint16_t>) : go(wy_fwd_kernel<64, M, false, uint16_t>);
+      if (D == 128) by_pm(std::integral_constant<int, 128>{}, uint16_t{});
+      else by_pm(std::integral_constant<int, 64>{}, uint16_t{});
     } else {
-      if (D == 128) lean ? go(wy_fwd_kernel<128, M, true, float>) : go(wy_fwd_kernel<128, M, false, float>);
-      else lean ? go(wy_fwd_kernel<64, M, true, float>) : go(wy_fwd_kernel<64, M, false, float>);
+      if (D == 128) by_pm(std::integral_constant<int, 128>{}, float{});
+      else by_pm(std::integral_constant<int, 64>{}, float{});
     }
     return 0;
   });

@@ -10,10 +10,15 @@ namespace gdn2 {
 // kind 1: diagonal-block piece of block [s0, s1): BTL legs exp(gc_i - r + half) and
 //         exp(r - gc_j - half), r = gc[s0], half = (gc[s0] - gc[s1-1]) / 2; or, with the
 //         lean diagonal, the exact exp(clip(gc_i - gc_j, +-diff_clip)) per element.
+// kind 2: as kind 1 for a diagonal block wider than the 64-token part (bs2 = 128 / 256): r and
+//         gc[s1-1] are the block's first and last rows, which lie in other parts; they come
+//         expressed in this part's gc frame from the anchor buffer (anchor_kernel).
+// Pieces are P x P squares, P = min(bs2, 32); P = 8 (bs2 = 8) is narrower than an MFMA tile
+// and such pieces are formed per element.
 struct Piece {
   int8_t row0, col0, P, kind, anchor, s0, s1, pad;
 };
-constexpr int MAX_PIECES = 16;
+constexpr int MAX_PIECES = 40;     // bs2 = 8 at T = 64: 36 pieces
 struct PieceList {
   Piece p[MAX_PIECES];
   int n;
@@ -96,6 +101,7 @@ __device__ __forceinline__ size_t io_off(const C& c, int chunk) {
 //   pointer may be null (not written).
 struct WyFwdArgs {
   const void *q, *k, *v, *w, *b, *g;   // fp32, or bfloat16 bits for the bf16-input variant
+  const float* anc;    // kind-2 pieces: the anchor buffer (AnchorArgs), else null
   float *wp_f, *uT_f, *kg_f, *kgT_f, *qg_f, *aqk_f;
   float *A, *gl;
   float *aqk, *akk, *wp, *u, *kg, *qg;
@@ -203,6 +209,7 @@ struct BwdStateRcArgs {
 
 struct BwdWyArgs {
   const float *q, *k, *v, *w, *b, *g, *A, *dout, *v_new_f, *dv_new_f;
+  const float* anc;    // kind-2 pieces: the anchor buffer (AnchorArgs), else null
   const float *dqg, *dwp, *dkg, *dlast;
   float *dq, *dk, *dv, *dw, *db, *dg;
   int n_chunks;
@@ -228,6 +235,20 @@ struct DecodeArgs {
 };
 
 hipError_t launch_decode(int D, const DecodeArgs& a, int n_bh, hipStream_t s);
+
+// Anchors of the diagonal blocks wider than a 64-token part (bs2 = 64 B, B = 2 or 4 parts; kind-2
+// pieces): for part j of a block, in the part's own gc frame (gc restarts at every part),
+//   anc[(part, 0, d)] = gc of the block's first row  = gc_0[0][d] - sum_{i<j} gl_i[d],
+//   anc[(part, 1, d)] = gc of the block's last row   = sum_{i>=j} gl_i[d],
+// with gl_i the last row of part i's gc, all formed with chunk_cumsum's arithmetic (so gl_i is
+// bit-identical to what every other kernel computes) and the sums in ascending part order.
+struct AnchorArgs {
+  const void* g;       // fp32 or bfloat16 bits
+  float* anc;          // (n_chunks, 2, D)
+  int n_chunks, B;     // B parts per diagonal block
+  Cfg cfg;
+};
+hipError_t launch_anchors(int D, const AnchorArgs& a, hipStream_t s, bool bf16_inputs);
 
 hipError_t launch_wy_fwd(int D, const WyFwdArgs& a, hipStream_t s, bool bf16_inputs = false);
 
@@ -266,20 +287,34 @@ __device__ __forceinline__ int xcd_remap(int nblk) {
   return (nblk % 8) ? b : (b % 8) * (nblk / 8) + b / 8;
 }
 
-// Device-side leg factors of a score piece (B4; the forward scores inline the same formulas).
-__device__ __forceinline__ float piece_row_leg(const Piece& pc, const float* sG, int LD, int i, int d) {
-  const float gi = sG[i * LD + d];
-  if (pc.kind == 0) return fast_exp(min0(gi - sG[pc.anchor * LD + d]));
-  const float r = sG[pc.s0 * LD + d];
-  const float half = 0.5f * (r - sG[(pc.s1 - 1) * LD + d]);
-  return fast_exp((gi - r) + half);
+// Leg factors of a score piece from gc values (fwd/scores.py:16-22, 39-65): gi / gj the gc of
+// the row / column, ga the anchor's (kind 0) or the diagonal block's first row (kinds 1, 2), gz
+// the block's last row (kinds 1, 2).  The forward's MFMA path inlines the same formulas.
+__device__ __forceinline__ float leg_row(int kind, float gi, float ga, float gz) {
+  if (kind == 0) return fast_exp(min0(gi - ga));
+  const float half = 0.5f * (ga - gz);
+  return fast_exp((gi - ga) + half);
 }
-__device__ __forceinline__ float piece_col_leg(const Piece& pc, const float* sG, int LD, int j, int d) {
-  const float gj = sG[j * LD + d];
-  if (pc.kind == 0) return fast_exp(min0(sG[pc.anchor * LD + d] - gj));
-  const float r = sG[pc.s0 * LD + d];
-  const float half = 0.5f * (r - sG[(pc.s1 - 1) * LD + d]);
-  return fast_exp((r - gj) - half);
+__device__ __forceinline__ float leg_col(int kind, float gj, float ga, float gz) {
+  if (kind == 0) return fast_exp(min0(ga - gj));
+  const float half = 0.5f * (ga - gz);
+  return fast_exp((ga - gj) - half);
+}
+// The same with gc in a row-major LDS tile (ld LD); ar / az: channel d's values of the anchor
+// buffer (kind 2; unused otherwise).
+__device__ __forceinline__ float piece_ga(const Piece& pc, const float* sG, int LD, int d, float ar) {
+  return pc.kind == 2 ? ar : sG[(pc.kind == 0 ? pc.anchor : pc.s0) * LD + d];
+}
+__device__ __forceinline__ float piece_gz(const Piece& pc, const float* sG, int LD, int d, float az) {
+  return pc.kind == 2 ? az : pc.kind == 1 ? sG[(pc.s1 - 1) * LD + d] : 0.f;
+}
+__device__ __forceinline__ float piece_row_leg(const Piece& pc, const float* sG, int LD, int i, int d, float ar,
+                                               float az) {
+  return leg_row(pc.kind, sG[i * LD + d], piece_ga(pc, sG, LD, d, ar), piece_gz(pc, sG, LD, d, az));
+}
+__device__ __forceinline__ float piece_col_leg(const Piece& pc, const float* sG, int LD, int j, int d, float ar,
+                                               float az) {
+  return leg_col(pc.kind, sG[j * LD + d], piece_ga(pc, sG, LD, d, ar), piece_gz(pc, sG, LD, d, az));
 }
 
 }  // namespace gdn2

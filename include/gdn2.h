@@ -45,8 +45,10 @@ enum { GDN2_OK = 0, GDN2_ERR_INVALID = 1, GDN2_ERR_UNSUPPORTED = 2, GDN2_ERR_HIP
 
 /* One segment call.  Field meaning follows BLRConfig (atomic_gdn2/config.py:38-60).
  * Supported by this build: bt in {64, 128, 256} (128 and 256 as 2 and 4 parts of 64 tokens;
- * with wy_eps > 0 they need state_ckpt >= 1), D in {64, 128}, L % bt == 0, bs2 in {16, 32, 64},
- * bs2 | score_bs | bt, mb a power of two dividing bt.
+ * with wy_eps > 0 they need state_ckpt >= 1), D in {64, 128}, L % bt == 0, bs2 >= 8 (so one of
+ * 8, 16, ..., 256), bs2 | score_bs | bt, mb a power of two dividing bt.  bs2 = 8 forms the
+ * scores per element; bs2 = 128 / 256 (a BTL diagonal block wider than a 64-token part) adds a
+ * pre-pass that writes each part's block end rows into the workspace (kernel id 9).
  *   L        tokens of this segment (a multiple of bt).
  *   seq_ld   tokens between the starts of consecutive (b, h) sequences in the raw operator
  *            tensors q..g, o, d_o, dq..dg (0 = L, i.e. contiguous (B, H, L, D)).  A segment
@@ -217,8 +219,9 @@ int gdn2_debug_stream(int mode, const void* src, void* dst, size_t bytes, void* 
  * duration in milliseconds and the launch count, then stops recording.
  * Kernel ids: 0 wy_fwd, 1 scan_fwd (with the output unless state_ckpt == 0 in training),
  * 2 scan_bwd, 3 bwd_state (state_ckpt == 0), 4 bwd_wy, 5 out_fwd (training, state_ckpt == 0),
- * 6 bwd_pre, 7 bwd_state_rc (state_ckpt >= 1: bwd_state with the states recomputed), 8 decode. */
-#define GDN2_NUM_KERNELS 9
+ * 6 bwd_pre, 7 bwd_state_rc (state_ckpt >= 1: bwd_state with the states recomputed), 8 decode,
+ * 9 anchors (bs2 > 64: the diagonal blocks' end rows, before wy_fwd and bwd_wy). */
+#define GDN2_NUM_KERNELS 10
 int gdn2_prof_begin(int max_launches);
 int gdn2_prof_end(double ms_sum[GDN2_NUM_KERNELS], int counts[GDN2_NUM_KERNELS]);
 

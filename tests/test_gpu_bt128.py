@@ -236,3 +236,60 @@ def test_bt256_checkpoint_intervals_agree_bitwise(ckpt):
     b = grad(cfg, D ** -0.5, arrs, h0, ckpt=ckpt)
     for n in a:
         assert torch.equal(a[n], b[n]), (ckpt, n)
+
+
+# bs2 outside [16, 64]: a diagonal block of 8 tokens (pieces narrower than a 16 x 16 tile, formed
+# elementwise) and diagonal blocks of 128 / 256 tokens (wider than the 64-token part: their end
+# rows come from the anchor pre-pass)
+INNER = [
+    dict(bt=64, score_bs=64, bs2=8, wy_eps=0.0),
+    dict(bt=64, score_bs=16, bs2=8, wy_eps=0.0),
+    dict(bt=128, score_bs=128, bs2=8, wy_eps=1e-3),
+    dict(bt=128, score_bs=64, bs2=8, wy_eps=0.02, diag="lean"),
+    dict(bt=128, score_bs=128, bs2=128, wy_eps=1e-3),
+    dict(bt=128, score_bs=128, bs2=128, wy_eps=0.0),
+    dict(bt=128, score_bs=128, bs2=128, wy_eps=0.05, diag="lean"),
+    dict(bt=256, score_bs=256, bs2=128, wy_eps=0.02),
+    dict(bt=256, score_bs=256, bs2=256, wy_eps=0.02),
+    dict(bt=256, score_bs=256, bs2=256, wy_eps=0.0, b3_dot_mode="bf16x3", solve_dot_mode="bf16x3"),
+]
+
+
+@pytest.mark.parametrize("kw", INNER, ids=lambda kw: ",".join(f"{k}={v}" for k, v in kw.items()))
+@pytest.mark.parametrize("D", [64, 128])
+def test_inner_block_sizes_match_oracle(kw, D):
+    """Forward and every gradient against the float64 oracle run at the same bt / score_bs /
+    bs2 over whole chunks (three chunks, h0 given)."""
+    bt = kw["bt"]
+    cfg = base_cfg(**{**dict(bc=bt // 2, mb=8, g_max=160.0 / kw["bs2"]), **kw})
+    banner(f"inner block {kw} D={D}")
+    scale = D ** -0.5
+    arrs = mk_inputs(1, 3 * bt, 2, D, 41, g=0.05, layout="bhld")
+    h0 = (np.random.default_rng(42).standard_normal((1, 2, D, D)) * 0.1).astype(np.float32)
+    hip = grad(cfg, scale, arrs, h0)
+    errs = compare(hip, oracle_grad(cfg, scale, arrs, h0), GATE, ("o", "h_final") + NAMES + ("dh0",))
+    banner(f"inner block max rel-L2 {max(errs.values()):.2e}")
+
+
+@pytest.mark.parametrize("bt,bs2", [(128, 128), (256, 256), (256, 128)])
+def test_wide_diagonal_blocks_at_the_half_span_limit(bt, bs2):
+    """|g| just under g_max = 160 / bs2 on every token: the BTL legs of a bs2-token diagonal
+    block reach e^(+-0.5 |g| (bs2 - 1)) ~ e^78, within float32 only because each part measures
+    its legs from the block's own first and last rows.  An anchor off by one part's gate sum
+    (|g| 64 ~ 78) overflows a leg in some part (an anchor error otherwise cancels in the
+    products of the legs), so this pins the anchor buffer to within the range float32 leaves."""
+    D = 64
+    cfg = base_cfg(bt=bt, bc=bt // 2, score_bs=bt, bs2=bs2, mb=8, wy_eps=1e-3, g_max=160.0 / bs2)
+    banner(f"wide diagonal blocks at the half-span limit bt={bt} bs2={bs2}")
+    scale = D ** -0.5
+    q, k, v, w, b, _ = mk_inputs(1, 2 * bt, 2, D, 43, layout="bhld")
+    rng = np.random.default_rng(44)
+    g = (-(0.97 + 0.02 * rng.uniform(size=q.shape)) * cfg.g_max).astype(np.float32)
+    assert 75.0 < float(-g.max()) * (bs2 - 1) / 2 and float(-g.min()) * (bs2 - 1) / 2 < 80.0
+    arrs = (q, k, v, w, b, g)
+    h0 = (rng.standard_normal((1, 2, D, D)) * 0.1).astype(np.float32)
+    hip = grad(cfg, scale, arrs, h0)
+    for n, x in hip.items():
+        assert torch.isfinite(x).all(), n
+    errs = compare(hip, oracle_grad(cfg, scale, arrs, h0), GATE, ("o", "h_final") + NAMES + ("dh0",))
+    banner(f"half-span limit max rel-L2 {max(errs.values()):.2e}")

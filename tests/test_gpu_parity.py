@@ -198,8 +198,9 @@ def test_wy_stage_config1(cfg1):
     assert float((M @ A.double() - I).abs().max()) < 1e-4
 
 
-@pytest.mark.parametrize("diag,bs2", [("btl", 32), ("btl", 16), ("lean", 32)])
-def test_build_scores_takes_gc(cfg1, diag, bs2):
+@pytest.mark.parametrize("diag,bs2,sbs", [("btl", 32, 64), ("btl", 16, 64), ("lean", 32, 64), ("btl", 8, 64),
+                                          ("btl", 8, 16), ("lean", 8, 32)])
+def test_build_scores_takes_gc(cfg1, diag, bs2, sbs):
     """stages.build_scores(q, k, b, gc, scale, cfg), the reference's Kernel A signature
     (fwd/scores.py:87-97): gc is the caller's in-chunk cumulative gate, used as given.  Against
     the kernel-semantics oracle on the same gc (float64), and equal to the scores of
@@ -208,8 +209,8 @@ def test_build_scores_takes_gc(cfg1, diag, bs2):
     from atomic_gdn2.stages import build_scores, wy_stage
     from oracle import gdn2_oracle as O
     arrs, scale, _ = cfg1
-    banner(f"build_scores(gc) {diag} bs2={bs2}")
-    cfg = base_cfg().with_(diag=diag, bs2=bs2)
+    banner(f"build_scores(gc) {diag} bs2={bs2} score_bs={sbs}")
+    cfg = base_cfg().with_(diag=diag, bs2=bs2, score_bs=sbs)
     q, k, v, w, b, g = (torch.from_numpy(a) for a in arrs)
     ch = lambda t: O.to_chunks(t, 64)
     gc = torch.cumsum(ch(g), dim=-2)                                   # float32, the caller's
@@ -224,23 +225,26 @@ def test_build_scores_takes_gc(cfg1, diag, bs2):
     assert rel_l2(akk_g, akk) > 1e-3
 
 
-def test_forward_residuals_config1(cfg1):
+@pytest.mark.parametrize("kw", [dict(), dict(bs2=8), dict(score_bs=16, bs2=8)],
+                         ids=lambda kw: ",".join(f"{k}={v}" for k, v in kw.items()) or "base")
+def test_forward_residuals_config1(cfg1, kw):
     """gdn2_fwd through the C ABI: every residual sub-buffer and o / h_final per chunk vs
     the kernel-semantics oracle (localises a forward error to a stage and a chunk)."""
     from atomic_gdn2 import _lib
     from oracle import gdn2_oracle as O
     arrs, scale, _ = cfg1
-    banner("fwd residuals config1")
-    cfg = base_cfg()
+    banner(f"fwd residuals config1 {kw}")
+    cfg = base_cfg(**kw)
     xs = to_dev(arrs)
     B, H, L, D = arrs[0].shape
     nc = L // 64
     desc = _lib.make_desc(cfg, B, H, L, D, scale)
     offs, tot = _lib.residual_layout(desc)
-    res = torch.zeros(tot, dtype=torch.uint8, device="cuda")
+    # residual and outputs start as NaN (all bits set), so an element the kernels leave unwritten shows
+    res = torch.full((tot,), 255, dtype=torch.uint8, device="cuda")
     ws = torch.zeros(_lib.lib().gdn2_fwd_workspace_bytes(ctypes.byref(desc), 1), dtype=torch.uint8, device="cuda")
-    o = torch.empty(B, H, L, D, device="cuda")
-    hf = torch.empty(B, H, D, D, device="cuda")
+    o = torch.full((B, H, L, D), float("nan"), device="cuda")
+    hf = torch.full((B, H, D, D), float("nan"), device="cuda")
     h0 = torch.zeros(B, H, D, D, device="cuda")
     _lib.check(_lib.lib().gdn2_fwd(ctypes.byref(desc), *map(_lib.ptr, xs), _lib.ptr(h0), _lib.ptr(o), _lib.ptr(hf),
                                    _lib.ptr(res), _lib.ptr(ws), _lib.stream_handle()), "gdn2_fwd")

@@ -92,9 +92,8 @@ def test_residual_layout_and_workspaces():
 
 @pytest.mark.parametrize("kw,msg", [
     (dict(bt=512, bc=256, score_bs=128), "bt in"),
-    (dict(bt=128, bc=64, score_bs=128, bs2=128, g_max=2.5), "bs2 <= 64"),
     (dict(D=96), "D in"),
-    (dict(bs2=8, g_max=20.0), "bs2 >= 16"),
+    (dict(bs2=4, g_max=40.0), "bs2 >= 8"),
     (dict(L=2000), "divisible"),
     (dict(L=0), "non-positive"),
     (dict(B=0), "non-positive"),
@@ -103,6 +102,22 @@ def test_descriptor_validation(kw, msg):
     from atomic_gdn2 import _lib
     with pytest.raises(ValueError, match=msg):
         _lib.residual_layout(_desc(**kw))
+
+
+@pytest.mark.parametrize("bt,bs2", [(64, 8), (128, 8), (128, 128), (256, 128), (256, 256)])
+def test_all_inner_block_sizes_accepted(bt, bs2):
+    """Every bs2 the reference's config admits at the supported chunk sizes is accepted; a
+    diagonal block wider than 64 tokens adds the anchor buffer (two rows of D floats per
+    64-token part) to both workspaces."""
+    from atomic_gdn2 import _lib
+    d = _desc(bt=bt, bc=bt // 2, score_bs=bt, bs2=bs2, g_max=160.0 / bs2)
+    _lib.residual_layout(d)
+    L = _lib.lib()
+    d0 = _desc(bt=bt, bc=bt // 2, score_bs=bt, bs2=min(bs2, 64), g_max=160.0 / bs2)
+    extra = 4 * 6 * 32 * 2 * 128 * 4 if bs2 > 64 else 0
+    for wr in (0, 1):
+        assert L.gdn2_fwd_workspace_bytes(ctypes.byref(d), wr) == L.gdn2_fwd_workspace_bytes(ctypes.byref(d0), wr) + extra
+    assert L.gdn2_bwd_workspace_bytes(ctypes.byref(d)) == L.gdn2_bwd_workspace_bytes(ctypes.byref(d0)) + extra
 
 
 def test_state_checkpoint_residual_layout():
