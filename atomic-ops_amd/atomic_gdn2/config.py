@@ -1,7 +1,7 @@
 """Single source of truth for the operator configuration.
 
 Mirrors ``BLRConfig`` / ``make_cfg`` / ``PROD`` of the reference
-(``atomic_gdn2/config.py:17-93``): same fields, defaults, validation errors and helpers.
+(``atomic_gdn2/config.py:8-83``): same fields, defaults, validation errors and helpers.
 The execution knobs ``group``, ``interpret`` and ``vmem_mb`` are accepted for drop-in
 compatibility; the HIP kernels do not use them.
 """

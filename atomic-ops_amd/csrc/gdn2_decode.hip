@@ -1,7 +1,7 @@
 // Token recurrence of the GDN-2 operator for serving, on gfx950: the single-token decode step
 // and the tail of the forward-only prefill (the tokens after its last full chunk), with the
 // semantics of the reference's inference module (notebooks/gdn2_v031_stage2_tpu.ipynb, cell 1,
-// INFERENCE_V031: _decode_body and decode_step; the per-token math is reference/ref.py:118-132).
+// INFERENCE_V031: _decode_body and decode_step; the per-token math is reference/ref.py:116-130).
 // Per token, for every (batch, head):
 //   S = reset ? 0 : state;   h = diag(e^{min(g,0)}) S;   erase_j = sum_d (b k)_d h[d][j];
 //   v_new = w v - erase;     h += k v_new^T;              o_j = sum_d h[d][j] (s q)_d;

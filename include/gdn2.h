@@ -36,14 +36,14 @@ extern "C" {
 
 #define GDN2_ABI_VERSION 3
 
-/* Matmul precision modes (atomic_gdn2/precision.py:27-31; config.py:51-53). */
+/* Matmul precision modes (atomic_gdn2/precision.py:27-31; config.py:41-43). */
 enum { GDN2_DOT_HIGHEST = 0, GDN2_DOT_BF16X3 = 1, GDN2_DOT_DEFAULT = 2 };
 /* Diagonal-block treatment of the scores (config.py:46). */
 enum { GDN2_DIAG_BTL = 0, GDN2_DIAG_LEAN = 1 };
 /* Status codes. */
 enum { GDN2_OK = 0, GDN2_ERR_INVALID = 1, GDN2_ERR_UNSUPPORTED = 2, GDN2_ERR_HIP = 3 };
 
-/* One segment call.  Field meaning follows BLRConfig (atomic_gdn2/config.py:38-60).
+/* One segment call.  Field meaning follows BLRConfig (atomic_gdn2/config.py:29-50).
  * Supported by this build: bt in {64, 128, 256} (128 and 256 as 2 and 4 parts of 64 tokens;
  * with wy_eps > 0 they need state_ckpt >= 1), D in {64, 128}, L % bt == 0, bs2 >= 8 (so one of
  * 8, 16, ..., 256), bs2 | score_bs | bt, mb a power of two dividing bt.  bs2 = 8 forms the

@@ -29,7 +29,7 @@ def test_half_span_of_constant_gate():
 
 
 def test_precondition_check_raises():
-    # test_t2_domain.py:36-39
+    # test_t2_domain.py:35-38
     g = -torch.full((1, 1, 128, 8), 6.0)
     with pytest.raises(RuntimeError):
         domain.check_preconditions(g, make_cfg(bs2=32, g_max=1e3), strict=True)

@@ -141,7 +141,7 @@ def test_legacy_strong_decay_beyond_the_btl_span(g_rate):
 
 @pytest.mark.gpu
 def test_legacy_pallas_shapes():
-    # tests/test_pallas.py:17-46 (ones inputs; shapes only)
+    # tests/test_pallas.py:15-41 (ones inputs; shapes only)
     if not torch.cuda.is_available():
         pytest.skip("no ROCm GPU")
     print("[gpu-test] legacy shapes", flush=True)
