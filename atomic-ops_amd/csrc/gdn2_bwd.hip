@@ -620,9 +620,11 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     else xdv[it] = ldg4(a.dv_new_f + tb + 4 * f);
   };
 
-  // P1: dAqk = (dO v_new^T) * causal; 16 tiles, two per wave
+  // P1: dAqk = (dO v_new^T) * causal; 16 tiles, two per wave.  Its MFMAs carry the loads of
+  // b, k and dWp (staged right after it); w, v and dv_new go out during P2a, which stages them
+  // next: each phase's loads then overlap the MFMAs of the phase before their use.
   static_assert(NW == 8, "P1 assumes two dAqk tiles per wave");
-  constexpr int NITEMS = 3 * NRT + 3 * NIT, NSLOT = 2 * NKB;
+  constexpr int NITEMS1 = 3 * NRT, NITEMS2 = 3 * NIT, NSLOT = 2 * NKB;
 #pragma unroll
   for (int m2 = 0; m2 < 2; ++m2) {
     const int t = wv + NW * m2, ti = t >> 2, tj = t & 3;
@@ -647,7 +649,7 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
 #pragma unroll
       for (int sl = m2 * NKB + kb; sl < m2 * NKB + kb + KSTEP; ++sl)
 #pragma unroll
-        for (int item = NITEMS * sl / NSLOT; item < NITEMS * (sl + 1) / NSLOT; ++item) prefetch(item);
+        for (int item = NITEMS1 * sl / NSLOT; item < NITEMS1 * (sl + 1) / NSLOT; ++item) prefetch(item);
       __builtin_amdgcn_sched_barrier(0);
     }
     drain(acc);
@@ -683,7 +685,18 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
     const float* ar = sX2 + (16 * ti + r) * LD + 4 * g;
     const float* br = sX1 + (16 * tj + r) * LD + 4 * g;
     accA[m2] = f4{0.f, 0.f, 0.f, 0.f};
-    mma_chain<B3, NKB>(accA[m2], 0, [&](int kb) { return ld4(ar + 16 * kb); }, [&](int kb) { return ld4(br + 16 * kb); });
+    constexpr int KSTEP = B3 == DOT_HIGHEST ? 1 : 2;      // the block steps of mma_chain<B3, NKB>
+#pragma unroll
+    for (int kb = 0; kb < NKB; kb += KSTEP) {
+      if constexpr (KSTEP == 1) mma16<B3>(accA[m2], ld4(ar + 16 * kb), ld4(br + 16 * kb));
+      else mma32<B3>(accA[m2], ld4(ar + 16 * kb), ld4(br + 16 * kb), ld4(ar + 16 * kb + 16), ld4(br + 16 * kb + 16));
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int sl = m2 * NKB + kb; sl < m2 * NKB + kb + KSTEP; ++sl)
+#pragma unroll
+        for (int item = NITEMS2 * sl / NSLOT; item < NITEMS2 * (sl + 1) / NSLOT; ++item) prefetch(NITEMS1 + item);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     drain(accA[m2]);
   }
   __syncthreads();

@@ -38,13 +38,13 @@ namespace gdn2 {
 //   window A (after the state h_pre is in LDS):
 //     V waves 0-3   v_new tile i = U - Wp[tile i, :] h_pre  (full key contraction, no
 //                   cross-wave reduction), written to LDS (and, for the backward, global)
-//     O waves 4-7   read h_pre from LDS for their output tile
+//     O waves 4-7   s Qg[tile j, :] h_pre for their output tile j
 //   window B (after v_new is in LDS):
 //     every wave w < D/16   h rows of key tile w: h = san(e^gamma h + Kg^T v_new), to LDS
 //     O wave j      o tile j = san(s Qg[tile j, :] h_pre + Aqk[tile j, :] v_new)
-//                   (fwd/cd_slim.py:24-27), at the default priority while the state work
-//                   runs at a raised one, so it takes the MFMA pipe when that work leaves it
-//                   idle.
+//                   (fwd/cd_slim.py:24-27)
+//   The chain's work (V, state rows) runs at a raised priority and the output's at the
+//   default one, so the output takes the MFMA pipe where the chain leaves it idle.
 // h_pre in LDS is block kb = key tile in the MFMA result layout of the owning wave, which is
 // the B operand of Wp h and the A operand of h^T Qg^T; v_new tiles are in the B-operand
 // layout of Kg^T v_new, which is the A operand of v_new^T Aqk^T.  FA(Wp), FA(Qg), FA(Aqk),
@@ -187,6 +187,30 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
       if (a.v_new_f) stg4(a.v_new_f + tb + frag_blk(vb, ti, T) + 4 * l, vn);
       nx.uu = ld4(a.uT_f + tbn + frag_blk(vb, ti, T) + 4 * l);
     }
+    if constexpr (O) {
+      // s Qg h_pre needs only h_pre: issued here, at the default priority, so that it fills the
+      // MFMA pipe around the V wave's chain (and its LDS / drain latencies) instead of running
+      // alone after the state update
+      __builtin_amdgcn_s_setprio(0);
+      if constexpr (MODE == DOT_HIGHEST) {
+#pragma unroll
+        for (int kb = 0; kb < NH; ++kb) {
+          mma16<MODE>(acc, hb[kb], op.x[kb]);
+          GDN2_SCHED_FENCE();
+          nx.x[kb] = ld4(a.qg_f + tbn + frag_blk(J, kb, D) + 4 * l);
+          GDN2_SCHED_FENCE();
+        }
+      } else {
+#pragma unroll
+        for (int kb = 0; kb < NH; kb += 2) {
+          mma32<MODE>(acc, hb[kb], op.x[kb], hb[kb + 1], op.x[kb + 1]);
+          GDN2_SCHED_FENCE();
+          nx.x[kb] = ld4(a.qg_f + tbn + frag_blk(J, kb, D) + 4 * l);
+          nx.x[kb + 1] = ld4(a.qg_f + tbn + frag_blk(J, kb + 1, D) + 4 * l);
+          GDN2_SCHED_FENCE();
+        }
+      }
+    }
     __syncthreads();
     // ---- window B ----
     float4 vv[4];
@@ -234,13 +258,6 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
       f4 acc2 = {0.f, 0.f, 0.f, 0.f};
       if constexpr (MODE == DOT_HIGHEST) {
 #pragma unroll
-        for (int kb = 0; kb < NH; ++kb) {
-          mma16<MODE>(acc, hb[kb], op.x[kb]);
-          GDN2_SCHED_FENCE();
-          nx.x[kb] = ld4(a.qg_f + tbn + frag_blk(J, kb, D) + 4 * l);
-          GDN2_SCHED_FENCE();
-        }
-#pragma unroll
         for (int u = 0; u <= J; ++u) {
           mma16<MODE>(acc2, vv[u], op.aq[u]);
           GDN2_SCHED_FENCE();
@@ -248,14 +265,6 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
           GDN2_SCHED_FENCE();
         }
       } else {
-#pragma unroll
-        for (int kb = 0; kb < NH; kb += 2) {
-          mma32<MODE>(acc, hb[kb], op.x[kb], hb[kb + 1], op.x[kb + 1]);
-          GDN2_SCHED_FENCE();
-          nx.x[kb] = ld4(a.qg_f + tbn + frag_blk(J, kb, D) + 4 * l);
-          nx.x[kb + 1] = ld4(a.qg_f + tbn + frag_blk(J, kb + 1, D) + 4 * l);
-          GDN2_SCHED_FENCE();
-        }
 #pragma unroll
         for (int u = 0; u <= J; u += 2) {
           if (u + 1 <= J) mma32<MODE>(acc2, vv[u], op.aq[u], vv[u + 1], op.aq[u + 1]);
