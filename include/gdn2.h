@@ -81,12 +81,12 @@ typedef struct gdn2_desc {
  *                           the first part of each checkpoint block (state_ckpt = K: parts
  *                           0, K, .., K (n64 / K - 1), then the n64 % K parts left over as one
  *                           block, or as blocks of bt / 64 parts -- single parts without
- *                           damping -- when those are at most two), FRAG(h_pre^T) (cd_slim.py:22)
- *   VNEW  (B,H,n64, D*64)   v_new of each part, FRAG(v_new^T)                  (cd_slim.py:23)
- *   WP    (B,H,n64, 64*D)   W = A (b k e^gc) of each part, FRAG(W)              (cd_slim.py:17)
- *   KG    (B,H,n64, 64*D)   gated k, FRAG(Kg)                                   (cd_slim.py:20)
- *   QG    (B,H,n64, 64*D)   gated q, FRAG(Qg)                                   (cd_slim.py:21)
- *   GL    (B,H,n64,D)       gc (within the part) of the part's last row         (cd_slim.py:19)
+ *                           damping -- when those are at most two), FRAG(h_pre^T) (cd_slim.py:23)
+ *   VNEW  (B,H,n64, D*64)   v_new of each part, FRAG(v_new^T)                  (cd_slim.py:29)
+ *   WP    (B,H,n64, 64*D)   W = A (b k e^gc) of each part, FRAG(W)              (cd_slim.py:18)
+ *   KG    (B,H,n64, 64*D)   gated k, FRAG(Kg)                                   (cd_slim.py:22)
+ *   QG    (B,H,n64, 64*D)   gated q, FRAG(Qg)                                   (cd_slim.py:22)
+ *   GL    (B,H,n64,D)       gc (within the part) of the part's last row         (cd_slim.py:20)
  * FRAG(M) of an R x C matrix M is the MFMA fragment order the kernels load with one
  * coalesced float4 per lane: 16x16 blocks in row-major block order (C/16 blocks per block
  * row, 256 floats each); inside a block, floats [4 l, 4 l + 4) with l = r + 16 c hold
