@@ -17,7 +17,8 @@
 // float4 per lane and block (fragment layout, written by the WY kernel) and are prefetched
 // one chunk ahead into the second of two register sets; the chunk loop is unrolled by two so
 // the sets never need copying, and all prefetch loads are unconditional so the compiler's
-// vmcnt waits stay exact.  Per chunk: two workgroup barriers.
+// vmcnt waits stay exact.  Per chunk: two syncs of the waves on the chain (workgroup barriers
+// in the reverse scan; in the forward scan, whose output waves trail the chain, LDS counters).
 //
 // The chain is h -> v_new -> h (dh -> dv_new -> dh).  The forward output o, which needs
 // h_pre and v_new but feeds nothing back, is computed inside the forward scan by waves of
@@ -32,31 +33,40 @@
 
 namespace gdn2 {
 
-// Forward scan, with the output fused in when no residual is kept (OUT; in training the
-// output waves only carry their state rows).  Eight waves per workgroup (slice of 16 value
-// columns of one (batch, head)); per chunk two barriers:
-//   window A (after the state h_pre is in LDS):
-//     V waves 0-3   v_new tile i = U - Wp[tile i, :] h_pre  (full key contraction, no
-//                   cross-wave reduction), written to LDS (and, for the backward, global)
-//     O waves 4-7   s Qg[tile j, :] h_pre for their output tile j
-//   window B (after v_new is in LDS):
-//     every wave w < D/16   h rows of key tile w: h = san(e^gamma h + Kg^T v_new), to LDS
-//     O wave j      o tile j = san(s Qg[tile j, :] h_pre + Aqk[tile j, :] v_new)
-//                   (fwd/cd_slim.py:24-27)
-//   The chain's work (V, state rows) runs at a raised priority and the output's at the
-//   default one, so the output takes the MFMA pipe where the chain leaves it idle.
+// Forward scan, one workgroup per (batch, head, slice of 16 value columns), eight waves:
+//   chain waves 0..3  the recurrence.  Wave w computes v_new tile w = U - Wp[tile w, :] h_pre
+//                     (window A, full key contraction) and keeps the state rows of key tiles
+//                     kt(w, j) = w + 4 j (j < D/64) in registers, updated in window B:
+//                     h = san(e^gamma h + Kg^T v_new) (fwd/cd_slim.py:24-27).  Two syncs per
+//                     chunk among these four waves only (an LDS counter, below): after window A
+//                     (v_new complete in LDS) and after window B (the next h_pre complete).
+//   output waves 4..7 (OUT) o tile j = san(s Qg[tile j, :] h_pre + Aqk[tile j, :] v_new)
+//                     (fwd/cd_slim.py:25,28), trailing the chain: a chunk's h_pre and v_new are
+//                     read as soon as its window-A sync has passed, and the MFMAs run after the
+//                     reads are released, at the default priority, in whatever gaps the chain
+//                     leaves in the MFMA pipe (the chain waves run at a raised one).
+// h_pre and v_new are double-buffered in LDS by chunk parity; the chain writes a buffer only
+// after every output wave has released the chunk that used it before.  All waits are bounded
+// spins (a wave that runs out of spins stops waiting and finishes, so the grid always drains;
+// the results are then wrong, which no in-range input can cause).  Syncs are LDS counters
+// with release increments and acquire loads (workgroup scope): every LDS write before a
+// release is visible to a wave whose acquire load sees the increment.
 // h_pre in LDS is block kb = key tile in the MFMA result layout of the owning wave, which is
 // the B operand of Wp h and the A operand of h^T Qg^T; v_new tiles are in the B-operand
 // layout of Kg^T v_new, which is the A operand of v_new^T Aqk^T.  FA(Wp), FA(Qg), FA(Aqk),
 // FA(Kg^T), FA(U^T) blocks are loaded as stored (one float4 per lane), one chunk ahead into
 // the second of two register sets, interleaved with the MFMAs.
 template <int NH>
-struct FwdOps {
-  float4 x[NH];    // V: FA(Wp) block (i, kb); O: FA(Qg) block (j, kb)
-  float4 aq[4];    // O: FA(Aqk) block (j, u), u <= j
-  float4 uu;       // V: FA(U^T) block (slice, i)
-  float4 kg[4];    // state rows: FA(Kg^T) block (w, u)
-  float4 gm;       // state rows: gamma[16w + 4g .. +3]
+struct ChainOps {
+  float4 x[NH];            // FA(Wp) block (w, kb)
+  float4 uu;               // FA(U^T) block (slice, w)
+  float4 kg[NH / 4][4];    // FA(Kg^T) blocks (kt(w, j), u)
+  float4 gm[NH / 4];       // gamma of key tile kt(w, j)
+};
+template <int NH>
+struct OutOps {
+  float4 x[NH];            // FA(Qg) block (j, kb)
+  float4 aq[4];            // FA(Aqk) block (j, u), u <= j
 };
 
 // Prefetch loads for the next chunk are issued in small groups between the MFMA groups of the
@@ -65,26 +75,61 @@ struct FwdOps {
 // stall overlaps the MFMAs already in flight.
 #define GDN2_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
 
-// ROLE < 0: V wave (v_new tile w); ROLE = j >= 0: O wave of output tile j (wave 4 + j).
-// OUT = false: no output (the O waves keep only their state rows and the barriers; the
-// output is then computed chunk-parallel from h_pre and v_new, gdn2_fwd.hip).
-// With Cfg::group = G > 1 (bt = 64 G, wy_eps > 0) the state rows also go to sHd after each part
-// j < G - 1 as the damped state h_d(j+1) = state_update(h_d(j), gamma, (1 - eps) Kg^T v_new)
-// (h_d(0) = h), from which the V waves compute the next part's v_new (the O waves and the
-// state update keep h).
-template <int D, int MODE, bool OUT, int ROLE>
-__device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, float4* sHd, float4* sV) {
-  constexpr int NH = D / 16, NVB = D / 16;
-  constexpr bool V = ROLE < 0, O = !V && OUT;
-  constexpr int J = V ? 0 : ROLE;
-  const float clip = a.cfg.clip, scale = a.cfg.scale;
+// Workgroup-local syncs on monotonic LDS counters.
+constexpr int SCAN_SPIN_MAX = 1 << 22;
+// One increment per wave: lane 0 alone issues the add (an add from every active lane would
+// count the wave's active lanes).
+__device__ __forceinline__ void lds_release_add(unsigned* ctr) {
+  if (lane_id() == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+// Waits until *ctr >= target; ok turns false (and stays false, so later waits return at once)
+// when the spin budget runs out.  SLEEP: pause between polls (the output waves, which wait
+// long and should leave the issue slots to the chain); the chain waves poll back to back.
+template <bool SLEEP>
+__device__ __forceinline__ void lds_acquire_wait(unsigned* ctr, unsigned target, bool& ok) {
+  if (!ok) return;
+  for (int i = 0; i < SCAN_SPIN_MAX; ++i) {
+    if (__hip_atomic_load(ctr, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) return;
+    if constexpr (SLEEP) __builtin_amdgcn_s_sleep(1);
+  }
+  ok = false;
+}
+// The same for a counter whose last observed value (seen, from an acquire load of this wave)
+// may already satisfy the target: then the sync has happened and nothing is read.
+__device__ __forceinline__ void lds_acquire_wait_cached(unsigned* ctr, unsigned target, unsigned& seen, bool& ok) {
+  if (!ok || seen >= target) return;
+  for (int i = 0; i < SCAN_SPIN_MAX; ++i) {
+    seen = __hip_atomic_load(ctr, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (seen >= target) return;
+  }
+  ok = false;
+}
+
+struct ScanFwdShared {
+  unsigned cbar;           // chain syncs, 4 per sync point: k = 0 after the initial state is in
+                           // LDS, k = 2 c + 1 after chunk c's window A, k = 2 c + 2 after its B
+  unsigned odone;          // output waves' releases: 4 per chunk
+};
+// cbar once sync point k has passed
+__device__ __forceinline__ unsigned cbar_at(int k) { return 4u * (unsigned)(k + 1); }
+
+// Chain wave w.  With Cfg::group = G > 1 (bt = 64 G, wy_eps > 0) the state rows also go to sHd
+// after each part j < G - 1 as the damped state h_d(j+1) = state_update(h_d(j), gamma,
+// (1 - eps) Kg^T v_new) (h_d(0) = h), from which the next part's v_new is computed (the output
+// and the state update keep h).
+template <int D, int MODE, bool OUT>
+__device__ __forceinline__ void scan_fwd_chain(const ScanFwdArgs& a, ScanFwdShared* sh, float4* sH, float4* sHd,
+                                               float4* sV) {
+  constexpr int NH = D / 16, NVB = D / 16, NJ = NH / 4;
+  const float clip = a.cfg.clip;
   const int nc = a.nc;
   const int lin = xcd_remap(gridDim.x);
   const int vb = lin % NVB, bh = lin / NVB, c0 = 16 * vb;
   const int l = lane_id(), r = l & 15, g = l >> 4, w = wave_id();
-  const int ti = w & 3;                        // v_new tile of a V wave
-  constexpr bool OWNS = V || NH == 8;           // keeps key tile w of the state (w < NH)
+  auto kt = [&](int j) { return w + 4 * j; };
   auto base = [&](int c) { return (size_t)bh * nc + (c < nc ? c : nc - 1); };   // clamped chunk
+  bool ok = true;
+  unsigned odone_seen = 0;      // the output waves trail by about a chunk: one read serves several waits
 
   // A set reset byte zeroes the state entering that chunk.  No load on the sequential path:
   // lane l holds the bytes of chunks 64 m + l of the current block m (fl_cur) and of the next
@@ -95,7 +140,6 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
     return (has_reset && c < nc) ? (int)a.reset[(size_t)bh * nc + c] : 0;
   };
   int fl_cur = load_flags(0), fl_nxt = load_flags(1);
-  // the byte of chunk c (c >= 1 ascending, one call per step), rotating the blocks as c enters one
   auto reset_at = [&](int c) -> int {
     if (!has_reset || c >= nc) return 0;
     if ((c & 63) == 0) {
@@ -104,219 +148,274 @@ __device__ __forceinline__ void scan_fwd_role(const ScanFwdArgs& a, float4* sH, 
     }
     return __builtin_amdgcn_readlane(fl_cur, c & 63);
   };
-  f4 h = {0.f, 0.f, 0.f, 0.f};
-  if (OWNS) {
+  f4 h[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    h[j] = f4{0.f, 0.f, 0.f, 0.f};
     if (a.h0 && !(has_reset && __builtin_amdgcn_readlane(fl_cur, 0))) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) h[e] = a.h0[(size_t)bh * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r];
+      for (int e = 0; e < 4; ++e) h[j][e] = a.h0[(size_t)bh * D * D + (size_t)(16 * kt(j) + 4 * g + e) * D + c0 + r];
     }
-    sH[w * WAVE + l] = f4_to_float4(h);
+    sH[kt(j) * WAVE + l] = f4_to_float4(h[j]);     // buffer 0: h_pre of chunk 0
   }
+  // sync point 0: every chain wave reads every key tile of chunk 0's h_pre
+  lds_release_add(&sh->cbar);
+  lds_acquire_wait<false>(&sh->cbar, cbar_at(0), ok);
 
-  auto load_all = [&](FwdOps<NH>& op, int c) {
-    const size_t tb = base(c) * T * D, sb = base(c) * T * T;
-    if constexpr (V) {
+  auto load_all = [&](ChainOps<NH>& op, int c) {
+    const size_t tb = base(c) * T * D;
 #pragma unroll
-      for (int kb = 0; kb < NH; ++kb) op.x[kb] = ld4(a.wp_f + tb + frag_blk(ti, kb, D) + 4 * l);
-      op.uu = ld4(a.uT_f + tb + frag_blk(vb, ti, T) + 4 * l);
-    }
-    if constexpr (O) {
+    for (int kb = 0; kb < NH; ++kb) op.x[kb] = ld4(a.wp_f + tb + frag_blk(w, kb, D) + 4 * l);
+    op.uu = ld4(a.uT_f + tb + frag_blk(vb, w, T) + 4 * l);
 #pragma unroll
-      for (int kb = 0; kb < NH; ++kb) op.x[kb] = ld4(a.qg_f + tb + frag_blk(J, kb, D) + 4 * l);
+    for (int j = 0; j < NJ; ++j) {
 #pragma unroll
-      for (int u = 0; u <= J; ++u) op.aq[u] = ld4(a.aqk_f + sb + frag_blk(J, u, T) + 4 * l);
-    }
-    if constexpr (OWNS) {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) op.kg[u] = ld4(a.kgT_f + tb + frag_blk(w, u, T) + 4 * l);
-      op.gm = ld4(a.gl + base(c) * D + 16 * w + 4 * g);
+      for (int u = 0; u < 4; ++u) op.kg[j][u] = ld4(a.kgT_f + tb + frag_blk(kt(j), u, T) + 4 * l);
+      op.gm[j] = ld4(a.gl + base(c) * D + 16 * kt(j) + 4 * g);
     }
   };
 
-  // Cfg::group = G > 1: chunk c is part c % G of a damped big chunk; the state rows keep the
-  // damped state h_d of the next part in registers (hdr) and pass it to the V waves through sHd
   const int G = a.cfg.group;
   const float ome = a.cfg.ome;
-  f4 hdr = {0.f, 0.f, 0.f, 0.f};
+  f4 hdr[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) hdr[j] = f4{0.f, 0.f, 0.f, 0.f};
   // checkpoint blocks: the next chunk that starts one and its slot (no division per chunk)
   const CkptBlocks ckb(nc, a.ckpt, G);
   int ck_next = 0, ck_slot = 0;
-  // the loop below is unrolled by two from c = 0 (register sets A / B); odd is c's parity
-  auto step = [&](const FwdOps<NH>& op, int c, FwdOps<NH>& nx, int cn, auto odd) {
-    (void)odd;
+  __builtin_amdgcn_s_setprio(2);
+  auto step = [&](const ChainOps<NH>& op, int c, ChainOps<NH>& nx, int cn, auto odd) {
+    constexpr int buf = decltype(odd)::value ? 1 : 0;      // c & 1
     const int part = G > 1 ? c % G : 0;
     const size_t ch = (size_t)bh * nc + c, tb = ch * T * D;
-    const size_t tbn = base(cn) * T * D, sbn = base(cn) * T * T;
+    const size_t tbn = base(cn) * T * D;
     const int rst_next = reset_at(cn);
-    if (OWNS && a.h_pre_f && c == ck_next) {
-      stg4(a.h_pre_f + ((size_t)bh * ckb.nblk + ck_slot) * D * D + frag_blk(vb, w, D) + 4 * l, f4_to_float4(h));
+    float4* sHc = sH + buf * NH * WAVE;            // h_pre of this chunk
+    float4* sHn = sH + (1 - buf) * NH * WAVE;      // h_pre of the next one
+    float4* sVc = sV + buf * 4 * WAVE;
+    if (a.h_pre_f && c == ck_next) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        stg4(a.h_pre_f + ((size_t)bh * ckb.nblk + ck_slot) * D * D + frag_blk(vb, kt(j), D) + 4 * l, f4_to_float4(h[j]));
       ck_next += ckb.len(ck_slot);
       ++ck_slot;
     }
-    // ---- window A ----
+    // ---- window A: v_new tile w ----
     float4 hb[NH];
-    if constexpr (V || O) {
-      const float4* src = (V && part > 0) ? sHd : sH;
+    {
+      const float4* src = part > 0 ? sHd : sHc;
 #pragma unroll
       for (int kb = 0; kb < NH; ++kb) hb[kb] = src[kb * WAVE + l];
     }
     f4 acc = {0.f, 0.f, 0.f, 0.f};
-    if constexpr (V) {
-      __builtin_amdgcn_s_setprio(2);
-      if constexpr (MODE == DOT_HIGHEST) {
+    if constexpr (MODE == DOT_HIGHEST) {
 #pragma unroll
-        for (int kb = 0; kb < NH; ++kb) {
-          mma16<MODE>(acc, op.x[kb], hb[kb]);
-          GDN2_SCHED_FENCE();
-          nx.x[kb] = ld4(a.wp_f + tbn + frag_blk(ti, kb, D) + 4 * l);
-          GDN2_SCHED_FENCE();
-        }
-      } else {
-#pragma unroll
-        for (int kb = 0; kb < NH; kb += 2) {
-          mma32<MODE>(acc, op.x[kb], hb[kb], op.x[kb + 1], hb[kb + 1]);
-          GDN2_SCHED_FENCE();
-          nx.x[kb] = ld4(a.wp_f + tbn + frag_blk(ti, kb, D) + 4 * l);
-          nx.x[kb + 1] = ld4(a.wp_f + tbn + frag_blk(ti, kb + 1, D) + 4 * l);
-          GDN2_SCHED_FENCE();
-        }
+      for (int kb = 0; kb < NH; ++kb) {
+        mma16<MODE>(acc, op.x[kb], hb[kb]);
+        GDN2_SCHED_FENCE();
+        nx.x[kb] = ld4(a.wp_f + tbn + frag_blk(w, kb, D) + 4 * l);
+        GDN2_SCHED_FENCE();
       }
-      drain(acc);
-      const float4 vn = sub4(op.uu, f4_to_float4(acc));
-      sV[ti * WAVE + l] = vn;
-      if (a.v_new_f) stg4(a.v_new_f + tb + frag_blk(vb, ti, T) + 4 * l, vn);
-      nx.uu = ld4(a.uT_f + tbn + frag_blk(vb, ti, T) + 4 * l);
-    }
-    if constexpr (O) {
-      // s Qg h_pre needs only h_pre: issued here, at the default priority, so that it fills the
-      // MFMA pipe around the V wave's chain (and its LDS / drain latencies) instead of running
-      // alone after the state update
-      __builtin_amdgcn_s_setprio(0);
-      if constexpr (MODE == DOT_HIGHEST) {
+    } else {
 #pragma unroll
-        for (int kb = 0; kb < NH; ++kb) {
-          mma16<MODE>(acc, hb[kb], op.x[kb]);
-          GDN2_SCHED_FENCE();
-          nx.x[kb] = ld4(a.qg_f + tbn + frag_blk(J, kb, D) + 4 * l);
-          GDN2_SCHED_FENCE();
-        }
-      } else {
-#pragma unroll
-        for (int kb = 0; kb < NH; kb += 2) {
-          mma32<MODE>(acc, hb[kb], op.x[kb], hb[kb + 1], op.x[kb + 1]);
-          GDN2_SCHED_FENCE();
-          nx.x[kb] = ld4(a.qg_f + tbn + frag_blk(J, kb, D) + 4 * l);
-          nx.x[kb + 1] = ld4(a.qg_f + tbn + frag_blk(J, kb + 1, D) + 4 * l);
-          GDN2_SCHED_FENCE();
-        }
+      for (int kb = 0; kb < NH; kb += 2) {
+        mma32<MODE>(acc, op.x[kb], hb[kb], op.x[kb + 1], hb[kb + 1]);
+        GDN2_SCHED_FENCE();
+        nx.x[kb] = ld4(a.wp_f + tbn + frag_blk(w, kb, D) + 4 * l);
+        nx.x[kb + 1] = ld4(a.wp_f + tbn + frag_blk(w, kb + 1, D) + 4 * l);
+        GDN2_SCHED_FENCE();
       }
     }
-    __syncthreads();
-    // ---- window B ----
+    drain(acc);
+    const float4 vn = sub4(op.uu, f4_to_float4(acc));
+    // the output waves have released chunk c - 2, which used this v_new buffer
+    if constexpr (OUT) lds_acquire_wait_cached(&sh->odone, 4u * (unsigned)(c > 1 ? c - 1 : 0), odone_seen, ok);
+    sVc[w * WAVE + l] = vn;
+    if (a.v_new_f) stg4(a.v_new_f + tb + frag_blk(vb, w, T) + 4 * l, vn);
+    nx.uu = ld4(a.uT_f + tbn + frag_blk(vb, w, T) + 4 * l);
+    lds_release_add(&sh->cbar);
+    lds_acquire_wait<false>(&sh->cbar, cbar_at(2 * c + 1), ok);
+    // ---- window B: the state rows of key tiles kt(w, j) ----
     float4 vv[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) vv[u] = sV[u * WAVE + l];
-    if constexpr (OWNS) {
-      __builtin_amdgcn_s_setprio(2);
-      // Kg^T v_new: the same chain as the backward's state recompute (gdn2_bwd.hip)
-      f4 hn = {0.f, 0.f, 0.f, 0.f};
-      if constexpr (MODE == DOT_HIGHEST) {
+    for (int u = 0; u < 4; ++u) vv[u] = sVc[u * WAVE + l];
+    f4 hn[NJ];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          mma16<MODE>(hn, op.kg[u], vv[u]);
-          GDN2_SCHED_FENCE();
-          nx.kg[u] = ld4(a.kgT_f + tbn + frag_blk(w, u, T) + 4 * l);
-          GDN2_SCHED_FENCE();
-        }
-      } else {
+    for (int j = 0; j < NJ; ++j) hn[j] = f4{0.f, 0.f, 0.f, 0.f};
+    // Kg^T v_new: the same chain per key tile as the backward's state recompute (gdn2_bwd.hip);
+    // the key tiles' chains interleaved
+    if constexpr (MODE == DOT_HIGHEST) {
 #pragma unroll
-        for (int u = 0; u < 4; u += 2) {
-          mma32<MODE>(hn, op.kg[u], vv[u], op.kg[u + 1], vv[u + 1]);
-          GDN2_SCHED_FENCE();
-          nx.kg[u] = ld4(a.kgT_f + tbn + frag_blk(w, u, T) + 4 * l);
-          nx.kg[u + 1] = ld4(a.kgT_f + tbn + frag_blk(w, u + 1, T) + 4 * l);
-          GDN2_SCHED_FENCE();
-        }
+      for (int u = 0; u < 4; ++u) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) mma16<MODE>(hn[j], op.kg[j][u], vv[u]);
+        GDN2_SCHED_FENCE();
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) nx.kg[j][u] = ld4(a.kgT_f + tbn + frag_blk(kt(j), u, T) + 4 * l);
+        GDN2_SCHED_FENCE();
       }
-      drain(hn);
-      const float gmv[4] = {op.gm.x, op.gm.y, op.gm.z, op.gm.w};
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; u += 2) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) mma32<MODE>(hn[j], op.kg[j][u], vv[u], op.kg[j][u + 1], vv[u + 1]);
+        GDN2_SCHED_FENCE();
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          nx.kg[j][u] = ld4(a.kgT_f + tbn + frag_blk(kt(j), u, T) + 4 * l);
+          nx.kg[j][u + 1] = ld4(a.kgT_f + tbn + frag_blk(kt(j), u + 1, T) + 4 * l);
+        }
+        GDN2_SCHED_FENCE();
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) drain(hn[j]);
+    // the output waves have released chunk c - 1, whose h_pre buffer the next h_pre overwrites
+    if constexpr (OUT) lds_acquire_wait_cached(&sh->odone, 4u * (unsigned)c, odone_seen, ok);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const float gmv[4] = {op.gm[j].x, op.gm[j].y, op.gm[j].z, op.gm[j].w};
       if (part < G - 1) {
         // h_d(part + 1) = san(e^gamma h_d(part) + (1 - eps) Kg^T v_new), h_d(0) = h(0); a reset
         // byte on the next part zeroes it with the state (the rest of the big chunk then starts
         // from zero, damped and true state alike)
-        const f4 hb0 = part == 0 ? h : hdr;
+        const f4 hb0 = part == 0 ? h[j] : hdr[j];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) hdr[e] = rst_next ? 0.f : state_update(hb0[e], gmv[e], ome * hn[e], clip);
-        sHd[w * WAVE + l] = f4_to_float4(hdr);   // read in the next step's window A, after its barrier
+        for (int e = 0; e < 4; ++e) hdr[j][e] = rst_next ? 0.f : state_update(hb0[e], gmv[e], ome * hn[j][e], clip);
+        sHd[kt(j) * WAVE + l] = f4_to_float4(hdr[j]);   // read in the next step's window A, after its sync
       }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) h[e] = state_update(h[e], gmv[e], hn[e], clip);
-      nx.gm = ld4(a.gl + base(cn) * D + 16 * w + 4 * g);
+      for (int e = 0; e < 4; ++e) h[j][e] = state_update(h[j][e], gmv[e], hn[j][e], clip);
+      nx.gm[j] = ld4(a.gl + base(cn) * D + 16 * kt(j) + 4 * g);
+      if (rst_next) h[j] = f4{0.f, 0.f, 0.f, 0.f};
+      sHn[kt(j) * WAVE + l] = f4_to_float4(h[j]);
     }
-    if constexpr (O) {
-      __builtin_amdgcn_s_setprio(0);
-      f4 acc2 = {0.f, 0.f, 0.f, 0.f};
-      if constexpr (MODE == DOT_HIGHEST) {
-#pragma unroll
-        for (int u = 0; u <= J; ++u) {
-          mma16<MODE>(acc2, vv[u], op.aq[u]);
-          GDN2_SCHED_FENCE();
-          nx.aq[u] = ld4(a.aqk_f + sbn + frag_blk(J, u, T) + 4 * l);
-          GDN2_SCHED_FENCE();
-        }
-      } else {
-#pragma unroll
-        for (int u = 0; u <= J; u += 2) {
-          if (u + 1 <= J) mma32<MODE>(acc2, vv[u], op.aq[u], vv[u + 1], op.aq[u + 1]);
-          else mma16<MODE>(acc2, vv[u], op.aq[u]);
-          GDN2_SCHED_FENCE();
-          nx.aq[u] = ld4(a.aqk_f + sbn + frag_blk(J, u, T) + 4 * l);
-          if (u + 1 <= J) nx.aq[u + 1] = ld4(a.aqk_f + sbn + frag_blk(J, u + 1, T) + 4 * l);
-          GDN2_SCHED_FENCE();
-        }
-      }
-      drain(acc, acc2);
-      // lane (r, g): o[16 J + r][c0 + 4 g .. + 3]
-      stg4(a.o + ((size_t)bh * a.cfg.seq_ld + (size_t)c * T) * D + (size_t)(16 * J + r) * D + c0 + 4 * g,
-           make_float4(sanitize(scale * acc[0] + acc2[0], clip), sanitize(scale * acc[1] + acc2[1], clip),
-                       sanitize(scale * acc[2] + acc2[2], clip), sanitize(scale * acc[3] + acc2[3], clip)));
-    }
-    // every wave has read h_pre (window A) before the first barrier, so the new state may
-    // overwrite it here
-    if (OWNS) {
-      if (rst_next) h = f4{0.f, 0.f, 0.f, 0.f};
-      sH[w * WAVE + l] = f4_to_float4(h);
-    }
-    __syncthreads();
+    lds_release_add(&sh->cbar);
+    lds_acquire_wait<false>(&sh->cbar, cbar_at(2 * c + 2), ok);
   };
 
-  FwdOps<NH> A, B;
+  ChainOps<NH> A, B;
   load_all(A, 0);
-  __syncthreads();
   int c = 0;
   for (; c + 1 < nc; c += 2) {
     step(A, c, B, c + 1, std::false_type{});
     step(B, c + 1, A, c + 2, std::true_type{});
   }
   if (c < nc) step(A, c, B, c + 1, std::false_type{});
-  if (OWNS) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) a.hf[(size_t)bh * D * D + (size_t)(16 * w + 4 * g + e) * D + c0 + r] = h[e];
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) a.hf[(size_t)bh * D * D + (size_t)(16 * kt(j) + 4 * g + e) * D + c0 + r] = h[j][e];
+}
+
+// Output wave J (wave 4 + J).  J is a compile-time parameter: the causal Aqk v_new chain's
+// length depends on it, and a runtime branch between the MFMAs of a chain would let the
+// compiler copy the accumulator at the merge point, right after an (opaque) asm MFMA.
+template <int D, int MODE, int J>
+__device__ __forceinline__ void scan_fwd_out(const ScanFwdArgs& a, ScanFwdShared* sh, const float4* sH,
+                                             const float4* sV) {
+  constexpr int NH = D / 16, NVB = D / 16;
+  const float clip = a.cfg.clip, scale = a.cfg.scale;
+  const int nc = a.nc;
+  const int lin = xcd_remap(gridDim.x);
+  const int vb = lin % NVB, bh = lin / NVB, c0 = 16 * vb;
+  const int l = lane_id(), r = l & 15, g = l >> 4;
+  auto base = [&](int c) { return (size_t)bh * nc + (c < nc ? c : nc - 1); };
+  bool ok = true;
+  auto load_all = [&](OutOps<NH>& op, int c) {
+    const size_t tb = base(c) * T * D, sb = base(c) * T * T;
+#pragma unroll
+    for (int kb = 0; kb < NH; ++kb) op.x[kb] = ld4(a.qg_f + tb + frag_blk(J, kb, D) + 4 * l);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (u <= J) op.aq[u] = ld4(a.aqk_f + sb + frag_blk(J, u, T) + 4 * l);
+  };
+  auto step = [&](const OutOps<NH>& op, int c, OutOps<NH>& nx, int cn, auto odd) {
+    constexpr int buf = decltype(odd)::value ? 1 : 0;
+    const size_t tbn = base(cn) * T * D, sbn = base(cn) * T * T;
+    // this chunk's h_pre and v_new are complete once its window-A sync has passed
+    lds_acquire_wait<true>(&sh->cbar, cbar_at(2 * c + 1), ok);
+    float4 hb[NH], vv[4];
+#pragma unroll
+    for (int kb = 0; kb < NH; ++kb) hb[kb] = sH[buf * NH * WAVE + kb * WAVE + l];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) vv[u] = u <= J ? sV[buf * 4 * WAVE + u * WAVE + l] : make_float4(0.f, 0.f, 0.f, 0.f);
+    lds_release_add(&sh->odone);       // the release waits for the reads above
+    f4 acc = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (MODE == DOT_HIGHEST) {
+#pragma unroll
+      for (int kb = 0; kb < NH; ++kb) {
+        mma16<MODE>(acc, hb[kb], op.x[kb]);
+        GDN2_SCHED_FENCE();
+        nx.x[kb] = ld4(a.qg_f + tbn + frag_blk(J, kb, D) + 4 * l);
+        GDN2_SCHED_FENCE();
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (u > J) continue;
+        mma16<MODE>(acc2, vv[u], op.aq[u]);
+        GDN2_SCHED_FENCE();
+        nx.aq[u] = ld4(a.aqk_f + sbn + frag_blk(J, u, T) + 4 * l);
+        GDN2_SCHED_FENCE();
+      }
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < NH; kb += 2) {
+        mma32<MODE>(acc, hb[kb], op.x[kb], hb[kb + 1], op.x[kb + 1]);
+        GDN2_SCHED_FENCE();
+        nx.x[kb] = ld4(a.qg_f + tbn + frag_blk(J, kb, D) + 4 * l);
+        nx.x[kb + 1] = ld4(a.qg_f + tbn + frag_blk(J, kb + 1, D) + 4 * l);
+        GDN2_SCHED_FENCE();
+      }
+#pragma unroll
+      for (int u = 0; u < 4; u += 2) {
+        if (u > J) continue;
+        if (u + 1 <= J) mma32<MODE>(acc2, vv[u], op.aq[u], vv[u + 1], op.aq[u + 1]);
+        else mma16<MODE>(acc2, vv[u], op.aq[u]);
+        GDN2_SCHED_FENCE();
+        nx.aq[u] = ld4(a.aqk_f + sbn + frag_blk(J, u, T) + 4 * l);
+        if (u + 1 <= J) nx.aq[u + 1] = ld4(a.aqk_f + sbn + frag_blk(J, u + 1, T) + 4 * l);
+        GDN2_SCHED_FENCE();
+      }
+    }
+    drain(acc, acc2);
+    // lane (r, g): o[16 J + r][c0 + 4 g .. + 3]
+    stg4(a.o + ((size_t)bh * a.cfg.seq_ld + (size_t)c * T) * D + (size_t)(16 * J + r) * D + c0 + 4 * g,
+         make_float4(sanitize(scale * acc[0] + acc2[0], clip), sanitize(scale * acc[1] + acc2[1], clip),
+                     sanitize(scale * acc[2] + acc2[2], clip), sanitize(scale * acc[3] + acc2[3], clip)));
+  };
+  OutOps<NH> A, B;
+  load_all(A, 0);
+  int c = 0;
+  for (; c + 1 < nc; c += 2) {
+    step(A, c, B, c + 1, std::false_type{});
+    step(B, c + 1, A, c + 2, std::true_type{});
   }
+  if (c < nc) step(A, c, B, c + 1, std::false_type{});
 }
 
 template <int D, int MODE, bool OUT>
 __global__ __launch_bounds__(8 * WAVE) void scan_fwd_kernel(ScanFwdArgs a) {
   constexpr int NH = D / 16;
-  __shared__ float4 sH[NH * WAVE];     // h_pre of the current chunk, [key tile][lane]
-  __shared__ float4 sHd[NH * WAVE];    // the damped state of the next part (Cfg::group)
-  __shared__ float4 sV[4 * WAVE];      // v_new tiles, [token tile][lane]
-  switch (wave_id()) {
-    case 4: scan_fwd_role<D, MODE, OUT, 0>(a, sH, sHd, sV); break;
-    case 5: scan_fwd_role<D, MODE, OUT, 1>(a, sH, sHd, sV); break;
-    case 6: scan_fwd_role<D, MODE, OUT, 2>(a, sH, sHd, sV); break;
-    case 7: scan_fwd_role<D, MODE, OUT, 3>(a, sH, sHd, sV); break;
-    default: scan_fwd_role<D, MODE, OUT, -1>(a, sH, sHd, sV); break;
+  __shared__ float4 sH[2 * NH * WAVE];     // h_pre by chunk parity, [buffer][key tile][lane]
+  __shared__ float4 sHd[NH * WAVE];        // the damped state of the next part (Cfg::group)
+  __shared__ float4 sV[2 * 4 * WAVE];      // v_new tiles by chunk parity, [buffer][token tile][lane]
+  __shared__ ScanFwdShared sh;
+  if (threadIdx.x == 0) {
+    sh.cbar = 0;
+    sh.odone = 0;
+  }
+  __syncthreads();
+  if constexpr (OUT) {
+    switch (wave_id()) {
+      case 4: scan_fwd_out<D, MODE, 0>(a, &sh, sH, sV); break;
+      case 5: scan_fwd_out<D, MODE, 1>(a, &sh, sH, sV); break;
+      case 6: scan_fwd_out<D, MODE, 2>(a, &sh, sH, sV); break;
+      case 7: scan_fwd_out<D, MODE, 3>(a, &sh, sH, sV); break;
+      default: scan_fwd_chain<D, MODE, OUT>(a, &sh, sH, sHd, sV); break;
+    }
+  } else {
+    if (wave_id() < 4) scan_fwd_chain<D, MODE, OUT>(a, &sh, sH, sHd, sV);
   }
 }
 
