@@ -46,7 +46,8 @@ namespace gdn2 {
 //                     reads are released, at the default priority, in whatever gaps the chain
 //                     leaves in the MFMA pipe (the chain waves run at a raised one).
 // h_pre and v_new are double-buffered in LDS by chunk parity; the chain writes a buffer only
-// after every output wave has released the chunk that used it before.  All waits are bounded
+// after every output wave has released the chunk that used it before (each output wave counts
+// its releases on a counter of its own, and the chain checks all four).  All waits are bounded
 // spins (a wave that runs out of spins stops waiting and finishes, so the grid always drains;
 // the results are then wrong, which no in-range input can cause).  Syncs are LDS counters
 // with release increments and acquire loads (workgroup scope): every LDS write before a
@@ -94,13 +95,25 @@ __device__ __forceinline__ void lds_acquire_wait(unsigned* ctr, unsigned target,
   }
   ok = false;
 }
-// The same for a counter whose last observed value (seen, from an acquire load of this wave)
-// may already satisfy the target: then the sync has happened and nothing is read.
-__device__ __forceinline__ void lds_acquire_wait_cached(unsigned* ctr, unsigned target, unsigned& seen, bool& ok) {
+// Waits until each of the counters ctr[0 .. N-1] is >= target.  seen is the smallest value of
+// this wave's last read: when it already satisfies the target the sync has happened and
+// nothing is read.  Waves that are not in lockstep with one another (the output waves) release a
+// counter each: with one shared counter the increments of a wave that is ahead could stand in
+// for those of a wave that is behind.  (The chain waves share one counter: none of them passes
+// a sync point before all of them have released it, so its sum is exact.)  The N counters are
+// read with relaxed loads in one round trip, then an acquire fence on LDS orders what follows.
+template <int N>
+__device__ __forceinline__ void lds_acquire_wait_each(unsigned* ctr, unsigned target, unsigned& seen, bool& ok) {
   if (!ok || seen >= target) return;
   for (int i = 0; i < SCAN_SPIN_MAX; ++i) {
-    seen = __hip_atomic_load(ctr, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
-    if (seen >= target) return;
+    unsigned m = 0xffffffffu;
+#pragma unroll
+    for (int j = 0; j < N; ++j) m = min(m, __hip_atomic_load(ctr + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+    seen = m;
+    if (m >= target) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+      return;
+    }
   }
   ok = false;
 }
@@ -108,7 +121,7 @@ __device__ __forceinline__ void lds_acquire_wait_cached(unsigned* ctr, unsigned 
 struct ScanFwdShared {
   unsigned cbar;           // chain syncs, 4 per sync point: k = 0 after the initial state is in
                            // LDS, k = 2 c + 1 after chunk c's window A, k = 2 c + 2 after its B
-  unsigned odone;          // output waves' releases: 4 per chunk
+  unsigned odone[4];       // output wave J's releases: 1 per chunk
 };
 // cbar once sync point k has passed
 __device__ __forceinline__ unsigned cbar_at(int k) { return 4u * (unsigned)(k + 1); }
@@ -229,7 +242,7 @@ __device__ __forceinline__ void scan_fwd_chain(const ScanFwdArgs& a, ScanFwdShar
     drain(acc);
     const float4 vn = sub4(op.uu, f4_to_float4(acc));
     // the output waves have released chunk c - 2, which used this v_new buffer
-    if constexpr (OUT) lds_acquire_wait_cached(&sh->odone, 4u * (unsigned)(c > 1 ? c - 1 : 0), odone_seen, ok);
+    if constexpr (OUT) lds_acquire_wait_each<4>(sh->odone, (unsigned)(c > 1 ? c - 1 : 0), odone_seen, ok);
     sVc[w * WAVE + l] = vn;
     if (a.v_new_f) stg4(a.v_new_f + tb + frag_blk(vb, w, T) + 4 * l, vn);
     nx.uu = ld4(a.uT_f + tbn + frag_blk(vb, w, T) + 4 * l);
@@ -271,7 +284,7 @@ __device__ __forceinline__ void scan_fwd_chain(const ScanFwdArgs& a, ScanFwdShar
 #pragma unroll
     for (int j = 0; j < NJ; ++j) drain(hn[j]);
     // the output waves have released chunk c - 1, whose h_pre buffer the next h_pre overwrites
-    if constexpr (OUT) lds_acquire_wait_cached(&sh->odone, 4u * (unsigned)c, odone_seen, ok);
+    if constexpr (OUT) lds_acquire_wait_each<4>(sh->odone, (unsigned)c, odone_seen, ok);
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const float gmv[4] = {op.gm[j].x, op.gm[j].y, op.gm[j].z, op.gm[j].w};
@@ -340,7 +353,7 @@ __device__ __forceinline__ void scan_fwd_out(const ScanFwdArgs& a, ScanFwdShared
     for (int kb = 0; kb < NH; ++kb) hb[kb] = sH[buf * NH * WAVE + kb * WAVE + l];
 #pragma unroll
     for (int u = 0; u < 4; ++u) vv[u] = u <= J ? sV[buf * 4 * WAVE + u * WAVE + l] : make_float4(0.f, 0.f, 0.f, 0.f);
-    lds_release_add(&sh->odone);       // the release waits for the reads above
+    lds_release_add(&sh->odone[J]);    // the release waits for the reads above
     f4 acc = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
     if constexpr (MODE == DOT_HIGHEST) {
 #pragma unroll
@@ -403,7 +416,7 @@ __global__ __launch_bounds__(8 * WAVE) void scan_fwd_kernel(ScanFwdArgs a) {
   __shared__ ScanFwdShared sh;
   if (threadIdx.x == 0) {
     sh.cbar = 0;
-    sh.odone = 0;
+    sh.odone[0] = sh.odone[1] = sh.odone[2] = sh.odone[3] = 0;
   }
   __syncthreads();
   if constexpr (OUT) {
