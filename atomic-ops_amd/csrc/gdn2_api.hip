@@ -244,14 +244,14 @@ int gdn2_residual_layout(const gdn2_desc* d, size_t offsets[GDN2_RES_COUNT], siz
   return GDN2_OK;
 }
 
-// forward workspace (fragment layouts): [U^T | Kg^T | anchors (bs2 > 64 only)], and without a
-// residual also [Wp | Qg | Aqk | gl] (with a residual those live in it).
+// forward workspace (fragment layouts): [U^T | anchors (bs2 > 64 only)], and without a
+// residual also [Kg | Wp | Qg | Aqk | gl] (with a residual those live in it).
 size_t gdn2_fwd_workspace_bytes(const gdn2_desc* d, int with_residual) {
   if (with_residual ? validate_residual(d) : validate(d)) return 0;
   const Dims x = dims(d);
-  size_t n = 2 * align_up(x.n_chunks * x.tD * 4) + anchor_bytes(d);
+  size_t n = align_up(x.n_chunks * x.tD * 4) + anchor_bytes(d);
   if (!with_residual)
-    n += 2 * align_up(x.n_chunks * x.tD * 4) + align_up(x.n_chunks * x.tT * 4) + align_up(x.n_chunks * x.D * 4);
+    n += 3 * align_up(x.n_chunks * x.tD * 4) + align_up(x.n_chunks * x.tT * 4) + align_up(x.n_chunks * x.D * 4);
   return n;
 }
 
@@ -286,13 +286,13 @@ int fwd_impl(const gdn2_desc* d, const void* q, const void* k, const void* v, co
   size_t o2 = 0;
   auto take = [&](size_t bytes) { float* p = at<float>(workspace, o2); o2 += align_up(bytes); return p; };
   float* uT = take(x.n_chunks * x.tD * 4);
-  float* kgT = take(x.n_chunks * x.tD * 4);
   void* anc_buf = take(anchor_bytes(d));
-  // residuals for the backward -- training only; otherwise Wp / Qg / Aqk / gl live in the
-  // workspace and Kg, h_pre and v_new are not stored at all (the scan consumes h_pre and v_new
-  // itself).  Wp is kept in the orientation the forward scan contracts over keys; the reverse
-  // scan, which contracts it over tokens, transposes it in LDS (gdn2_scan.hip).
-  float *A = nullptr, *wp, *kg = nullptr, *qg, *aqk, *gl, *hpre = nullptr, *vnew = nullptr;
+  // residuals for the backward -- training only; otherwise Kg / Wp / Qg / Aqk / gl live in the
+  // workspace and h_pre and v_new are not stored at all (the scan consumes h_pre and v_new
+  // itself).  Wp is kept in the orientation the forward scan contracts over keys and Kg in the
+  // one the reverse scan does; each scan turns the other one's blocks around in LDS
+  // (gdn2_scan.hip).
+  float *A = nullptr, *wp, *kg, *qg, *aqk, *gl, *hpre = nullptr, *vnew = nullptr;
   if (residual) {
     size_t off[GDN2_RES_COUNT], tot;
     residual_offsets(d, off, &tot);
@@ -305,6 +305,7 @@ int fwd_impl(const gdn2_desc* d, const void* q, const void* k, const void* v, co
     qg = at<float>(residual, off[GDN2_RES_QG]);
     gl = at<float>(residual, off[GDN2_RES_GL]);
   } else {
+    kg = take(x.n_chunks * x.tD * 4);
     wp = take(x.n_chunks * x.tD * 4);
     qg = take(x.n_chunks * x.tD * 4);
     aqk = take(x.n_chunks * x.tT * 4);
@@ -316,7 +317,7 @@ int fwd_impl(const gdn2_desc* d, const void* q, const void* k, const void* v, co
   if (st) return st;
   gdn2::WyFwdArgs wa{};
   wa.q = q; wa.k = k; wa.v = v; wa.w = w; wa.b = b; wa.g = g; wa.anc = anc;
-  wa.wp_f = wp; wa.uT_f = uT; wa.kg_f = kg; wa.kgT_f = kgT; wa.qg_f = qg;
+  wa.wp_f = wp; wa.uT_f = uT; wa.kg_f = kg; wa.qg_f = qg;
   wa.aqk_f = aqk; wa.A = A; wa.gl = gl;
   wa.n_chunks = (int)x.n_chunks;
   wa.cfg = cfg;
@@ -330,7 +331,7 @@ int fwd_impl(const gdn2_desc* d, const void* q, const void* k, const void* v, co
   // chunk-parallel from them.
   const int ck = eff_ckpt(d);
   const bool fused_out = !residual || ck > 0;
-  gdn2::ScanFwdArgs sa{wp, kgT, uT, gl, h0, qg, aqk, h_final, fused_out ? o : nullptr, hpre, vnew,
+  gdn2::ScanFwdArgs sa{wp, kg, uT, gl, h0, qg, aqk, h_final, fused_out ? o : nullptr, hpre, vnew,
                        (int)x.nc, (int)x.n_bh, ck, cfg, reset};
   e = timed(1, s, [&] { return gdn2::launch_scan_fwd(d->D, sa, s); });
   if (e != hipSuccess) return hip_fail(e, "scan_fwd launch");

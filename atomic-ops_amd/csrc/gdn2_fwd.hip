@@ -25,7 +25,7 @@ namespace gdn2 {
 // three workgroups share a CU (768 chunks at config 2 = 3 per CU, all resident at once) and their
 // load / store bursts overlap each other's score, inverse and Wp / U phases.  The D channels
 // are taken in passes of DC = 32: each pass forms
-// gc for its channels, the gated fragments Kg / Qg / Kg^T and X = b k e^gc in registers, and
+// gc for its channels, the gated fragments Kg / Qg and X = b k e^gc in registers, and
 // stages gc, q, k and b k in LDS in fragment layout, from which every wave computes its score
 // tiles over the pass's k blocks (the accumulators carry across passes, so each tile's chain is
 // the one-pass chain: k blocks in ascending order).
@@ -366,8 +366,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void w
     if (a.g_is_gc) cs.store_as_is(sG);
     else cs.run(sG, reinterpret_cast<float4*>(sQ));
 
-    // 2. gated fragments (cd_slim.py:17-21): Kg = san(k e^{min(gl - gc, 0)}) as FRAG(Kg) and,
-    //    through the wave's transpose tile, FRAG(Kg^T); Qg = san(q e^{min(gc, 0)}); X = b k e^{min(gc, 0)}
+    // 2. gated fragments (cd_slim.py:17-21): Kg = san(k e^{min(gl - gc, 0)}) as FRAG(Kg) (the
+    //    forward scan turns its blocks around itself); Qg = san(q e^{min(gc, 0)}); X = b k e^{min(gc, 0)}
     //    (transposed, kept for Wp).  Staged for the scores: gc (already), q, k, b k.
     float4 kgv[NKBP], qgv[NKBP], bkv[NKBP];
 #pragma unroll
@@ -392,7 +392,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void w
       if (a.kg) stg4(a.kg + tb + row * D + d, kgv[kb]);
       if (a.qg_f) stg4(a.qg_f + tb + frag_blk(wv, kg, D) + 4 * l, qgv[kb]);
       if (a.qg) stg4(a.qg + tb + row * D + d, qgv[kb]);
-      if (a.kgT_f) stg4(a.kgT_f + tb + frag_blk(kg, wv, T) + 4 * l, wave_transpose16(tr, kgv[kb], r, g));
     }
     if (a.gl && tid < DC) a.gl[(size_t)chunk * D + DC * p + tid] = sG[frag_off(T - 1, tid, DC)];
     // kind-2 anchors of this pass's channels (first row | last row of the diagonal block)

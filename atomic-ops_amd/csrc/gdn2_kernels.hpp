@@ -94,7 +94,7 @@ __device__ __forceinline__ size_t io_off(const C& c, int chunk) {
 }
 
 // Per-chunk outputs of the WY build.  "_f" outputs are in fragment layout (gdn2_common.hpp):
-//   wp_f FA(Wp) (T x D), uT_f FA(U^T) (D x T), kg_f FA(Kg) (T x D), kgT_f FA(Kg^T) (D x T),
+//   wp_f FA(Wp) (T x D), uT_f FA(U^T) (D x T), kg_f FA(Kg) (T x D),
 //   qg_f FA(Qg) (T x D), aqk_f FA(Aqk) (T x T).  A (T x T) and gl (D) are row-major.  The plain
 //   row-major
 //   aqk / akk / wp / u / kg / qg are written only for the stage-level entry point.  Any
@@ -102,7 +102,7 @@ __device__ __forceinline__ size_t io_off(const C& c, int chunk) {
 struct WyFwdArgs {
   const void *q, *k, *v, *w, *b, *g;   // fp32, or bfloat16 bits for the bf16-input variant
   const float* anc;    // kind-2 pieces: the anchor buffer (AnchorArgs), else null
-  float *wp_f, *uT_f, *kg_f, *kgT_f, *qg_f, *aqk_f;
+  float *wp_f, *uT_f, *kg_f, *qg_f, *aqk_f;
   float *A, *gl;
   float *aqk, *akk, *wp, *u, *kg, *qg;
   int n_chunks;
@@ -139,7 +139,7 @@ struct CkptBlocks {
   }
 };
 
-// Forward state scan: reads FA(Wp), FA(Kg^T), FA(U^T), gl; writes the final state hf
+// Forward state scan: reads FA(Wp), FA(Kg), FA(U^T), gl; writes the final state hf
 // (row-major D x D) and, when h_pre_f / v_new_f are set, per chunk the entering state h_pre as
 // FA(h_pre^T) (D x D) and v_new as FA(v_new^T) (D x T).  With o set it also reads FA(Qg),
 // FA(Aqk) and writes o (row-major T x D per chunk); otherwise out_fwd computes o.
@@ -149,7 +149,7 @@ struct CkptBlocks {
 // the state entering that chunk is zero (a document boundary at the chunk's first token; at
 // chunk 0 it replaces h0).
 struct ScanFwdArgs {
-  const float *wp_f, *kgT_f, *uT_f, *gl, *h0, *qg_f, *aqk_f;
+  const float *wp_f, *kg_f, *uT_f, *gl, *h0, *qg_f, *aqk_f;
   float *hf, *o, *h_pre_f, *v_new_f;    // o, h_pre_f, v_new_f may be null
   int nc, n_bh, ckpt;
   Cfg cfg;

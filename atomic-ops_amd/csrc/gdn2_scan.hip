@@ -55,13 +55,14 @@ namespace gdn2 {
 // h_pre in LDS is block kb = key tile in the MFMA result layout of the owning wave, which is
 // the B operand of Wp h and the A operand of h^T Qg^T; v_new tiles are in the B-operand
 // layout of Kg^T v_new, which is the A operand of v_new^T Aqk^T.  FA(Wp), FA(Qg), FA(Aqk),
-// FA(Kg^T), FA(U^T) blocks are loaded as stored (one float4 per lane), one chunk ahead into
-// the second of two register sets, interleaved with the MFMAs.
+// FA(Kg), FA(U^T) blocks are loaded as stored (one float4 per lane), one chunk ahead into
+// the second of two register sets, interleaved with the MFMAs; the FA(Kg) blocks are turned
+// into FA(Kg^T) blocks by the chain wave itself, between the MFMAs of window A.
 template <int NH>
 struct ChainOps {
   float4 x[NH];            // FA(Wp) block (w, kb)
   float4 uu;               // FA(U^T) block (slice, w)
-  float4 kg[NH / 4][4];    // FA(Kg^T) blocks (kt(w, j), u)
+  float4 kg[NH / 4][4];    // FA(Kg) blocks (u, kt(w, j)), turned into FA(Kg^T) blocks (kt, u) in window A
   float4 gm[NH / 4];       // gamma of key tile kt(w, j)
 };
 template <int NH>
@@ -132,7 +133,7 @@ __device__ __forceinline__ unsigned cbar_at(int k) { return 4u * (unsigned)(k + 
 // and the state update keep h).
 template <int D, int MODE, bool OUT>
 __device__ __forceinline__ void scan_fwd_chain(const ScanFwdArgs& a, ScanFwdShared* sh, float4* sH, float4* sHd,
-                                               float4* sV) {
+                                               float4* sV, float* sTrK) {
   constexpr int NH = D / 16, NVB = D / 16, NJ = NH / 4;
   const float clip = a.cfg.clip;
   const int nc = a.nc;
@@ -183,7 +184,7 @@ __device__ __forceinline__ void scan_fwd_chain(const ScanFwdArgs& a, ScanFwdShar
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) op.kg[j][u] = ld4(a.kgT_f + tb + frag_blk(kt(j), u, T) + 4 * l);
+      for (int u = 0; u < 4; ++u) op.kg[j][u] = ld4(a.kg_f + tb + frag_blk(u, kt(j), D) + 4 * l);
       op.gm[j] = ld4(a.gl + base(c) * D + 16 * kt(j) + 4 * g);
     }
   };
@@ -220,6 +221,11 @@ __device__ __forceinline__ void scan_fwd_chain(const ScanFwdArgs& a, ScanFwdShar
 #pragma unroll
       for (int kb = 0; kb < NH; ++kb) hb[kb] = src[kb * WAVE + l];
     }
+    // window B's A operands, FA(Kg^T) blocks (kt(w, j), u): this chunk's FA(Kg) blocks (u, kt)
+    // turned around through the wave's transpose tile, one per MFMA group while the chain runs
+    // (the residual keeps Kg in the orientation the reverse scan contracts over keys)
+    float4 kgt[NJ][4];
+    static_assert(4 * NJ == NH, "one transpose per key block of the chain");
     f4 acc = {0.f, 0.f, 0.f, 0.f};
     if constexpr (MODE == DOT_HIGHEST) {
 #pragma unroll
@@ -227,6 +233,7 @@ __device__ __forceinline__ void scan_fwd_chain(const ScanFwdArgs& a, ScanFwdShar
         mma16<MODE>(acc, op.x[kb], hb[kb]);
         GDN2_SCHED_FENCE();
         nx.x[kb] = ld4(a.wp_f + tbn + frag_blk(w, kb, D) + 4 * l);
+        kgt[kb / 4][kb % 4] = wave_transpose16(sTrK, op.kg[kb / 4][kb % 4], r, g);
         GDN2_SCHED_FENCE();
       }
     } else {
@@ -236,6 +243,8 @@ __device__ __forceinline__ void scan_fwd_chain(const ScanFwdArgs& a, ScanFwdShar
         GDN2_SCHED_FENCE();
         nx.x[kb] = ld4(a.wp_f + tbn + frag_blk(w, kb, D) + 4 * l);
         nx.x[kb + 1] = ld4(a.wp_f + tbn + frag_blk(w, kb + 1, D) + 4 * l);
+        kgt[kb / 4][kb % 4] = wave_transpose16(sTrK, op.kg[kb / 4][kb % 4], r, g);
+        kgt[kb / 4][kb % 4 + 1] = wave_transpose16(sTrK, op.kg[kb / 4][kb % 4 + 1], r, g);
         GDN2_SCHED_FENCE();
       }
     }
@@ -261,22 +270,22 @@ __device__ __forceinline__ void scan_fwd_chain(const ScanFwdArgs& a, ScanFwdShar
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) mma16<MODE>(hn[j], op.kg[j][u], vv[u]);
+        for (int j = 0; j < NJ; ++j) mma16<MODE>(hn[j], kgt[j][u], vv[u]);
         GDN2_SCHED_FENCE();
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) nx.kg[j][u] = ld4(a.kgT_f + tbn + frag_blk(kt(j), u, T) + 4 * l);
+        for (int j = 0; j < NJ; ++j) nx.kg[j][u] = ld4(a.kg_f + tbn + frag_blk(u, kt(j), D) + 4 * l);
         GDN2_SCHED_FENCE();
       }
     } else {
 #pragma unroll
       for (int u = 0; u < 4; u += 2) {
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) mma32<MODE>(hn[j], op.kg[j][u], vv[u], op.kg[j][u + 1], vv[u + 1]);
+        for (int j = 0; j < NJ; ++j) mma32<MODE>(hn[j], kgt[j][u], vv[u], kgt[j][u + 1], vv[u + 1]);
         GDN2_SCHED_FENCE();
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-          nx.kg[j][u] = ld4(a.kgT_f + tbn + frag_blk(kt(j), u, T) + 4 * l);
-          nx.kg[j][u + 1] = ld4(a.kgT_f + tbn + frag_blk(kt(j), u + 1, T) + 4 * l);
+          nx.kg[j][u] = ld4(a.kg_f + tbn + frag_blk(u, kt(j), D) + 4 * l);
+          nx.kg[j][u + 1] = ld4(a.kg_f + tbn + frag_blk(u + 1, kt(j), D) + 4 * l);
         }
         GDN2_SCHED_FENCE();
       }
@@ -413,6 +422,7 @@ __global__ __launch_bounds__(8 * WAVE) void scan_fwd_kernel(ScanFwdArgs a) {
   __shared__ float4 sH[2 * NH * WAVE];     // h_pre by chunk parity, [buffer][key tile][lane]
   __shared__ float4 sHd[NH * WAVE];        // the damped state of the next part (Cfg::group)
   __shared__ float4 sV[2 * 4 * WAVE];      // v_new tiles by chunk parity, [buffer][token tile][lane]
+  __shared__ __attribute__((aligned(16))) float sTrK[4 * 16 * TRP];   // chain waves' transpose tiles
   __shared__ ScanFwdShared sh;
   if (threadIdx.x == 0) {
     sh.cbar = 0;
@@ -425,10 +435,10 @@ __global__ __launch_bounds__(8 * WAVE) void scan_fwd_kernel(ScanFwdArgs a) {
       case 5: scan_fwd_out<D, MODE, 1>(a, &sh, sH, sV); break;
       case 6: scan_fwd_out<D, MODE, 2>(a, &sh, sH, sV); break;
       case 7: scan_fwd_out<D, MODE, 3>(a, &sh, sH, sV); break;
-      default: scan_fwd_chain<D, MODE, OUT>(a, &sh, sH, sHd, sV); break;
+      default: scan_fwd_chain<D, MODE, OUT>(a, &sh, sH, sHd, sV, sTrK + wave_id() * 16 * TRP); break;
     }
   } else {
-    if (wave_id() < 4) scan_fwd_chain<D, MODE, OUT>(a, &sh, sH, sHd, sV);
+    if (wave_id() < 4) scan_fwd_chain<D, MODE, OUT>(a, &sh, sH, sHd, sV, sTrK + wave_id() * 16 * TRP);
   }
 }
 

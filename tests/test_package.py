@@ -83,9 +83,9 @@ def test_residual_layout_and_workspaces():
         assert nxt - o >= s
     L = _lib.lib()
     d = _desc()
-    # [U^T | Kg^T], without a residual also [Wp | Qg | Aqk | gl] (with one they are residuals;
+    # [U^T], without a residual also [Kg | Wp | Qg | Aqk | gl] (with one they are residuals;
     # h_pre / v_new never leave the scan)
-    assert L.gdn2_fwd_workspace_bytes(ctypes.byref(d), 1) == N * 2 * 64 * 128 * 4
+    assert L.gdn2_fwd_workspace_bytes(ctypes.byref(d), 1) == N * 64 * 128 * 4
     assert L.gdn2_fwd_workspace_bytes(ctypes.byref(d), 0) == N * (4 * 64 * 128 + 64 * 64 + 128) * 4
     assert L.gdn2_bwd_workspace_bytes(ctypes.byref(d)) >= N * (4 * 64 * 128 + 128 * 128 + 128) * 4
 
