@@ -543,37 +543,12 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
   const float* __restrict__ dwp = a.dwp + tb;
   const int next = chunk + gridDim.x;
 
-  // X1 = v_new, X2 = dO, sA = A, sG = gc.  Every load is issued before the cumsum waits for
-  // its g: one memory round trip for the whole prologue.
+  // X1 = v_new, X2 = dO, sA = A, sG = gc.  Non-persistent: every load is issued before the
+  // cumsum waits for its g, one memory round trip for the whole prologue.  Persistent: X1 and X2
+  // arrived by DMA during the previous chunk's B4 (the first chunk's are waited for here), and
+  // A and g, loaded above, are only stored after P1, which reads neither: their round trip runs
+  // under P1's MFMAs.
   if constexpr (PERSIST) {
-    // A from registers; gc of this wave's columns by an in-wave cumsum that adds in the order
-    // chunk_cumsum does (runs of four rows, then the totals of the runs above in order), so gc
-    // is bit-identical to every other kernel's.  Run s = 4 t + g is this lane's row tile t.
-#pragma unroll
-    for (int it = 0; it < NIA; ++it) {
-      const int f = tid + it * NT;
-      st4(sA + (f >> 4) * LT + 4 * (f & 15), xa[it]);
-    }
-    float xr[4][4], offt[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      xr[t][0] = xg[t].x;
-      xr[t][1] = xr[t][0] + xg[t].y;
-      xr[t][2] = xr[t][1] + xg[t].z;
-      xr[t][3] = xr[t][2] + xg[t].w;
-    }
-    float run = 0.f;
-#pragma unroll
-    for (int s2 = 0; s2 < 16; ++s2) {
-      const int t2 = s2 >> 2, g2 = s2 & 3;
-      offt[t2] = g == g2 ? run : offt[t2];
-      run = run + __shfl(xr[t2][3], r + 16 * g2);
-    }
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sG[(16 * t + 4 * g + e) * LD + dcol] = offt[t] + xr[t][e];
-    // the first chunk's DMA (later chunks' are waited for after B4)
     if (first) __builtin_amdgcn_s_waitcnt(WAIT_VMCNT0);
   } else {
     float4 xvn[NIT], xdo[NIT], xa[NIA];
@@ -658,6 +633,35 @@ __global__ __launch_bounds__(512) void bwd_wy_kernel(BwdWyArgs a) {
       const int i = 16 * ti + 4 * g + e, j = 16 * tj + r;
       sDAq[i * LT + j] = j <= i ? acc[e] : 0.f;
     }
+  }
+  if constexpr (PERSIST) {
+    // A from registers; gc of this wave's columns by an in-wave cumsum that adds in the order
+    // chunk_cumsum does (runs of four rows, then the totals of the runs above in order), so gc
+    // is bit-identical to every other kernel's.  Run s = 4 t + g is this lane's row tile t.
+#pragma unroll
+    for (int it = 0; it < NIA; ++it) {
+      const int f = tid + it * NT;
+      st4(sA + (f >> 4) * LT + 4 * (f & 15), xa[it]);
+    }
+    float xr[4][4], offt[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      xr[t][0] = xg[t].x;
+      xr[t][1] = xr[t][0] + xg[t].y;
+      xr[t][2] = xr[t][1] + xg[t].z;
+      xr[t][3] = xr[t][2] + xg[t].w;
+    }
+    float run = 0.f;
+#pragma unroll
+    for (int s2 = 0; s2 < 16; ++s2) {
+      const int t2 = s2 >> 2, g2 = s2 & 3;
+      offt[t2] = g == g2 ? run : offt[t2];
+      run = run + __shfl(xr[t2][3], r + 16 * g2);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sG[(16 * t + 4 * g + e) * LD + dcol] = offt[t] + xr[t][e];
   }
   __syncthreads();
 
