@@ -80,11 +80,12 @@ def lib():
         L.gdn2_scores.argtypes = [P(Gdn2Desc)] + [_vp] * 7
         L.gdn2_debug_gemm.argtypes = [_c_int, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp]
         L.gdn2_debug_stream.argtypes = [_c_int, _vp, _vp, _c_size, _vp]
+        L.gdn2_debug_mfma.argtypes = [_c_int, _c_int, _vp, _vp]
         L.gdn2_prof_begin.argtypes = [_c_int]
         L.gdn2_prof_end.argtypes = [P(_c_dbl), P(_c_int)]
         for fn in ("gdn2_residual_layout", "gdn2_fwd", "gdn2_fwd_bf16", "gdn2_fwd_noalloc", "gdn2_fwd_reset",
                    "gdn2_decode", "gdn2_bwd", "gdn2_wy_stage", "gdn2_scores", "gdn2_debug_gemm", "gdn2_debug_stream",
-                   "gdn2_prof_begin", "gdn2_prof_end"):
+                   "gdn2_debug_mfma", "gdn2_prof_begin", "gdn2_prof_end"):
             getattr(L, fn).restype = _c_int
         if L.gdn2_abi_version() != ABI_VERSION:
             raise Gdn2Error("libgdn2_hip.so ABI version mismatch")

@@ -573,6 +573,15 @@ int gdn2_debug_stream(int mode, const void* src, void* dst, size_t bytes, void* 
   return GDN2_OK;
 }
 
+int gdn2_debug_mfma(int blocks, int iters, float* out, void* stream) {
+  if (blocks < 1 || blocks > (1 << 20) || iters < 1 || iters > (1 << 20))
+    return fail(GDN2_ERR_INVALID, "mfma probe blocks and iters must be in [1, 2^20]");
+  if (!out) return fail(GDN2_ERR_INVALID, "null buffer pointer");
+  hipError_t e = gdn2::launch_mfma_probe(blocks, iters, out, reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "mfma probe launch");
+  return GDN2_OK;
+}
+
 int gdn2_prof_begin(int max_launches) {
   if (max_launches <= 0) return fail(GDN2_ERR_INVALID, "max_launches must be positive");
   while ((int)g_prof.pool.size() < max_launches) {

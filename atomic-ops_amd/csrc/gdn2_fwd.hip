@@ -712,6 +712,29 @@ hipError_t launch_stream_probe(int mode, const void* src, void* dst, size_t n4, 
   return hipGetLastError();
 }
 
+// diagnostics: the fp32 MFMA rate the kernels' FLOP counts are measured against.  Every wave
+// issues iters rounds of eight independent v_mfma_f32_16x16x4_f32 (2048 FLOP each) on A = B = x
+// and writes the sum of its accumulators (8 * 4 * 4 x^2 iters per lane), which keeps them live.
+__global__ __launch_bounds__(256) void mfma_probe_kernel(float* __restrict__ out, int iters, float x) {
+  typedef float v4 __attribute__((ext_vector_type(4)));
+  v4 acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = v4{0.f, 0.f, 0.f, 0.f};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, x, acc[i], 0, 0, 0);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s += (acc[i][0] + acc[i][1]) + (acc[i][2] + acc[i][3]);
+  out[(size_t)blockIdx.x * 256 + threadIdx.x] = s;
+}
+
+hipError_t launch_mfma_probe(int blocks, int iters, float* out, hipStream_t s) {
+  hipLaunchKernelGGL(mfma_probe_kernel, dim3(blocks), dim3(256), 0, s, out, iters, 1.0f);
+  return hipGetLastError();
+}
+
 // ------------------------------------------------------------------------------------
 // Anchors of the diagonal blocks wider than a part (AnchorArgs): one workgroup per block of B
 // parts; each part's gc by chunk_cumsum (the arithmetic of every other kernel), its last row gl

@@ -412,6 +412,40 @@ def hbm_stream_rates(n_bytes=1 << 30, reps=10):
     return out
 
 
+def mfma_sustained_rates(iters=20480):
+    """The box's sustained fp32 MFMA rate (TFLOP/s) with one and with two waves per SIMD: the
+    library's probe (gdn2_debug_mfma: independent v_mfma_f32_16x16x4_f32, eight per round) on
+    one (two) four-wave workgroups per CU, timed with HIP events on its stream; the median of 3
+    launches after one untimed one.  A context figure for the kernels' MFMA rates: the roofline
+    keeps the published peak."""
+    import torch
+    from atomic_gdn2 import _lib
+    n_cu = torch.cuda.get_device_properties(0).multi_processor_count
+    L_ = _lib.lib()
+    stream = _lib.stream_handle()
+    out = {}
+    for wps in (1, 2):
+        blocks = n_cu * wps
+        buf = torch.empty(blocks * 256, device="cuda")
+
+        def run():
+            _lib.check(L_.gdn2_debug_mfma(blocks, iters, _lib.ptr(buf), stream), "gdn2_debug_mfma")
+        run()
+        per = []
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()                              # torch's current stream = the launch stream
+            run()
+            e1.record()
+            e1.synchronize()
+            per.append(e0.elapsed_time(e1))
+        ms = sorted(per)[1]
+        flop = blocks * 4 * iters * 8 * 2048
+        out[f"waves_per_simd_{wps}"] = round(flop / (ms * 1e-3) / 1e12, 1)
+    out["published_peak"] = PEAK_FP32_MFMA
+    return out
+
+
 def bench_e2e_lm(seed, reps=4, rounds=3, warm=2):
     """Config 5: one training step of the reference's benchmark LM (8 GDN-2
     blocks, 34,873,952 parameters, B8 L2048, vocab 256, CE + clip_by_global_norm(1.0) + AdamW)
@@ -459,6 +493,8 @@ def main():
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end LM training step")
     ap.add_argument("--hbm-rates", action="store_true",
                     help="only print the HBM copy / read / fill rates of the streaming probe and exit")
+    ap.add_argument("--mfma-rate", action="store_true",
+                    help="only print the sustained fp32 MFMA rates (gdn2_debug_mfma) and exit")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run 5 plain device copies of a 256 MiB fp32 buffer (reference for the "
                          "FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -504,6 +540,9 @@ def main():
         return
     if args.hbm_rates:
         print(json.dumps({"hbm_stream_tb_s": hbm_stream_rates()}), flush=True)
+        return
+    if args.mfma_rate:
+        print(json.dumps({"mfma_fp32_sustained_tflops": mfma_sustained_rates()}), flush=True)
         return
     if args.profile_only:
         if args.seq_len == L_:
@@ -598,6 +637,7 @@ def main():
     # each kernel's achieved HBM rate against what a plain copy reaches on this box
     rates = hbm_stream_rates()
     out["hbm_stream_tb_s"] = rates
+    out["mfma_fp32_sustained_tflops"] = mfma_sustained_rates()
     for kd in kern.values():
         if "hbm_gb_per_s" in kd:
             kd["hbm_frac_of_copy"] = round(kd["hbm_gb_per_s"] / 1e3 / rates["copy"], 3)

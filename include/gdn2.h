@@ -213,6 +213,13 @@ int gdn2_debug_gemm(int mode, const float* A, const float* B, float* C, int M, i
  * multiple of 4096, both buffers 16-byte aligned. */
 int gdn2_debug_stream(int mode, const void* src, void* dst, size_t bytes, void* stream);
 
+/* Diagnostics (no counterpart in the reference): the sustained fp32 MFMA rate that the kernels'
+ * FLOP counts are judged against.  `blocks` workgroups of four waves; every wave issues `iters`
+ * rounds of eight independent v_mfma_f32_16x16x4_f32 (2048 FLOP each), i.e. the launch does
+ * blocks * 4 * iters * 8 * 2048 FLOP.  out holds blocks * 256 floats; each is 128 * iters (the
+ * lane's accumulator sum for all-ones operands).  1 <= blocks, iters <= 1 << 20. */
+int gdn2_debug_mfma(int blocks, int iters, float* out, void* stream);
+
 /* Per-kernel timing with HIP events recorded on the launch stream around every kernel.
  * gdn2_prof_begin(n) starts recording for up to n launches (process-wide, not re-entrant);
  * gdn2_prof_end synchronises on the recorded events and returns, per kernel id, the summed

@@ -130,6 +130,19 @@ def test_mfma_tile_layout(mode, shape):
     assert rel_l2(C, ref) < 1e-6
 
 
+def test_mfma_probe_does_the_products_it_counts():
+    """The MFMA rate probe's lanes each end with the closed-form sum of their accumulators
+    (eight accumulators of four elements, each 4 * iters for all-ones operands: 128 * iters),
+    so the FLOPs the bench divides by were all issued; the guard past the end is untouched."""
+    from atomic_gdn2 import _lib
+    blocks, iters = 8, 64
+    banner(f"mfma probe {blocks} x {iters}")
+    out = torch.full((blocks * 256 + 256,), -7.0, device="cuda")
+    _lib.check(_lib.lib().gdn2_debug_mfma(blocks, iters, _lib.ptr(out), _lib.stream_handle()), "mfma probe")
+    torch.cuda.synchronize()
+    assert bool((out[: blocks * 256] == 128.0 * iters).all()) and bool((out[blocks * 256:] == -7.0).all())
+
+
 def test_stream_probe_copy_and_fill():
     """The HBM rate probe moves exactly the bytes it is given (copy) and writes its pattern
     (fill); the read mode leaves its sentinel target alone."""

@@ -170,6 +170,18 @@ def test_stream_probe_arguments_rejected_without_gpu_work(mode, nbytes, src, dst
     assert st == 1 and msg in _lib.lib().gdn2_last_error()
 
 
+@pytest.mark.parametrize("blocks,iters,out,msg", [
+    (0, 16, 16, b"blocks and iters"),
+    ((1 << 20) + 1, 16, 16, b"blocks and iters"),
+    (1, 0, 16, b"blocks and iters"),
+    (1, 16, None, b"null"),
+])
+def test_mfma_probe_arguments_rejected_without_gpu_work(blocks, iters, out, msg):
+    from atomic_gdn2 import _lib
+    st = _lib.lib().gdn2_debug_mfma(blocks, iters, out, None)
+    assert st == 1 and msg in _lib.lib().gdn2_last_error()
+
+
 def test_python_boundary_errors():
     from atomic_gdn2 import make_cfg, make_blr_trainable
     cfg = make_cfg(bt=64, bc=32, score_bs=64, bs2=32)
