@@ -255,7 +255,7 @@ __device__ __forceinline__ void wy_inverse(const Cfg& cf, const float* sK, float
     const int i = f / (T / 4), j = 4 * (f % (T / 4));
     const float4 x = san4(ld4(sI + i * LT + j), cf.clip);
     st4(sI + i * LT + j, x);
-    if (A_out) stg4(A_out + i * T + j, x);
+    if (A_out) stg4_keep(A_out + i * T + j, x);
   }
   __syncthreads();
 }
@@ -388,10 +388,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void w
 #pragma unroll
     for (int kb = 0; kb < NKBP; ++kb) {
       const int kg = NKBP * p + kb, d = DC * p + 16 * kb + 4 * g;
-      if (a.kg_f) stg4(a.kg_f + tb + frag_blk(wv, kg, D) + 4 * l, kgv[kb]);
-      if (a.kg) stg4(a.kg + tb + row * D + d, kgv[kb]);
-      if (a.qg_f) stg4(a.qg_f + tb + frag_blk(wv, kg, D) + 4 * l, qgv[kb]);
-      if (a.qg) stg4(a.qg + tb + row * D + d, qgv[kb]);
+      if (a.kg_f) stg4_keep(a.kg_f + tb + frag_blk(wv, kg, D) + 4 * l, kgv[kb]);
+      if (a.kg) stg4_keep(a.kg + tb + row * D + d, kgv[kb]);
+      if (a.qg_f) stg4_keep(a.qg_f + tb + frag_blk(wv, kg, D) + 4 * l, qgv[kb]);
+      if (a.qg) stg4_keep(a.qg + tb + row * D + d, qgv[kb]);
     }
     if (a.gl && tid < DC) a.gl[(size_t)chunk * D + DC * p + tid] = sG[frag_off(T - 1, tid, DC)];
     // kind-2 anchors of this pass's channels (first row | last row of the diagonal block)
@@ -460,9 +460,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void w
       if (PM == PM_ELEM && ti == tj && r < 8 && g >= 2) {
         const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
         st4(sK + i * LT + j0, z);
-        if (a.aqk_f) stg4(a.aqk_f + sb + frag_blk(ti, tj, T) + 4 * l, z);
-        if (a.aqk) stg4(a.aqk + sb + i * T + j0, z);
-        if (a.akk) stg4(a.akk + sb + i * T + j0, z);
+        if (a.aqk_f) stg4_keep(a.aqk_f + sb + frag_blk(ti, tj, T) + 4 * l, z);
+        if (a.aqk) stg4_keep(a.aqk + sb + i * T + j0, z);
+        if (a.akk) stg4_keep(a.akk + sb + i * T + j0, z);
       }
       continue;
     }
@@ -474,18 +474,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void w
     }
     const float4 aq4 = make_float4(aq[0], aq[1], aq[2], aq[3]), ak4 = make_float4(ak[0], ak[1], ak[2], ak[3]);
     st4(sK + i * LT + j0, scale4(ak4, ome));
-    if (a.aqk_f) stg4(a.aqk_f + sb + frag_blk(ti, tj, T) + 4 * l, aq4);
-    if (a.aqk) stg4(a.aqk + sb + i * T + j0, aq4);
-    if (a.akk) stg4(a.akk + sb + i * T + j0, ak4);
+    if (a.aqk_f) stg4_keep(a.aqk_f + sb + frag_blk(ti, tj, T) + 4 * l, aq4);
+    if (a.aqk) stg4_keep(a.aqk + sb + i * T + j0, aq4);
+    if (a.akk) stg4_keep(a.akk + sb + i * T + j0, ak4);
   }
   // upper tiles (tj > ti): zeros
   for (int t = wv; t < 16; t += 4) {
     const int ti = t / 4, tj = t % 4;
     if (tj <= ti) continue;
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (a.aqk_f) stg4(a.aqk_f + sb + frag_blk(ti, tj, T) + 4 * l, z);
-    if (a.aqk) stg4(a.aqk + sb + (16 * ti + r) * T + 16 * tj + 4 * g, z);
-    if (a.akk) stg4(a.akk + sb + (16 * ti + r) * T + 16 * tj + 4 * g, z);
+    if (a.aqk_f) stg4_keep(a.aqk_f + sb + frag_blk(ti, tj, T) + 4 * l, z);
+    if (a.aqk) stg4_keep(a.aqk + sb + (16 * ti + r) * T + 16 * tj + 4 * g, z);
+    if (a.akk) stg4_keep(a.akk + sb + (16 * ti + r) * T + 16 * tj + 4 * g, z);
   }
   if constexpr (ELEM) {
 #pragma unroll
@@ -519,11 +519,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void w
     const float4 pv = san4(f4_to_float4(acc), clip);
     if constexpr (decltype(matc)::value == 0) {
       // pv = Wp[16 ti + r][16 tj + 4 g .. + 3]
-      if (a.wp_f) stg4(a.wp_f + tb + frag_blk(ti, tj, D) + 4 * l, pv);
-      if (a.wp) stg4(a.wp + tb + (size_t)(16 * ti + r) * D + 16 * tj + 4 * g, pv);
+      if (a.wp_f) stg4_keep(a.wp_f + tb + frag_blk(ti, tj, D) + 4 * l, pv);
+      if (a.wp) stg4_keep(a.wp + tb + (size_t)(16 * ti + r) * D + 16 * tj + 4 * g, pv);
     } else {
       // pv.e = U[16 ti + 4 g + e][16 tj + r]
-      if (a.uT_f) stg4(a.uT_f + tb + frag_blk(tj, ti, T) + 4 * l, pv);
+      if (a.uT_f) stg4_keep(a.uT_f + tb + frag_blk(tj, ti, T) + 4 * l, pv);
       if (a.u) {
         float* o = a.u + tb + (size_t)(16 * ti + 4 * g) * D + 16 * tj + r;
         o[0] = pv.x; o[D] = pv.y; o[2 * D] = pv.z; o[3 * D] = pv.w;
