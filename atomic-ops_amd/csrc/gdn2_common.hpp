@@ -394,10 +394,11 @@ __device__ __forceinline__ void stg4(float* p, const float4& x) {
   __builtin_nontemporal_store(v, reinterpret_cast<f4*>(p));
 }
 // Plain (cache-allocating) global store, for the WY build's outputs (the scan operands and the
-// residual).  Measured against the streaming store at config 2: the WY build 62.8 -> 59.5 us,
-// and the reverse scan and bwd_pre, which read that residual in the backward, 1-3 us faster
-// each (the lines appear to stay in MI355X's 256 MB memory-side cache); the same switch for the
-// backward's intermediates gained nothing, and for its gradients it cost bwd_wy 2-4 us.
+// residual) and the operator's output o.  Measured against the streaming store at config 2: the
+// WY build 62.8 -> 59.5 us, and the reverse scan and bwd_pre, which read that residual in the
+// backward, 1-3 us faster each (the lines appear to stay in MI355X's 256 MB memory-side cache);
+// o, which the caller's loss reads next, -2.5 us per gradient evaluation.  The same switch for
+// the backward's intermediates gained nothing, and for its gradients it cost bwd_wy 2-4 us.
 __device__ __forceinline__ void stg4_keep(float* p, const float4& x) {
   const f4 v = {x.x, x.y, x.z, x.w};
   *reinterpret_cast<f4*>(p) = v;

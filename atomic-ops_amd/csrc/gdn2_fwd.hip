@@ -648,7 +648,7 @@ __global__ __launch_bounds__(256) void out_fwd_kernel(OutFwdArgs a) {
       drain(acc1, acc2);
       const float4 ov = make_float4(sanitize(scale * acc1[0] + acc2[0], clip), sanitize(scale * acc1[1] + acc2[1], clip),
                                     sanitize(scale * acc1[2] + acc2[2], clip), sanitize(scale * acc1[3] + acc2[3], clip));
-      stg4(a.o + io_off<D>(a.cfg, chunk) + (size_t)(16 * tq + r) * D + 16 * cb + 4 * g, ov);
+      stg4_keep(a.o + io_off<D>(a.cfg, chunk) + (size_t)(16 * tq + r) * D + 16 * cb + 4 * g, ov);
     }
   }
 }

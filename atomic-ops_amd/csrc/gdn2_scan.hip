@@ -402,7 +402,7 @@ __device__ __forceinline__ void scan_fwd_out(const ScanFwdArgs& a, ScanFwdShared
     }
     drain(acc, acc2);
     // lane (r, g): o[16 J + r][c0 + 4 g .. + 3]
-    stg4(a.o + ((size_t)bh * a.cfg.seq_ld + (size_t)c * T) * D + (size_t)(16 * J + r) * D + c0 + 4 * g,
+    stg4_keep(a.o + ((size_t)bh * a.cfg.seq_ld + (size_t)c * T) * D + (size_t)(16 * J + r) * D + c0 + 4 * g,
          make_float4(sanitize(scale * acc[0] + acc2[0], clip), sanitize(scale * acc[1] + acc2[1], clip),
                      sanitize(scale * acc[2] + acc2[2], clip), sanitize(scale * acc[3] + acc2[3], clip)));
   };
