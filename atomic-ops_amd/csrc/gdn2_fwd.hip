@@ -713,17 +713,21 @@ hipError_t launch_stream_probe(int mode, const void* src, void* dst, size_t n4, 
 }
 
 // diagnostics: the fp32 MFMA rate the kernels' FLOP counts are measured against.  Every wave
-// issues iters rounds of eight independent v_mfma_f32_16x16x4_f32 (2048 FLOP each) on A = B = x
-// and writes the sum of its accumulators (8 * 4 * 4 x^2 iters per lane), which keeps them live.
+// issues iters rounds of eight independent mma16 (the kernels' primitive: four dependent
+// v_mfma_f32_16x16x4_f32, 8192 FLOP) on all-x operands, drains them as the kernels do and
+// writes the sum of its accumulators (8 * 4 * 16 x^2 iters per lane), which keeps them live.
 __global__ __launch_bounds__(256) void mfma_probe_kernel(float* __restrict__ out, int iters, float x) {
-  typedef float v4 __attribute__((ext_vector_type(4)));
-  v4 acc[8];
+  f4 acc[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = v4{0.f, 0.f, 0.f, 0.f};
-  for (int it = 0; it < iters; ++it) {
+  for (int i = 0; i < 8; ++i) acc[i] = f4{0.f, 0.f, 0.f, 0.f};
+  const float4 v = make_float4(x, x, x, x);
+  int it = 0;
+  do {                                   // iters >= 1 (gdn2_debug_mfma): no zero-trip path
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, x, acc[i], 0, 0, 0);
-  }
+    for (int i = 0; i < 8; ++i) mma16<DOT_HIGHEST>(acc[i], v, v);
+  } while (++it < iters);
+  drain(acc[0], acc[1], acc[2], acc[3]);
+  drain(acc[4], acc[5], acc[6], acc[7]);
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) s += (acc[i][0] + acc[i][1]) + (acc[i][2] + acc[i][3]);

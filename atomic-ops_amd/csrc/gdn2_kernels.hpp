@@ -279,7 +279,8 @@ hipError_t launch_gemm_probe(int mode, const float* A, const float* B, float* C,
 // 2 fill dst.
 hipError_t launch_stream_probe(int mode, const void* src, void* dst, size_t n4, hipStream_t s);
 // Diagnostics: blocks workgroups of four waves, each wave iters rounds of eight independent
-// v_mfma_f32_16x16x4_f32; out[blocks * 256] gets each lane's accumulator sum (128 iters).
+// mma16 (4 v_mfma_f32_16x16x4_f32 each); out[blocks * 256] gets each lane's accumulator sum
+// (512 iters).
 hipError_t launch_mfma_probe(int blocks, int iters, float* out, hipStream_t s);
 
 // Linear work index of this workgroup such that consecutive indices (workgroups of one

@@ -412,9 +412,9 @@ def hbm_stream_rates(n_bytes=1 << 30, reps=10):
     return out
 
 
-def mfma_sustained_rates(iters=20480):
+def mfma_sustained_rates(iters=5120):
     """The box's sustained fp32 MFMA rate (TFLOP/s) with one and with two waves per SIMD: the
-    library's probe (gdn2_debug_mfma: independent v_mfma_f32_16x16x4_f32, eight per round) on
+    library's probe (gdn2_debug_mfma: eight independent 16-deep mma16 products per round) on
     one (two) four-wave workgroups per CU, timed with HIP events on its stream; the median of 3
     launches after one untimed one.  A context figure for the kernels' MFMA rates: the roofline
     keeps the published peak."""
@@ -440,7 +440,7 @@ def mfma_sustained_rates(iters=20480):
             e1.synchronize()
             per.append(e0.elapsed_time(e1))
         ms = sorted(per)[1]
-        flop = blocks * 4 * iters * 8 * 2048
+        flop = blocks * 4 * iters * 8 * 8192
         out[f"waves_per_simd_{wps}"] = round(flop / (ms * 1e-3) / 1e12, 1)
     out["published_peak"] = PEAK_FP32_MFMA
     return out

@@ -215,9 +215,10 @@ int gdn2_debug_stream(int mode, const void* src, void* dst, size_t bytes, void* 
 
 /* Diagnostics (no counterpart in the reference): the sustained fp32 MFMA rate that the kernels'
  * FLOP counts are judged against.  `blocks` workgroups of four waves; every wave issues `iters`
- * rounds of eight independent v_mfma_f32_16x16x4_f32 (2048 FLOP each), i.e. the launch does
- * blocks * 4 * iters * 8 * 2048 FLOP.  out holds blocks * 256 floats; each is 128 * iters (the
- * lane's accumulator sum for all-ones operands).  1 <= blocks, iters <= 1 << 20. */
+ * rounds of eight independent 16-deep products, each four dependent v_mfma_f32_16x16x4_f32
+ * (8192 FLOP) as the kernels issue them, i.e. the launch does blocks * 4 * iters * 8 * 8192 FLOP.
+ * out holds blocks * 256 floats; each is 512 * iters (the lane's accumulator sum for all-ones
+ * operands).  1 <= blocks, iters <= 1 << 20. */
 int gdn2_debug_mfma(int blocks, int iters, float* out, void* stream);
 
 /* Per-kernel timing with HIP events recorded on the launch stream around every kernel.

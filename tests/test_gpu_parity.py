@@ -132,7 +132,7 @@ def test_mfma_tile_layout(mode, shape):
 
 def test_mfma_probe_does_the_products_it_counts():
     """The MFMA rate probe's lanes each end with the closed-form sum of their accumulators
-    (eight accumulators of four elements, each 4 * iters for all-ones operands: 128 * iters),
+    (eight accumulators of four elements, each 16 * iters for all-ones operands: 512 * iters),
     so the FLOPs the bench divides by were all issued; the guard past the end is untouched."""
     from atomic_gdn2 import _lib
     blocks, iters = 8, 64
@@ -140,7 +140,7 @@ def test_mfma_probe_does_the_products_it_counts():
     out = torch.full((blocks * 256 + 256,), -7.0, device="cuda")
     _lib.check(_lib.lib().gdn2_debug_mfma(blocks, iters, _lib.ptr(out), _lib.stream_handle()), "mfma probe")
     torch.cuda.synchronize()
-    assert bool((out[: blocks * 256] == 128.0 * iters).all()) and bool((out[blocks * 256:] == -7.0).all())
+    assert bool((out[: blocks * 256] == 512.0 * iters).all()) and bool((out[blocks * 256:] == -7.0).all())
 
 
 def test_stream_probe_copy_and_fill():
