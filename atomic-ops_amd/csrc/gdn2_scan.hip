@@ -138,7 +138,10 @@ __device__ __forceinline__ void scan_fwd_chain(const ScanFwdArgs& a, ScanFwdShar
   const float clip = a.cfg.clip;
   const int nc = a.nc;
   const int lin = xcd_remap(gridDim.x);
-  const int vb = lin % NVB, bh = lin / NVB, c0 = 16 * vb;
+  // (batch, head)s in reverse order: the WY build writes them in ascending order, so the first
+  // workgroups read the lines written last, the likeliest to be still cached (when the grid
+  // takes several rounds, config 4: about -1 % of the scan; config 2: -0.9 us)
+  const int vb = lin % NVB, bh = a.n_bh - 1 - lin / NVB, c0 = 16 * vb;
   const int l = lane_id(), r = l & 15, g = l >> 4, w = wave_id();
   auto kt = [&](int j) { return w + 4 * j; };
   auto base = [&](int c) { return (size_t)bh * nc + (c < nc ? c : nc - 1); };   // clamped chunk
@@ -340,7 +343,7 @@ __device__ __forceinline__ void scan_fwd_out(const ScanFwdArgs& a, ScanFwdShared
   const float clip = a.cfg.clip, scale = a.cfg.scale;
   const int nc = a.nc;
   const int lin = xcd_remap(gridDim.x);
-  const int vb = lin % NVB, bh = lin / NVB, c0 = 16 * vb;
+  const int vb = lin % NVB, bh = a.n_bh - 1 - lin / NVB, c0 = 16 * vb;   // as the chain waves
   const int l = lane_id(), r = l & 15, g = l >> 4;
   auto base = [&](int c) { return (size_t)bh * nc + (c < nc ? c : nc - 1); };
   bool ok = true;
